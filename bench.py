@@ -1,0 +1,236 @@
+#!/usr/bin/env python3
+"""Benchmark of the block-verify FFN on one MI355X.
+
+Workload (one "step"): the 27B-shape FFN of a draft block of B activation rows,
+  launch 1  gate/up 17408x5120 Q4_0 CWENR-RSI pair, SwiGLU fused  -> h [B][17408]
+  launch 2  down    5120x17408 Q4_0 CWENR-RS                       -> y [B][5120]
+with seeded synthetic weights (f16 scales |N(0,0.02)|/8, nibbles uniform) and
+f32 N(0,1) activations.  The headline is B=8; B=1 and B=16 are reported beside
+it.  Four independent weight copies (600 MB, more than the 256 MB MALL) are
+rotated step by step so every step streams its weights from HBM.
+
+Prints ONE JSON line (driver contract).  `--gpus N` with N > 1 exits: this
+build runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "verified tok/s + HBM GB/s (% of peak), Q4_0 27B-shape verify B=1/8/16"
+H, I = 5120, 17408
+PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
+NCOPIES = 4
+
+
+def ffn_bytes(B: int) -> tuple[int, int]:
+    """Algorithmic HBM bytes of the two launches: weights once + activations in
+    + outputs written once (18 bytes per 32-weight Q4_0 block)."""
+    w_gu = I * (H // 32) * 36          # both sides of the RSI pair
+    w_d = H * (I // 32) * 18
+    l1 = w_gu + B * H * 4 + B * I * 4
+    l2 = w_d + B * I * 4 + B * H * 4
+    return l1, l2
+
+
+def make_weights(seed: int, copy: int):
+    from cwen_amd import synth
+    gq, gs = synth.q4_rsi(seed, I, H, key=2 * copy)
+    dq, ds = synth.q4_rs(seed, H, I, key=2 * copy + 1)
+    return gq, gs, dq, ds
+
+
+def gpu_leg(steps: int, warmup: int, Bs: list[int]) -> dict:
+    import torch
+    from cwen_amd import gpu, synth
+    ctx = gpu.Context(0)
+    Wgu, Wd = [], []
+    for c in range(NCOPIES):
+        gq, gs, dq, ds = make_weights(0, c)
+        Wgu.append(gpu.Weight(ctx, gpu.T_Q4_0RSI, gq, gs, H, I))
+        Wd.append(gpu.Weight(ctx, gpu.T_Q4_0RS, dq, ds, I, H))
+        del gq, gs, dq, ds
+    stream = torch.cuda.current_stream()
+    out = {}
+    for B in Bs:
+        X = torch.from_numpy(synth.activations(0, B, H)).cuda()
+        Hb = torch.empty(B, I, device="cuda")
+        Y = torch.empty(B, H, device="cuda")
+
+        def step(i: int, ev=None):
+            c = i % NCOPIES
+            if ev is not None:
+                ev[0].record(stream)
+            gpu.gemvb_swiglu(ctx, Wgu[c], X, Hb, B, stream=stream)
+            if ev is not None:
+                ev[1].record(stream)
+            gpu.gemvb(ctx, Wd[c], Hb, Y, B, stream=stream)
+            if ev is not None:
+                ev[2].record(stream)
+
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        # whole-step timing
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for i in range(steps):
+            step(i)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms_step = t0.elapsed_time(t1) / steps
+        # per-launch timing (events bracket each launch on the launch stream)
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        for i in range(steps):
+            step(i, evs[i])
+        torch.cuda.synchronize()
+        l1_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+        l2_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+        b1, b2 = ffn_bytes(B)
+        out[B] = {
+            "ms_per_step": ms_step,
+            "gbs": (b1 + b2) / (ms_step * 1e-3) / 1e9,
+            "tok_s": B / (ms_step * 1e-3),
+            "swiglu_ms": l1_ms, "down_ms": l2_ms,
+            "swiglu_gbs": b1 / (l1_ms * 1e-3) / 1e9,
+            "down_gbs": b2 / (l2_ms * 1e-3) / 1e9,
+            "bytes_per_step": b1 + b2,
+        }
+    ctx_keep = (Wgu, Wd)  # noqa: F841  keep weights alive until here
+    return out
+
+
+def cpu_child(B: int, reps: int) -> None:
+    """CPU baseline leg: the reference engine's own mlp_blk kernels (gemvb x3 +
+    silu_mul, run.c:2677-2681), compiled from its run.c (oracle/_ref); the
+    oracle's scalar port when that build is absent."""
+    from cwen_amd import synth
+    X = synth.activations(0, B, H)
+    copies = [make_weights(0, c) for c in range(2)]
+    try:
+        from oracle.binding import Reference
+        R = Reference()
+        kind, cores = "reference", R.L.ref_omp_threads()
+
+        def ffn(c):
+            gq, gs, dq, ds = copies[c]
+            a = R.gemvb(102, gq, gs, H, I, X, side=0)
+            b = R.gemvb(102, gq, gs, H, I, X, side=1)
+            h = R.silu_mul(a, b)
+            return R.gemvb(101, dq, ds, I, H, h)
+        label = f"run.c gemvb/silu_mul ({R.isa})"
+    except RuntimeError:
+        from oracle.binding import Oracle
+        O = Oracle()
+        kind, cores = "port", 1
+
+        def ffn(c):
+            gq, gs, dq, ds = copies[c]
+            h = O.silu_mul(O.gemvb(102, gq, gs, H, I, X, 0), O.gemvb(102, gq, gs, H, I, X, 1))
+            return O.gemvb(101, dq, ds, I, H, h)
+        label = "oracle scalar port"
+    for i in range(2):
+        ffn(i % 2)
+    ts = []
+    budget = time.perf_counter() + 10.0   # bounded sample: ~10 s of CPU work
+    for i in range(reps):
+        t = time.perf_counter()
+        ffn(i % 2)
+        ts.append(time.perf_counter() - t)
+        if time.perf_counter() > budget:
+            break
+    med, mn = float(np.median(ts)), float(np.min(ts))
+    b1, b2 = ffn_bytes(B)
+    print(json.dumps({"value": (b1 + b2) / med / 1e9, "unit": "GB/s", "cores": cores, "kind": kind,
+                      "ms_median": med * 1e3, "ms_min": mn * 1e3, "tok_s": B / med,
+                      "sample": f"{len(ts)} FFN steps at B={B} after 2 warmups, 2 weight copies "
+                                f"rotated; {label}; median"}))
+
+
+def cpu_leg(B: int) -> dict | None:
+    env = dict(os.environ)
+    env.setdefault("OMP_NUM_THREADS", str(min(16, os.cpu_count() or 1)))
+    env.setdefault("OMP_PROC_BIND", "close")
+    env.setdefault("OMP_PLACES", "cores")
+    env.setdefault("OMP_WAIT_POLICY", "passive")
+    try:
+        r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-child", "--B", str(B)],
+                           capture_output=True, text=True, env=env, timeout=240)
+        line = [l for l in r.stdout.splitlines() if l.startswith("{")]
+        return json.loads(line[-1]) if r.returncode == 0 and line else None
+    except (subprocess.TimeoutExpired, json.JSONDecodeError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--B", type=int, default=8, help=argparse.SUPPRESS)
+    args = ap.parse_args()
+    if args.cpu_child:
+        cpu_child(args.B, reps=2000)
+        return 0
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+    res = gpu_leg(args.steps, args.warmup, [8, 1, 16])
+    h = res[8]
+    b1, _ = ffn_bytes(8)
+    line = {
+        "metric": METRIC,
+        "value": round(h["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 weights, f16 MFMA operands, f32 accumulate",
+        "data": "synthetic (seeded Q4_0 weights, N(0,1) activations), 4 weight copies rotated",
+        "config": {
+            "workload": "FFN block verify: gate/up 17408x5120 Q4_0 RSI + SwiGLU, down 5120x17408 Q4_0 RS",
+            "B": 8, "d_model": H, "ffn": I, "weight_copies": NCOPIES,
+            "frac_of_peak": round(h["gbs"] / PEAK_GBS, 4),
+            "verified_tok_s": round(h["tok_s"], 1),
+            "per_B": {str(B): {"ms_per_step": round(r["ms_per_step"], 5), "GB_s": round(r["gbs"], 1),
+                               "frac_of_peak": round(r["gbs"] / PEAK_GBS, 4),
+                               "verified_tok_s": round(r["tok_s"], 1),
+                               "swiglu_ms": round(r["swiglu_ms"], 5), "down_ms": round(r["down_ms"], 5),
+                               "swiglu_GB_s": round(r["swiglu_gbs"], 1), "down_GB_s": round(r["down_gbs"], 1)}
+                      for B, r in sorted(res.items())},
+        },
+        "roofline": {
+            "kernel": "q4_gemv_kernel<2,SWIGLU> (gate/up pair), B=8",
+            "bound": "hbm",
+            "achieved": round(h["swiglu_gbs"], 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(h["swiglu_gbs"] / PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes": b1,
+        },
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_leg(8),
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,187 @@
+// C ABI entry points of libcwen_gpu: context, weight upload, GEMV dispatch.
+#include <stdlib.h>
+#include <string.h>
+#include "cwen_internal.h"
+
+namespace {
+
+constexpr size_t kPartialFloats = (size_t)16 << 20;  // 64 MiB of split-K partials
+constexpr int kCounters = 1 << 16;
+
+int env_int(const char *name, int dflt, int lo, int hi) {
+  const char *s = getenv(name);
+  if (!s || !*s) return dflt;
+  char *end = nullptr;
+  long v = strtol(s, &end, 10);
+  if (*end || v < lo || v > hi) return dflt;
+  return (int)v;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char *cwen_version(void) { return "cwen-gpu 0.1 gfx950"; }
+
+int cwen_ctx_create(int device, cwen_ctx **out) {
+  if (!out) return CWEN_EINVAL;
+  *out = nullptr;
+  int ndev = 0;
+  CWEN_HIP_TRY(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipSetDevice(device));
+  cwen_ctx *c = (cwen_ctx *)calloc(1, sizeof(cwen_ctx));
+  if (!c) return CWEN_ENOMEM;
+  c->device = device;
+  c->wg_target = env_int("CWEN_GEMV_WG_TARGET", 512, 64, 65536);
+  if (hipMalloc((void **)&c->partials, kPartialFloats * sizeof(float)) != hipSuccess) {
+    free(c);
+    return CWEN_ENOMEM;
+  }
+  if (hipMalloc((void **)&c->counters, kCounters * sizeof(int)) != hipSuccess) {
+    (void)hipFree(c->partials);
+    free(c);
+    return CWEN_ENOMEM;
+  }
+  c->partials_floats = kPartialFloats;
+  c->ncounters = kCounters;
+  if (hipMemset(c->counters, 0, kCounters * sizeof(int)) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess) {
+    (void)hipFree(c->counters);
+    (void)hipFree(c->partials);
+    free(c);
+    return CWEN_EHIP;
+  }
+  *out = c;
+  return CWEN_OK;
+}
+
+int cwen_ctx_destroy(cwen_ctx *ctx) {
+  if (!ctx) return CWEN_EINVAL;
+  (void)hipSetDevice(ctx->device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(ctx->partials);
+  (void)hipFree(ctx->counters);
+  free(ctx);
+  return CWEN_OK;
+}
+
+int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *scales,
+                       int ne0, int ne1, cwen_weight **out) {
+  if (!ctx || !data || !out || ne0 <= 0 || ne1 <= 0) return CWEN_EINVAL;
+  *out = nullptr;
+  if (type != CWEN_T_Q4_0 && type != CWEN_T_Q4_0RS && type != CWEN_T_Q4_0RSI) return CWEN_ETYPE;
+  if (ne0 % Q4_TILE_K) return CWEN_EINVAL;
+  const bool split_scales = (type != CWEN_T_Q4_0);
+  if (split_scales && !scales) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipSetDevice(ctx->device));
+
+  const size_t nblk = (size_t)(ne0 / 32) * ne1;
+  size_t qbytes = 0, sbytes = 0;
+  int nside = 1;
+  if (type == CWEN_T_Q4_0) qbytes = nblk * 18;
+  else if (type == CWEN_T_Q4_0RS) { qbytes = nblk * 16; sbytes = nblk * 2; }
+  else { qbytes = nblk * 32; sbytes = nblk * 4; nside = 2; }
+
+  cwen_weight *w = (cwen_weight *)calloc(1, sizeof(cwen_weight));
+  if (!w) return CWEN_ENOMEM;
+  w->ctx = ctx;
+  w->type = type;
+  w->ne0 = ne0;
+  w->ne1 = ne1;
+  w->nside = nside;
+  w->nrg = (ne1 + Q4_ROWS - 1) / Q4_ROWS;
+  w->nkt = ne0 / Q4_TILE_K;
+  w->bytes = (size_t)w->nrg * w->nkt * nside * Q4_TILE_BYTES;
+  w->src_bytes = qbytes + sbytes;
+  q4_choose_split(ctx, w);
+
+  uint8_t *dsrc = nullptr;
+  uint16_t *dsc = nullptr;
+  int rc = CWEN_OK;
+  if (hipMalloc((void **)&w->dev, w->bytes) != hipSuccess) { rc = CWEN_ENOMEM; goto fail; }
+  if (hipMalloc((void **)&dsrc, qbytes) != hipSuccess) { rc = CWEN_ENOMEM; goto fail; }
+  if (sbytes && hipMalloc((void **)&dsc, sbytes) != hipSuccess) { rc = CWEN_ENOMEM; goto fail; }
+  if (hipMemcpy(dsrc, data, qbytes, hipMemcpyHostToDevice) != hipSuccess) { rc = CWEN_EHIP; goto fail; }
+  if (sbytes && hipMemcpy(dsc, scales, sbytes, hipMemcpyHostToDevice) != hipSuccess) {
+    rc = CWEN_EHIP;
+    goto fail;
+  }
+  rc = q4_repack(w, dsrc, dsc, nullptr);
+  if (rc != CWEN_OK) goto fail;
+  if (hipDeviceSynchronize() != hipSuccess) { rc = CWEN_EHIP; goto fail; }
+  (void)hipFree(dsrc);
+  if (dsc) (void)hipFree(dsc);
+  *out = w;
+  return CWEN_OK;
+fail:
+  if (dsrc) (void)hipFree(dsrc);
+  if (dsc) (void)hipFree(dsc);
+  if (w->dev) (void)hipFree(w->dev);
+  free(w);
+  return rc;
+}
+
+int cwen_weight_free(cwen_weight *w) {
+  if (!w) return CWEN_EINVAL;
+  (void)hipSetDevice(w->ctx->device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(w->dev);
+  free(w);
+  return CWEN_OK;
+}
+
+int cwen_weight_info(const cwen_weight *w, int *type, int *ne0, int *ne1, int *nside,
+                     size_t *stream_bytes) {
+  if (!w) return CWEN_EINVAL;
+  if (type) *type = w->type;
+  if (ne0) *ne0 = w->ne0;
+  if (ne1) *ne1 = w->ne1;
+  if (nside) *nside = w->nside;
+  if (stream_bytes) *stream_bytes = w->bytes;
+  return CWEN_OK;
+}
+
+static int check_act(const float *X, int xs, int K, int B) {
+  if (!X || B < 1 || B > CWEN_BMAX) return CWEN_EINVAL;
+  if (!aligned16(X) || (xs & 3) || (B > 1 && xs < K)) return CWEN_EINVAL;
+  return CWEN_OK;
+}
+static int check_out(const float *Y, int ys, int M, int B) {
+  if (!Y || (B > 1 && ys < M) || ys < 0) return CWEN_EINVAL;
+  return CWEN_OK;
+}
+
+int cwen_gemvb(cwen_ctx *ctx, const cwen_weight *W, int side, const float *X, int xs, float *Y,
+               int ys, int B, void *stream) {
+  if (!ctx || !W || W->ctx != ctx) return CWEN_EINVAL;
+  if (side < 0 || side >= W->nside) return CWEN_EINVAL;
+  int rc = check_act(X, xs, W->ne0, B);
+  if (rc) return rc;
+  if ((rc = check_out(Y, ys, W->ne1, B))) return rc;
+  return q4_gemv_launch(ctx, W, 1, side, Q4_EPI_STORE, X, xs, Y, nullptr, ys, B,
+                        (hipStream_t)stream);
+}
+
+int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *YA,
+                    float *YB, int ys, int B, void *stream) {
+  if (!ctx || !W || W->ctx != ctx || W->nside != 2) return CWEN_EINVAL;
+  int rc = check_act(X, xs, W->ne0, B);
+  if (rc) return rc;
+  if ((rc = check_out(YA, ys, W->ne1, B)) || (rc = check_out(YB, ys, W->ne1, B))) return rc;
+  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_STORE, X, xs, YA, YB, ys, B, (hipStream_t)stream);
+}
+
+int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *H,
+                      int hs, int B, void *stream) {
+  if (!ctx || !W || W->ctx != ctx || W->nside != 2) return CWEN_EINVAL;
+  int rc = check_act(X, xs, W->ne0, B);
+  if (rc) return rc;
+  if ((rc = check_out(H, hs, W->ne1, B))) return rc;
+  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_SWIGLU, X, xs, H, nullptr, hs, B,
+                        (hipStream_t)stream);
+}
+
+}  // extern "C"

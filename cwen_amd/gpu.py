@@ -1,0 +1,150 @@
+"""ctypes binding of libcwen_gpu.so (the C ABI in include/cwen_gpu.h).
+
+This is plumbing for Python callers (tests, bench): every compute call goes
+straight to the HIP library.  Importing it on a machine without the built
+library raises; there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libcwen_gpu.so"
+
+CWEN_OK = 0
+ERRORS = {-1: "EINVAL", -2: "EHIP", -3: "ENOMEM", -4: "ETYPE", -5: "ESCRATCH"}
+
+T_F32, T_Q4_0, T_Q8_0, T_Q6_K, T_Q4_0RS, T_Q4_0RSI = 0, 2, 8, 14, 101, 102
+BMAX = 16
+
+# (name, restype, argtypes) of every exported entry point.
+_VP, _I, _F = C.c_void_p, C.c_int, C.POINTER(C.c_float)
+SIGNATURES = [
+    ("cwen_version", C.c_char_p, []),
+    ("cwen_ctx_create", _I, [_I, C.POINTER(_VP)]),
+    ("cwen_ctx_destroy", _I, [_VP]),
+    ("cwen_weight_upload", _I, [_VP, _I, _VP, _VP, _I, _I, C.POINTER(_VP)]),
+    ("cwen_weight_free", _I, [_VP]),
+    ("cwen_weight_info", _I, [_VP, C.POINTER(_I), C.POINTER(_I), C.POINTER(_I), C.POINTER(_I),
+                              C.POINTER(C.c_size_t)]),
+    ("cwen_gemvb", _I, [_VP, _VP, _I, _VP, _I, _VP, _I, _I, _VP]),
+    ("cwen_gemvb_pair", _I, [_VP, _VP, _VP, _I, _VP, _VP, _I, _I, _VP]),
+    ("cwen_gemvb_swiglu", _I, [_VP, _VP, _VP, _I, _VP, _I, _I, _VP]),
+]
+
+
+class CwenError(RuntimeError):
+    def __init__(self, fn: str, rc: int):
+        super().__init__(f"{fn} failed: {rc} ({ERRORS.get(rc, '?')})")
+        self.rc = rc
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m cwen_amd.build`")
+        L = C.CDLL(str(LIB_PATH))
+        for name, res, args in SIGNATURES:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(fn: str, rc: int) -> None:
+    if rc != CWEN_OK:
+        raise CwenError(fn, rc)
+
+
+def _ptr(t) -> int:
+    """Device pointer of a torch tensor (or raw int)."""
+    return t if isinstance(t, int) else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return stream if isinstance(stream, int) else stream.cuda_stream
+
+
+class Context:
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check("cwen_ctx_create", lib().cwen_ctx_create(device, C.byref(h)))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h:
+            lib().cwen_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Weight:
+    """A device-resident weight uploaded from a reference layout (host arrays)."""
+
+    def __init__(self, ctx: Context, wtype: int, data: np.ndarray, scales: np.ndarray | None,
+                 ne0: int, ne1: int):
+        data = np.ascontiguousarray(data)
+        sc = None if scales is None else np.ascontiguousarray(scales)
+        h = C.c_void_p()
+        check("cwen_weight_upload",
+              lib().cwen_weight_upload(ctx.h, wtype, data.ctypes.data,
+                                       None if sc is None else sc.ctypes.data,
+                                       ne0, ne1, C.byref(h)))
+        self.h, self.ctx, self.type, self.K, self.M = h, ctx, wtype, ne0, ne1
+
+    def info(self) -> dict:
+        t, k, m, ns = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        sb = C.c_size_t()
+        check("cwen_weight_info", lib().cwen_weight_info(self.h, C.byref(t), C.byref(k), C.byref(m),
+                                                         C.byref(ns), C.byref(sb)))
+        return {"type": t.value, "ne0": k.value, "ne1": m.value, "nside": ns.value,
+                "stream_bytes": sb.value}
+
+    def free(self) -> None:
+        if self.h:
+            lib().cwen_weight_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def gemvb(ctx: Context, W: Weight, X, Y, B: int, side: int = 0, xs: int | None = None,
+          ys: int | None = None, stream=None) -> None:
+    xs = W.K if xs is None else xs
+    ys = W.M if ys is None else ys
+    check("cwen_gemvb", lib().cwen_gemvb(ctx.h, W.h, side, _ptr(X), xs, _ptr(Y), ys, B, _stream(stream)))
+
+
+def gemvb_pair(ctx: Context, W: Weight, X, YA, YB, B: int, xs: int | None = None,
+               ys: int | None = None, stream=None) -> None:
+    xs = W.K if xs is None else xs
+    ys = W.M if ys is None else ys
+    check("cwen_gemvb_pair", lib().cwen_gemvb_pair(ctx.h, W.h, _ptr(X), xs, _ptr(YA), _ptr(YB), ys, B,
+                                                   _stream(stream)))
+
+
+def gemvb_swiglu(ctx: Context, W: Weight, X, H, B: int, xs: int | None = None,
+                 hs: int | None = None, stream=None) -> None:
+    xs = W.K if xs is None else xs
+    hs = W.M if hs is None else hs
+    check("cwen_gemvb_swiglu", lib().cwen_gemvb_swiglu(ctx.h, W.h, _ptr(X), xs, _ptr(H), hs, B,
+                                                       _stream(stream)))

@@ -1,0 +1,108 @@
+"""Seeded synthetic inputs for the block-verify workloads (numpy, host side).
+
+Distributions follow the workload definitions:
+  * Q4_0 weights: per 32-weight block an f16 scale d = f16(|N(0, 0.02)| / 8)
+    and 16 bytes of nibbles uniform over 0..15; weight = (nibble - 8) * d.
+  * Q6_K weights: ql/qh bytes uniform (6-bit quants uniform), int8 sub-scales
+    uniform over [-128, 127], f16 d = f16(|N(0, 0.002)|).
+  * Q8_0 weights: int8 quants uniform, f16 d = f16(|N(0, 0.02)| / 64).
+  * Activations: f32 N(0, 1).
+
+Generators are numpy PCG64 streams keyed by (seed, purpose) so every array
+is reproducible on any host with the same numpy.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+QK4 = 32
+QK_K = 256
+
+
+def rng(seed: int, *key: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(np.random.SeedSequence([seed, *key])))
+
+
+def _f16_bits(x: np.ndarray) -> np.ndarray:
+    return x.astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+def q4_scales(g: np.random.Generator, n: int) -> np.ndarray:
+    return _f16_bits(np.abs(g.standard_normal(n, dtype=np.float32) * np.float32(0.02)) / np.float32(8))
+
+
+def q4_nibble_bytes(g: np.random.Generator, n: int) -> np.ndarray:
+    return g.integers(0, 256, size=n, dtype=np.uint8)
+
+
+def q4_rs(seed: int, M: int, K: int, key: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """CWENR split layout: qs[M][nb][16] bytes, sc[M][nb] f16 bits."""
+    nb = K // QK4
+    g = rng(seed, 1, key)
+    sc = q4_scales(g, M * nb)
+    qs = q4_nibble_bytes(g, M * nb * 16)
+    return qs, sc
+
+
+def q4_rsi(seed: int, M: int, K: int, key: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """CWENR interleaved pair: qs[M][nb][A16|B16], sc[M][nb][A|B]."""
+    nb = K // QK4
+    g = rng(seed, 2, key)
+    sc = q4_scales(g, M * nb * 2)
+    qs = q4_nibble_bytes(g, M * nb * 32)
+    return qs, sc
+
+
+def q4_gguf(seed: int, M: int, K: int, key: int = 0) -> np.ndarray:
+    """GGUF Q4_0: 18-byte blocks {f16 d; u8 qs[16]} row-major."""
+    nb = K // QK4
+    g = rng(seed, 3, key)
+    sc = q4_scales(g, M * nb)
+    qs = q4_nibble_bytes(g, M * nb * 16)
+    out = np.empty((M * nb, 18), dtype=np.uint8)
+    out[:, 0:2] = sc.view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = qs.reshape(-1, 16)
+    return out.reshape(-1)
+
+
+def q6_k(seed: int, M: int, K: int, key: int = 0) -> np.ndarray:
+    """GGUF Q6_K: 210-byte super-blocks {ql[128] qh[64] i8 sc[16] f16 d}."""
+    nsb = M * (K // QK_K)
+    g = rng(seed, 4, key)
+    blk = g.integers(0, 256, size=(nsb, 210), dtype=np.uint8)
+    d = _f16_bits(np.abs(g.standard_normal(nsb, dtype=np.float32) * np.float32(0.002)))
+    blk[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+    return blk.reshape(-1)
+
+
+def q8_0(seed: int, M: int, K: int, key: int = 0) -> np.ndarray:
+    """GGUF Q8_0: 34-byte blocks {f16 d; i8 qs[32]}."""
+    nblk = M * (K // QK4)
+    g = rng(seed, 5, key)
+    blk = g.integers(0, 256, size=(nblk, 34), dtype=np.uint8)
+    d = _f16_bits(np.abs(g.standard_normal(nblk, dtype=np.float32) * np.float32(0.02)) / np.float32(64))
+    blk[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    return blk.reshape(-1)
+
+
+def activations(seed: int, B: int, K: int, key: int = 0) -> np.ndarray:
+    """f32 N(0,1) activation block [B][K]."""
+    return rng(seed, 6, key).standard_normal((B, K), dtype=np.float32)
+
+
+def rs_to_gguf(qs: np.ndarray, sc: np.ndarray) -> np.ndarray:
+    """Re-assemble a split (RS) tensor into GGUF 18-byte blocks (the inverse of
+    the reference's v3 split, tools/repack_q4.py:75-81)."""
+    nblk = sc.size
+    out = np.empty((nblk, 18), dtype=np.uint8)
+    out[:, 0:2] = sc.view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = qs.reshape(-1, 16)
+    return out.reshape(-1)
+
+
+def rsi_side(qs: np.ndarray, sc: np.ndarray, M: int, K: int, side: int) -> tuple[np.ndarray, np.ndarray]:
+    """Extract one side of an interleaved pair as a split (RS) tensor."""
+    nb = K // QK4
+    q = qs.reshape(M, nb, 2, 16)[:, :, side, :]
+    s = sc.reshape(M, nb, 2)[:, :, side]
+    return np.ascontiguousarray(q).reshape(-1), np.ascontiguousarray(s).reshape(-1)

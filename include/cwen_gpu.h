@@ -1,0 +1,103 @@
+/* cwen_gpu.h -- C ABI of the MI355X (gfx950) block-verify library.
+ *
+ * The reference engine (maci0/cwen run.c) is one C translation unit whose
+ * hot path is a set of static functions over global state.  This header is
+ * the drop-in boundary for that path: plain C types, plain pointers and
+ * sizes, no C++ or torch types.  Each entry point names the reference
+ * function it replaces (run.c:line).
+ *
+ * Conventions
+ *   - Every function returns an int status: 0 on success, a negative
+ *     CWEN_E* code on failure (the reference exit(1)s or asserts instead;
+ *     the host wrapper maps a failure to that policy).
+ *   - Activation and output pointers (X, Y, logits ...) are DEVICE pointers
+ *     to f32 data.  X and Y rows must start 16-byte aligned and their
+ *     strides (xs, ys, in floats) must be multiples of 4.
+ *   - `stream` is a hipStream_t passed as void*; NULL means the default
+ *     stream.  Calls are asynchronous on that stream unless stated.
+ *   - One context drives one device.  A context and every weight created
+ *     on it are not thread-safe, and calls on different streams that share
+ *     a context must not overlap (they share the context's scratch).
+ */
+#ifndef CWEN_GPU_H
+#define CWEN_GPU_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define CWEN_OK         0
+#define CWEN_EINVAL   (-1)   /* bad argument or shape                    */
+#define CWEN_EHIP     (-2)   /* a HIP runtime call failed                */
+#define CWEN_ENOMEM   (-3)   /* device allocation failed                 */
+#define CWEN_ETYPE    (-4)   /* weight type not supported by this call   */
+#define CWEN_ESCRATCH (-5)   /* a shape exceeds the context's scratch    */
+
+/* ggml / CWENR weight type ids -- the same numeric ids as run.c:97-103 */
+#define CWEN_T_F32      0
+#define CWEN_T_Q4_0     2    /* GGUF 18-byte blocks {f16 d; u8 qs[16]}          */
+#define CWEN_T_Q8_0     8    /* GGUF 34-byte blocks {f16 d; i8 qs[32]}          */
+#define CWEN_T_Q6_K    14    /* GGUF 210-byte super-blocks of 256                */
+#define CWEN_T_Q4_0RS  101   /* CWENR split: qs[ne1][nb][16] + f16 sc[ne1][nb]   */
+#define CWEN_T_Q4_0RSI 102   /* CWENR interleaved pair: qs[ne1][nb][A16|B16],
+                                 f16 sc[ne1][nb][A|B]                            */
+
+/* Largest verify block (SPEC_BMAX, run.c:192). */
+#define CWEN_BMAX 16
+
+typedef struct cwen_ctx cwen_ctx;        /* device, stream-independent scratch */
+typedef struct cwen_weight cwen_weight;  /* one device-resident weight matrix  */
+
+/* Library version string, e.g. "cwen-gpu 0.1 gfx950". */
+const char *cwen_version(void);
+
+/* Create a context on HIP device `device`: selects it, allocates the split-K
+ * scratch.  Replaces alloc_state's scratch part (run.c:3928-4005). */
+int cwen_ctx_create(int device, cwen_ctx **out);
+int cwen_ctx_destroy(cwen_ctx *ctx);
+
+/* Upload one weight matrix given in a reference layout in HOST memory and
+ * repack it on the device into the tile layout the kernels stream.
+ * `data`/`scales` are what the reference's Tensor.data / Tensor.scales point
+ * at (run.c:132): for Q4_0RS and Q4_0RSI `scales` is the f16 scale channel,
+ * for the self-contained GGUF types it is NULL.  ne0 = K (inputs), ne1 = M
+ * (rows).  A Q4_0RSI blob is uploaded once and holds both sides of the pair
+ * (the reference binds it as two Tensors with pair_side 0/1 over the same
+ * data, run.c:3544-3579).  Replaces the CWENR/GGUF binding of a tensor
+ * (run.c:3372-3466, 3544-3579); the reference uses it in place from mmap. */
+int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *scales,
+                       int ne0, int ne1, cwen_weight **out);
+int cwen_weight_free(cwen_weight *w);
+/* Device bytes the kernels stream per full pass over the weight. */
+int cwen_weight_info(const cwen_weight *w, int *type, int *ne0, int *ne1,
+                     int *nside, size_t *stream_bytes);
+
+/* Batched GEMV over a verify block: Y[b*ys + i] = row i of W . X[b*xs ...]
+ * for b < B (1 <= B <= 16).  For a Q4_0RSI pair weight `side` picks A (0)
+ * or B (1), as Tensor.pair_side does; other types require side 0.
+ * Per output the arithmetic does not depend on B or on the other columns,
+ * so a column computed in a block is bit-identical to the same column
+ * computed alone.  Replaces gemvb (run.c:1577-1680) and, at B=1, gemv
+ * (run.c:1419-1527). */
+int cwen_gemvb(cwen_ctx *ctx, const cwen_weight *W, int side,
+               const float *X, int xs, float *Y, int ys, int B, void *stream);
+
+/* Both sides of a Q4_0RSI pair in one pass over the interleaved stream:
+ * YA = W_A . X, YB = W_B . X.  Replaces the two gemvb calls over one blob
+ * in layer_full_blk (run.c:2724-2725) and gemv_dual_same_shape (run.c:1802). */
+int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs,
+                    float *YA, float *YB, int ys, int B, void *stream);
+
+/* Gate/up pair with the SwiGLU epilogue fused: H[b*hs + i] =
+ * silu(W_A[i] . X_b) * (W_B[i] . X_b).  Replaces mlp_blk's gate gemvb, up
+ * gemvb and silu_mul (run.c:2677-2680). */
+int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs,
+                      float *H, int hs, int B, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CWEN_GPU_H */

@@ -1,0 +1,226 @@
+"""ctypes binding of the oracle (liboracle.so) and of the reference checker
+builds (oracle/_ref/libcwen_ref_*.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "liboracle.so"
+REF_DIR = HERE / "_ref"
+
+_VP, _I, _F = C.c_void_p, C.c_int, C.c_float
+
+
+class OrcTensor(C.Structure):
+    _fields_ = [("data", _VP), ("scales", _VP), ("type", _I), ("ne0", _I), ("ne1", _I),
+                ("pair_side", _I)]
+
+
+def _f32p(a: np.ndarray) -> int:
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data
+
+
+def _i32p(a: np.ndarray) -> int:
+    assert a.dtype == np.int32 and a.flags.c_contiguous
+    return a.ctypes.data
+
+
+class Oracle:
+    """The scalar C restatement (oracle/cwen_oracle.c)."""
+
+    def __init__(self, path: Path = ORACLE_SO):
+        if not path.exists():
+            raise RuntimeError(f"{path} not built; run `make -C oracle`")
+        L = C.CDLL(str(path))
+        L.orc_f16_to_f32.restype = _F
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [_F]
+        L.orc_gemvb.restype = _I
+        L.orc_gemvb.argtypes = [C.POINTER(OrcTensor), _VP, _I, _VP, _I, _I]
+        L.orc_silu_mul.argtypes = [_VP, _VP, _I]
+        L.orc_rmsnorm.argtypes = [_VP, _VP, _VP, _I]
+        L.orc_conv1d_update.argtypes = [_VP, _VP, _VP, _I]
+        L.orc_gdn_step.argtypes = [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I]
+        L.orc_argmax.restype = _I
+        L.orc_argmax.argtypes = [_VP, _I]
+        L.orc_walk.restype = _I
+        L.orc_walk.argtypes = [_VP, C.c_long, _I, _VP, _I, C.POINTER(_I)]
+        L.orc_ngram_draft.restype = _I
+        L.orc_ngram_draft.argtypes = [_VP, _I, _VP, _I, _I]
+        self.L = L
+
+    def gemvb(self, wtype: int, data: np.ndarray, scales, K: int, M: int, X: np.ndarray,
+              side: int = 0) -> np.ndarray:
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        B = X.shape[0]
+        Y = np.empty((B, M), dtype=np.float32)
+        t = OrcTensor(data.ctypes.data, None if scales is None else scales.ctypes.data,
+                      wtype, K, M, side)
+        rc = self.L.orc_gemvb(C.byref(t), _f32p(X), K, _f32p(Y), M, B)
+        if rc:
+            raise RuntimeError(f"orc_gemvb rc={rc}")
+        return Y
+
+    def silu_mul(self, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+        a = np.array(a, dtype=np.float32, copy=True)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        self.L.orc_silu_mul(_f32p(a), _f32p(b), a.size)
+        return a
+
+    def rmsnorm(self, x: np.ndarray, w: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        o = np.empty_like(x)
+        self.L.orc_rmsnorm(_f32p(o), _f32p(x), _f32p(np.ascontiguousarray(w, np.float32)), x.size)
+        return o
+
+    def conv1d_update(self, qkv: np.ndarray, hist: np.ndarray, kw: np.ndarray):
+        qkv = np.array(qkv, dtype=np.float32, copy=True)
+        hist = np.array(hist, dtype=np.float32, copy=True)
+        self.L.orc_conv1d_update(_f32p(qkv), _f32p(hist), _f32p(np.ascontiguousarray(kw, np.float32)),
+                                 qkv.size)
+        return qkv, hist
+
+    def gdn_step(self, S, qkv, z, decay, beta, wn, nkh, nvh, dk):
+        S = np.array(S, dtype=np.float32, copy=True)
+        qkv = np.array(qkv, dtype=np.float32, copy=True)
+        out = np.empty(nvh * dk, dtype=np.float32)
+        args = [np.ascontiguousarray(a, np.float32) for a in (z, decay, beta, wn)]
+        self.L.orc_gdn_step(_f32p(S), _f32p(qkv), *(_f32p(a) for a in args), _f32p(out), nkh, nvh, dk)
+        return S, qkv, out
+
+    def argmax(self, lg: np.ndarray) -> int:
+        lg = np.ascontiguousarray(lg, dtype=np.float32)
+        return self.L.orc_argmax(_f32p(lg), lg.size)
+
+    def walk(self, logits: np.ndarray, drafts: np.ndarray) -> tuple[int, int]:
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        d = np.ascontiguousarray(drafts, dtype=np.int32)
+        bonus = C.c_int()
+        k = self.L.orc_walk(_f32p(logits), logits.shape[1], logits.shape[1], _i32p(d), d.size,
+                            C.byref(bonus))
+        return k, bonus.value
+
+    def ngram_draft(self, hist: np.ndarray, n_key: int, max_d: int) -> np.ndarray:
+        h = np.ascontiguousarray(hist, dtype=np.int32)
+        out = np.zeros(max(max_d, 1), dtype=np.int32)
+        n = self.L.orc_ngram_draft(_i32p(h), h.size, _i32p(out), n_key, max_d)
+        return out[:n]
+
+
+def cpu_has_avx512() -> bool:
+    try:
+        flags = Path("/proc/cpuinfo").read_text()
+    except OSError:
+        return False
+    return all(f" {x}" in flags for x in ("avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512_vnni"))
+
+
+def ref_lib_path(isa: str | None = None) -> Path:
+    if isa is None:
+        isa = "avx512" if cpu_has_avx512() else "avx2"
+    return REF_DIR / f"libcwen_ref_{isa}.so"
+
+
+class Reference:
+    """The reference engine's own kernels, compiled from its run.c (oracle/_ref)."""
+
+    def __init__(self, isa: str | None = None):
+        path = ref_lib_path(isa)
+        if not path.exists():
+            raise RuntimeError(f"{path} not built (needs the reference tree; `make -C oracle`)")
+        self.isa = path.stem.split("_")[-1]
+        L = C.CDLL(str(path))
+        L.ref_vocab.restype = _I
+        L.ref_gemv.restype = _I
+        L.ref_gemv.argtypes = [_I, _VP, _VP, _I, _I, _I, _VP, _VP]
+        L.ref_gemvb.restype = _I
+        L.ref_gemvb.argtypes = [_I, _VP, _VP, _I, _I, _I, _VP, _I, _VP, _I, _I]
+        L.ref_silu_mul.argtypes = [_VP, _VP, _I]
+        L.ref_rmsnorm.argtypes = [_VP, _VP, _VP, _I]
+        L.ref_conv1d_update.restype = _I
+        L.ref_conv1d_update.argtypes = [_VP, _VP, _VP]
+        L.ref_gdn_step.restype = _I
+        L.ref_gdn_step.argtypes = [_VP, _VP, _VP, _VP, _VP, _VP, _VP]
+        L.ref_argmax.restype = _I
+        L.ref_argmax.argtypes = [_VP, _I]
+        L.ref_walk.restype = _I
+        L.ref_walk.argtypes = [_VP, C.c_long, _I, _VP, _I, C.POINTER(_I)]
+        L.ref_ngram_draft.restype = _I
+        L.ref_ngram_draft.argtypes = [_VP, _I, _VP, _I, _I]
+        L.ref_omp_threads.restype = _I
+        self.L = L
+        self.vocab = L.ref_vocab()
+
+    def gemvb(self, wtype, data, scales, K, M, X, side=0, out: np.ndarray | None = None):
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        B = X.shape[0]
+        Y = np.empty((B, M), dtype=np.float32) if out is None else out
+        rc = self.L.ref_gemvb(wtype, data.ctypes.data, None if scales is None else scales.ctypes.data,
+                              K, M, side, _f32p(X), K, Y.ctypes.data, M, B)
+        if rc:
+            raise RuntimeError(f"ref_gemvb rc={rc}")
+        return Y
+
+    def gemv(self, wtype, data, scales, K, M, x, side=0):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(M, dtype=np.float32)
+        rc = self.L.ref_gemv(wtype, data.ctypes.data, None if scales is None else scales.ctypes.data,
+                             K, M, side, _f32p(x), _f32p(y))
+        if rc:
+            raise RuntimeError(f"ref_gemv rc={rc}")
+        return y
+
+    def silu_mul(self, a, b):
+        a = np.array(a, dtype=np.float32, copy=True)
+        self.L.ref_silu_mul(_f32p(a), _f32p(np.ascontiguousarray(b, np.float32)), a.size)
+        return a
+
+    def rmsnorm(self, x, w):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        o = np.empty_like(x)
+        self.L.ref_rmsnorm(_f32p(o), _f32p(x), _f32p(np.ascontiguousarray(w, np.float32)), x.size)
+        return o
+
+    def conv1d_update(self, qkv, hist, kw):
+        qkv = np.array(qkv, dtype=np.float32, copy=True)
+        hist = np.array(hist, dtype=np.float32, copy=True)
+        self.L.ref_conv1d_update(_f32p(qkv), _f32p(hist), _f32p(np.ascontiguousarray(kw, np.float32)))
+        return qkv, hist
+
+    def gdn_step(self, S, qkv, z, decay, beta, wn):
+        S = np.array(S, dtype=np.float32, copy=True)
+        qkv = np.array(qkv, dtype=np.float32, copy=True)
+        z = np.array(z, dtype=np.float32, copy=True)
+        decay = np.array(decay, dtype=np.float32, copy=True)
+        beta = np.array(beta, dtype=np.float32, copy=True)
+        out = np.empty(48 * 128, dtype=np.float32)
+        self.L.ref_gdn_step(_f32p(S), _f32p(qkv), _f32p(z), _f32p(decay), _f32p(beta),
+                            _f32p(np.ascontiguousarray(wn, np.float32)), _f32p(out))
+        return S, qkv, out
+
+    def argmax(self, lg):
+        lg = np.ascontiguousarray(lg, dtype=np.float32)
+        return self.L.ref_argmax(_f32p(lg), lg.size)
+
+    def walk(self, logits, drafts):
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        d = np.ascontiguousarray(drafts, dtype=np.int32)
+        bonus = C.c_int()
+        k = self.L.ref_walk(_f32p(logits), logits.shape[1], logits.shape[1], _i32p(d), d.size,
+                            C.byref(bonus))
+        return k, bonus.value
+
+    def ngram_draft(self, hist, n_key, max_d):
+        h = np.ascontiguousarray(hist, dtype=np.int32)
+        out = np.zeros(max(max_d, 1), dtype=np.int32)
+        n = self.L.ref_ngram_draft(_i32p(h), h.size, _i32p(out), n_key, max_d)
+        return out[:n]

@@ -1,0 +1,314 @@
+"""Pins the oracle (oracle/cwen_oracle.c) before anything is checked against it.
+
+Each oracle function is checked three ways where possible:
+  * against the reference engine's own kernels compiled from its run.c
+    (oracle/_ref): bit-exact where the reference AVX2 build runs the same
+    scalar code path (RS/RSI/Q8_0 dots, silu_mul, conv), within f32
+    reassociation tolerance where it runs SIMD (GGUF Q4_0, Q6_K, rmsnorm,
+    GDN);
+  * against an independent numpy float64 decode on tiny shapes;
+  * against closed forms / invariants (numpy's float16 conversion, argmax
+    semantics, GDN identities).
+CPU only.
+"""
+import numpy as np
+import pytest
+
+from cwen_amd import synth
+from util import rel_err
+
+T_Q4_0, T_Q8_0, T_Q6_K, T_RS, T_RSI = 2, 8, 14, 101, 102
+
+
+# ---------------------------------------------------------------- f16
+def test_f16_to_f32_exhaustive(oracle):
+    bits = np.arange(65536, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.L.orc_f16_to_f32(int(b)) for b in bits], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_rne(oracle):
+    g = np.random.default_rng(7)
+    x = np.concatenate([
+        g.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** g.integers(-9, 6, 20000),
+        np.array([0.0, -0.0, 65504.0, 65520.0, 1e9, -1e9, np.inf, -np.inf, 5.96e-8, 2.98e-8,
+                  2.99e-8, 1e-8, 6.1e-5, 6.09e-5], dtype=np.float32),
+        # exact halfway points between adjacent halves (ties to even)
+        ((np.arange(1024, 2048, dtype=np.float32) + np.float32(0.5)) * np.float32(2.0 ** -10)),
+    ]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.L.orc_f32_to_f16(float(v)) for v in x], dtype=np.uint16)
+    assert np.array_equal(got, want)
+    assert oracle.L.orc_f32_to_f16(float("nan")) & 0x7e00 == 0x7e00
+
+
+# ---------------------------------------------------------------- dequant (numpy f64)
+def deq_q4_blocks(qs16: np.ndarray, d: np.ndarray) -> np.ndarray:
+    """[nblk,16] bytes + [nblk] f16 bits -> [nblk,32] float64 weights."""
+    lo = (qs16 & 0xF).astype(np.float64) - 8
+    hi = (qs16 >> 4).astype(np.float64) - 8
+    dd = d.view(np.float16).astype(np.float64)[:, None]
+    return np.concatenate([lo, hi], axis=1) * dd
+
+
+def deq_q6k(blk: np.ndarray, M: int, K: int) -> np.ndarray:
+    b = blk.reshape(-1, 210)
+    out = np.empty((b.shape[0], 256))
+    for s in range(b.shape[0]):
+        ql, qh = b[s, :128].astype(np.int32), b[s, 128:192].astype(np.int32)
+        sc = b[s, 192:208].view(np.int8).astype(np.float64)
+        d = float(b[s, 208:210].view(np.float16)[0])
+        for half in range(2):
+            L, Hh, S = ql[64 * half:64 * half + 64], qh[32 * half:32 * half + 32], sc[8 * half:8 * half + 8]
+            for l in range(32):
+                is_ = l // 16
+                q = [(L[l] & 0xF) | (((Hh[l] >> 0) & 3) << 4), (L[l + 32] & 0xF) | (((Hh[l] >> 2) & 3) << 4),
+                     (L[l] >> 4) | (((Hh[l] >> 4) & 3) << 4), (L[l + 32] >> 4) | (((Hh[l] >> 6) & 3) << 4)]
+                for j in range(4):
+                    out[s, 128 * half + l + 32 * j] = d * S[is_ + 2 * j] * (q[j] - 32)
+    return out.reshape(M, K)
+
+
+SMALL = [(64, 256), (48, 512)]
+
+
+@pytest.mark.parametrize("M,K", SMALL)
+def test_q4_rs_vs_f64(oracle, M, K):
+    qs, sc = synth.q4_rs(11, M, K)
+    X = synth.activations(11, 3, K)
+    W = deq_q4_blocks(qs.reshape(-1, 16), sc).reshape(M, K)
+    want = X.astype(np.float64) @ W.T
+    got = oracle.gemvb(T_RS, qs, sc, K, M, X)
+    assert rel_err(got, want) < 2e-6
+
+
+@pytest.mark.parametrize("side", [0, 1])
+def test_q4_rsi_vs_f64(oracle, side):
+    M, K = 40, 256
+    qs, sc = synth.q4_rsi(12, M, K)
+    X = synth.activations(12, 2, K)
+    q1, s1 = synth.rsi_side(qs, sc, M, K, side)
+    W = deq_q4_blocks(q1.reshape(-1, 16), s1).reshape(M, K)
+    got = oracle.gemvb(T_RSI, qs, sc, K, M, X, side=side)
+    assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
+
+
+def test_q4_gguf_vs_f64(oracle):
+    M, K = 32, 512
+    blk = synth.q4_gguf(13, M, K).reshape(-1, 18)
+    W = deq_q4_blocks(np.ascontiguousarray(blk[:, 2:]), np.ascontiguousarray(blk[:, :2]).view(np.uint16).ravel())
+    X = synth.activations(13, 2, K)
+    got = oracle.gemvb(T_Q4_0, blk.ravel(), None, K, M, X)
+    assert rel_err(got, X.astype(np.float64) @ W.reshape(M, K).T) < 2e-6
+
+
+def test_q8_0_vs_f64(oracle):
+    M, K = 24, 256
+    blk = synth.q8_0(14, M, K).reshape(-1, 34)
+    d = np.ascontiguousarray(blk[:, :2]).view(np.float16).astype(np.float64)
+    W = (blk[:, 2:].view(np.int8).astype(np.float64) * d).reshape(M, K)
+    X = synth.activations(14, 2, K)
+    got = oracle.gemvb(T_Q8_0, blk.ravel(), None, K, M, X)
+    assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
+
+
+def test_q6_k_vs_f64(oracle):
+    M, K = 6, 512
+    blk = synth.q6_k(15, M, K)
+    W = deq_q6k(blk, M, K)
+    X = synth.activations(15, 2, K)
+    got = oracle.gemvb(T_Q6_K, blk, None, K, M, X)
+    assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
+
+
+# ---------------------------------------------------------------- vs reference kernels
+@pytest.mark.parametrize("wtype", [T_RS, T_RSI, T_Q8_0])
+def test_scalar_paths_bit_exact_vs_reference_avx2(oracle, ref_avx2, wtype):
+    """The reference AVX2 build runs these dots on its scalar path: same bits."""
+    M, K, B = 96, 1024, 4
+    if wtype == T_RS:
+        data, sc = synth.q4_rs(21, M, K)
+    elif wtype == T_RSI:
+        data, sc = synth.q4_rsi(21, M, K)
+    else:
+        data, sc = synth.q8_0(21, M, K), None
+    X = synth.activations(21, B, K)
+    for side in ([0, 1] if wtype == T_RSI else [0]):
+        want = ref_avx2.gemvb(wtype, data, sc, K, M, X, side=side)
+        got = oracle.gemvb(wtype, data, sc, K, M, X, side=side)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("isa", ["avx2", "avx512"])
+@pytest.mark.parametrize("wtype", [T_Q4_0, T_RS, T_RSI, T_Q8_0, T_Q6_K])
+def test_gemvb_vs_reference(oracle, isa, wtype):
+    from oracle.binding import Reference, ref_lib_path, cpu_has_avx512
+    if not ref_lib_path(isa).exists():
+        pytest.skip("reference checker build absent")
+    if isa == "avx512" and not cpu_has_avx512():
+        pytest.skip("host lacks AVX-512")
+    R = Reference(isa)
+    M, K = 80, 2048
+    if wtype == T_Q4_0:
+        data, sc = synth.q4_gguf(22, M, K), None
+    elif wtype == T_RS:
+        data, sc = synth.q4_rs(22, M, K)
+    elif wtype == T_RSI:
+        data, sc = synth.q4_rsi(22, M, K)
+    elif wtype == T_Q8_0:
+        data, sc = synth.q8_0(22, M, K), None
+    else:
+        data, sc = synth.q6_k(22, M, K), None
+    for B in (1, 3, 8, 16):
+        X = synth.activations(22, B, K, key=B)
+        for side in ([0, 1] if wtype == T_RSI else [0]):
+            want = R.gemvb(wtype, data, sc, K, M, X, side=side)
+            got = oracle.gemvb(wtype, data, sc, K, M, X, side=side)
+            assert rel_err(got, want) < 1e-5, (B, side)
+
+
+def test_silu_mul_bit_exact(oracle, ref_avx2):
+    g = np.random.default_rng(3)
+    a = (g.standard_normal(4099) * 4).astype(np.float32)
+    b = g.standard_normal(4099).astype(np.float32)
+    assert np.array_equal(oracle.silu_mul(a, b).view(np.uint32), ref_avx2.silu_mul(a, b).view(np.uint32))
+
+
+def test_silu_closed_form(oracle):
+    x = np.linspace(-30, 30, 1001).astype(np.float32)
+    one = np.ones_like(x)
+    got = oracle.silu_mul(x, one).astype(np.float64)
+    xd = x.astype(np.float64)
+    assert np.max(np.abs(got - xd / (1 + np.exp(-xd)))) < 1e-5
+
+
+def test_rmsnorm_vs_reference(oracle, ref):
+    g = np.random.default_rng(4)
+    x = g.standard_normal(5120).astype(np.float32)
+    w = (1 + 0.1 * g.standard_normal(5120)).astype(np.float32)
+    assert rel_err(oracle.rmsnorm(x, w), ref.rmsnorm(x, w)) < 1e-6
+    xd = x.astype(np.float64)
+    want = w * xd / np.sqrt(np.mean(xd * xd) + 1e-6)
+    assert rel_err(oracle.rmsnorm(x, w), want) < 1e-6
+
+
+def test_conv1d_bit_exact(oracle, ref_avx2):
+    C = 10240
+    g = np.random.default_rng(5)
+    qkv = g.standard_normal(C).astype(np.float32)
+    hist = g.standard_normal((C, 3)).astype(np.float32)
+    kw = (0.5 * g.standard_normal((C, 4))).astype(np.float32)
+    o1, h1 = oracle.conv1d_update(qkv, hist, kw)
+    o2, h2 = ref_avx2.conv1d_update(qkv, hist, kw)
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(h1, h2)
+    # the history shifts by one and takes the raw input
+    assert np.array_equal(h1[:, :2], hist[:, 1:]) and np.array_equal(h1[:, 2], qkv)
+
+
+def _gdn_inputs(seed):
+    g = np.random.default_rng(seed)
+    S = (0.01 * g.standard_normal((48, 128, 128))).astype(np.float32)
+    qkv = g.standard_normal(10240).astype(np.float32)
+    z = g.standard_normal(6144).astype(np.float32)
+    decay = np.log(g.uniform(0.05, 1.0, 48)).astype(np.float32)
+    beta = (1 / (1 + np.exp(-g.standard_normal(48)))).astype(np.float32)
+    wn = (1 + 0.1 * g.standard_normal(128)).astype(np.float32)
+    return S, qkv, z, decay, beta, wn
+
+
+@pytest.mark.parametrize("isa", ["avx2", "avx512"])
+def test_gdn_step_vs_reference(oracle, isa):
+    from oracle.binding import Reference, ref_lib_path, cpu_has_avx512
+    if not ref_lib_path(isa).exists():
+        pytest.skip("reference checker build absent")
+    if isa == "avx512" and not cpu_has_avx512():
+        pytest.skip("host lacks AVX-512")
+    R = Reference(isa)
+    S, qkv, z, decay, beta, wn = _gdn_inputs(6)
+    S1, q1, o1 = oracle.gdn_step(S, qkv, z, decay, beta, wn, 16, 48, 128)
+    S2, q2, o2 = R.gdn_step(S, qkv, z, decay, beta, wn)
+    assert rel_err(S1, S2) < 1e-5
+    assert rel_err(q1, q2) < 1e-6
+    assert rel_err(o1, o2) < 1e-5
+
+
+def test_gdn_step_closed_form(oracle):
+    """f64 restatement of the delta rule on a tiny head: S'=gS + k(beta(v - (gS)^T k))^T."""
+    g = np.random.default_rng(8)
+    nkh, nvh, dk = 2, 4, 8
+    S = g.standard_normal((nvh, dk, dk)).astype(np.float32)
+    qkv = g.standard_normal((2 * nkh + nvh) * dk).astype(np.float32)
+    z = g.standard_normal(nvh * dk).astype(np.float32)
+    decay = np.log(g.uniform(0.3, 1, nvh)).astype(np.float32)
+    beta = g.uniform(0, 1, nvh).astype(np.float32)
+    wn = g.uniform(0.5, 1.5, dk).astype(np.float32)
+    S1, _, out = oracle.gdn_step(S, qkv, z, decay, beta, wn, nkh, nvh, dk)
+    q = qkv[:nkh * dk].reshape(nkh, dk).astype(np.float64)
+    k = qkv[nkh * dk:2 * nkh * dk].reshape(nkh, dk).astype(np.float64)
+    v = qkv[2 * nkh * dk:].reshape(nvh, dk).astype(np.float64)
+    q /= np.sqrt((q * q).sum(1, keepdims=True) + 1e-6)
+    k /= np.sqrt((k * k).sum(1, keepdims=True) + 1e-6)
+    for hv in range(nvh):
+        hk = hv % nkh
+        Sh = S[hv].astype(np.float64) * np.exp(float(decay[hv]))
+        delta = float(beta[hv]) * (v[hv] - Sh.T @ k[hk])
+        Sh = Sh + np.outer(k[hk], delta)
+        assert np.allclose(S1[hv], Sh, rtol=1e-5, atol=1e-5)
+        o = (Sh.T @ q[hk]) / np.sqrt(dk)
+        zz = z[hv * dk:(hv + 1) * dk].astype(np.float64)
+        o = wn * o / np.sqrt(np.mean(o * o) + 1e-6) * zz / (1 + np.exp(-zz))
+        assert np.allclose(out[hv * dk:(hv + 1) * dk], o, rtol=1e-4, atol=1e-5)
+
+
+def test_gdn_identity_gates(oracle):
+    """decay = 0 (g = 1) and beta = 0 leave the state unchanged."""
+    S, qkv, z, decay, beta, wn = _gdn_inputs(9)
+    S1, _, _ = oracle.gdn_step(S, qkv, z, np.zeros(48, np.float32), np.zeros(48, np.float32), wn, 16, 48, 128)
+    assert np.array_equal(S1, S)
+
+
+# ---------------------------------------------------------------- argmax / walk / drafter
+def test_argmax_semantics(oracle, ref):
+    g = np.random.default_rng(10)
+    V = 151936
+    for t in range(20):
+        lg = g.standard_normal(V).astype(np.float32)
+        if t % 4 == 1:
+            lg[g.integers(0, V, 5)] = lg.max()                   # ties: first index wins
+        if t % 4 == 2:
+            lg[g.integers(1, V, 50)] = np.nan                     # NaN never wins
+        if t % 4 == 3:
+            lg[:] = -np.inf
+        want_np = int(np.nanargmax(lg)) if not np.all(np.isneginf(lg)) else 0
+        a = oracle.argmax(lg)
+        assert a == ref.argmax(lg) == want_np
+    lg = g.standard_normal(1000).astype(np.float32)
+    lg[0] = np.nan                                                # NaN at 0: nothing beats it
+    assert oracle.argmax(lg) == ref.argmax(lg) == 0
+
+
+def test_walk_vs_reference(oracle, ref):
+    g = np.random.default_rng(11)
+    V = 151936
+    for E in (0, 1, 3, 7, 15):
+        logits = g.standard_normal((E + 1, V)).astype(np.float32)
+        am = logits.argmax(1)
+        for trial in range(4):
+            d = np.where(g.random(E) < 0.7, am[:E], g.integers(0, V, E)).astype(np.int32)
+            assert oracle.walk(logits, d) == ref.walk(logits, d)
+
+
+def test_ngram_draft_vs_reference(oracle, ref):
+    g = np.random.default_rng(12)
+    for t in range(30):
+        base = g.integers(0, 50, g.integers(20, 80))
+        hist = np.concatenate([base, base[: g.integers(5, len(base))], g.integers(0, 50, 3), base[:20]])
+        hist = hist.astype(np.int32)
+        for n_key in (2, 4, 16):
+            for max_d in (1, 7, 15):
+                assert np.array_equal(oracle.ngram_draft(hist, n_key, max_d), ref.ngram_draft(hist, n_key, max_d))

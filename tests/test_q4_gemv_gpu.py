@@ -1,0 +1,196 @@
+"""Parity of the HIP Q4_0 batched GEMV (libcwen_gpu.so through its C ABI)
+against the oracle, plus the block-invariance property the speculative path
+relies on.
+
+Tolerance (stated): rel_err = max|y - y_oracle| / max|y_oracle| <= 1e-3 on
+f32 outputs.  The kernel's only rounding beyond f32 accumulation is the f16
+activation operand (2^-11 relative per element), which puts the expected
+error near 1e-4.
+"""
+import numpy as np
+import pytest
+
+from cwen_amd import synth
+from util import rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+T_Q4_0, T_RS, T_RSI = 2, 101, 102
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from cwen_amd import gpu
+    ctx = gpu.Context(0)
+    yield torch, gpu, ctx
+    torch.cuda.synchronize()
+
+
+def _run(env, W, X, side=0, mode="single"):
+    torch, gpu, ctx = env
+    B = X.shape[0]
+    Xd = torch.from_numpy(np.ascontiguousarray(X)).cuda()
+    if mode == "single":
+        Y = torch.full((B, W.M), float("nan"), device="cuda")
+        gpu.gemvb(ctx, W, Xd, Y, B, side=side)
+        torch.cuda.synchronize()
+        return Y.cpu().numpy()
+    if mode == "pair":
+        YA = torch.full((B, W.M), float("nan"), device="cuda")
+        YB = torch.full((B, W.M), float("nan"), device="cuda")
+        gpu.gemvb_pair(ctx, W, Xd, YA, YB, B)
+        torch.cuda.synchronize()
+        return YA.cpu().numpy(), YB.cpu().numpy()
+    H = torch.full((B, W.M), float("nan"), device="cuda")
+    gpu.gemvb_swiglu(ctx, W, Xd, H, B)
+    torch.cuda.synchronize()
+    return H.cpu().numpy()
+
+
+SHAPES = [(16, 128), (20, 256), (100, 512), (48, 5120), (1024, 1024), (5120, 5120)]
+
+
+@pytest.mark.parametrize("M,K", SHAPES)
+def test_rs_parity(env, oracle, M, K):
+    torch, gpu, ctx = env
+    qs, sc = synth.q4_rs(101, M, K)
+    W = gpu.Weight(ctx, T_RS, qs, sc, K, M)
+    for B in (1, 3, 8, 16):
+        X = synth.activations(101, B, K, key=B)
+        got = _run(env, W, X)
+        want = oracle.gemvb(T_RS, qs, sc, K, M, X)
+        assert np.isfinite(got).all()
+        assert rel_err(got, want) <= TOL, (M, K, B, rel_err(got, want))
+
+
+@pytest.mark.parametrize("M,K", [(64, 256), (5120, 5120)])
+def test_gguf_parity(env, oracle, M, K):
+    torch, gpu, ctx = env
+    blk = synth.q4_gguf(102, M, K)
+    W = gpu.Weight(ctx, T_Q4_0, blk, None, K, M)
+    for B in (1, 8):
+        X = synth.activations(102, B, K, key=B)
+        got = _run(env, W, X)
+        assert rel_err(got, oracle.gemvb(T_Q4_0, blk, None, K, M, X)) <= TOL
+
+
+@pytest.mark.parametrize("M,K", [(40, 256), (1000, 2048)])
+def test_rsi_single_pair_swiglu(env, oracle, M, K):
+    torch, gpu, ctx = env
+    qs, sc = synth.q4_rsi(103, M, K)
+    W = gpu.Weight(ctx, T_RSI, qs, sc, K, M)
+    for B in (1, 5, 16):
+        X = synth.activations(103, B, K, key=B)
+        wa = oracle.gemvb(T_RSI, qs, sc, K, M, X, side=0)
+        wb = oracle.gemvb(T_RSI, qs, sc, K, M, X, side=1)
+        assert rel_err(_run(env, W, X, side=0), wa) <= TOL
+        assert rel_err(_run(env, W, X, side=1), wb) <= TOL
+        ya, yb = _run(env, W, X, mode="pair")
+        assert rel_err(ya, wa) <= TOL and rel_err(yb, wb) <= TOL
+        h = _run(env, W, X, mode="swiglu")
+        assert rel_err(h, oracle.silu_mul(wa, wb)) <= TOL
+
+
+def test_block_invariance_bitwise(env):
+    """A column computed inside a block of B is bit-identical to the same
+    column computed alone (B=1) and inside a different block size."""
+    torch, gpu, ctx = env
+    M, K = 5120, 17408
+    qs, sc = synth.q4_rs(104, M, K)
+    W = gpu.Weight(ctx, T_RS, qs, sc, K, M)
+    X = synth.activations(104, 16, K)
+    full = _run(env, W, X)
+    for b in (0, 5, 15):
+        one = _run(env, W, X[b:b + 1])
+        assert np.array_equal(one[0].view(np.uint32), full[b].view(np.uint32))
+    eight = _run(env, W, X[3:11])
+    assert np.array_equal(eight.view(np.uint32), full[3:11].view(np.uint32))
+
+
+def test_pair_invariance_bitwise(env):
+    torch, gpu, ctx = env
+    M, K = 2048, 5120
+    qs, sc = synth.q4_rsi(105, M, K)
+    W = gpu.Weight(ctx, T_RSI, qs, sc, K, M)
+    X = synth.activations(105, 16, K)
+    h16 = _run(env, W, X, mode="swiglu")
+    h1 = _run(env, W, X[7:8], mode="swiglu")
+    assert np.array_equal(h1[0].view(np.uint32), h16[7].view(np.uint32))
+    ya, _ = _run(env, W, X, mode="pair")
+    assert np.array_equal(_run(env, W, X, side=0).view(np.uint32), ya.view(np.uint32))
+
+
+def test_repeat_deterministic(env):
+    torch, gpu, ctx = env
+    M, K = 5120, 17408
+    qs, sc = synth.q4_rs(106, M, K)
+    W = gpu.Weight(ctx, T_RS, qs, sc, K, M)
+    X = synth.activations(106, 8, K)
+    a = _run(env, W, X)
+    for _ in range(3):
+        assert np.array_equal(_run(env, W, X).view(np.uint32), a.view(np.uint32))
+
+
+def test_strided_activations_and_outputs(env, oracle):
+    torch, gpu, ctx = env
+    M, K, B = 96, 512, 4
+    qs, sc = synth.q4_rs(107, M, K)
+    W = gpu.Weight(ctx, T_RS, qs, sc, K, M)
+    X = synth.activations(107, B, K)
+    Xpad = np.zeros((B, K + 64), np.float32)
+    Xpad[:, :K] = X
+    Xd = torch.from_numpy(Xpad).cuda()
+    Y = torch.full((B, M + 32), 7.0, device="cuda")
+    gpu.gemvb(ctx, W, Xd, Y, B, xs=K + 64, ys=M + 32)
+    torch.cuda.synchronize()
+    Yh = Y.cpu().numpy()
+    assert rel_err(Yh[:, :M], oracle.gemvb(T_RS, qs, sc, K, M, X)) <= TOL
+    assert np.all(Yh[:, M:] == 7.0)  # nothing written past M
+
+
+def test_argument_errors(env):
+    torch, gpu, ctx = env
+    M, K = 32, 256
+    qs, sc = synth.q4_rs(108, M, K)
+    W = gpu.Weight(ctx, T_RS, qs, sc, K, M)
+    X = torch.zeros(17, K, device="cuda")
+    Y = torch.zeros(17, M, device="cuda")
+    for B in (0, 17):
+        with pytest.raises(gpu.CwenError):
+            gpu.gemvb(ctx, W, X, Y, B)
+    with pytest.raises(gpu.CwenError):
+        gpu.gemvb(ctx, W, X.data_ptr() + 4, Y, 1)          # misaligned activations
+    with pytest.raises(gpu.CwenError):
+        gpu.gemvb(ctx, W, X, Y, 1, side=1)                 # RS has one side
+    with pytest.raises(gpu.CwenError):
+        gpu.gemvb_swiglu(ctx, W, X, Y, 1)                  # needs a pair
+    qs2, sc2 = synth.q4_rs(108, M, 96)
+    with pytest.raises(gpu.CwenError):
+        gpu.Weight(ctx, T_RS, qs2, sc2, 96, M)             # K not a multiple of 128
+    with pytest.raises(gpu.CwenError):
+        gpu.Weight(ctx, 3, qs, sc, K, M)                   # Q4_1 is not a supported type
+
+
+@pytest.mark.slow
+def test_ffn_block_full_size(env, oracle):
+    """The FFN workload at full size, B=8: RSI gate/up + SwiGLU, then RS down."""
+    torch, gpu, ctx = env
+    H, I, B = 5120, 17408, 8
+    gq, gs = synth.q4_rsi(0, I, H)
+    dq, ds = synth.q4_rs(0, H, I, key=1)
+    X = synth.activations(0, B, H)
+    Wgu = gpu.Weight(ctx, T_RSI, gq, gs, H, I)
+    Wd = gpu.Weight(ctx, T_RS, dq, ds, I, H)
+    Xd = torch.from_numpy(X).cuda()
+    Hd = torch.empty(B, I, device="cuda")
+    Yd = torch.empty(B, H, device="cuda")
+    gpu.gemvb_swiglu(ctx, Wgu, Xd, Hd, B)
+    gpu.gemvb(ctx, Wd, Hd, Yd, B)
+    torch.cuda.synchronize()
+    h_want = oracle.silu_mul(oracle.gemvb(T_RSI, gq, gs, H, I, X, 0), oracle.gemvb(T_RSI, gq, gs, H, I, X, 1))
+    assert rel_err(Hd.cpu().numpy(), h_want) <= TOL
+    y_want = oracle.gemvb(T_RS, dq, ds, I, H, h_want)
+    assert rel_err(Yd.cpu().numpy(), y_want) <= TOL
