@@ -26,6 +26,9 @@ HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
+    # MFMA results in VGPRs: the epilogue reads them with VALU ops directly
+    # instead of a v_accvgpr_read per element.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{ROOT / 'include'}", f"-I{CSRC}",
 ]
 

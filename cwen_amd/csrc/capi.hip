@@ -5,9 +5,6 @@
 
 namespace {
 
-constexpr size_t kPartialFloats = (size_t)16 << 20;  // 64 MiB of split-K partials
-constexpr int kCounters = 1 << 16;
-
 int env_int(const char *name, int dflt, int lo, int hi) {
   const char *s = getenv(name);
   if (!s || !*s) return dflt;
@@ -18,6 +15,8 @@ int env_int(const char *name, int dflt, int lo, int hi) {
 }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+constexpr size_t kScratchHalves = (size_t)CWEN_BMAX * CWEN_KMAX;
 
 }  // namespace
 
@@ -35,24 +34,15 @@ int cwen_ctx_create(int device, cwen_ctx **out) {
   cwen_ctx *c = (cwen_ctx *)calloc(1, sizeof(cwen_ctx));
   if (!c) return CWEN_ENOMEM;
   c->device = device;
-  c->wg_target = env_int("CWEN_GEMV_WG_TARGET", 512, 64, 65536);
-  if (hipMalloc((void **)&c->partials, kPartialFloats * sizeof(float)) != hipSuccess) {
+  c->wg_target = env_int("CWEN_GEMV_WG_TARGET", 2048, 64, 65536);
+  if (hipMalloc((void **)&c->xh, kScratchHalves * 2) != hipSuccess) {
     free(c);
     return CWEN_ENOMEM;
   }
-  if (hipMalloc((void **)&c->counters, kCounters * sizeof(int)) != hipSuccess) {
-    (void)hipFree(c->partials);
+  if (hipMalloc((void **)&c->hh, kScratchHalves * 2) != hipSuccess) {
+    (void)hipFree(c->xh);
     free(c);
     return CWEN_ENOMEM;
-  }
-  c->partials_floats = kPartialFloats;
-  c->ncounters = kCounters;
-  if (hipMemset(c->counters, 0, kCounters * sizeof(int)) != hipSuccess ||
-      hipDeviceSynchronize() != hipSuccess) {
-    (void)hipFree(c->counters);
-    (void)hipFree(c->partials);
-    free(c);
-    return CWEN_EHIP;
   }
   *out = c;
   return CWEN_OK;
@@ -62,8 +52,8 @@ int cwen_ctx_destroy(cwen_ctx *ctx) {
   if (!ctx) return CWEN_EINVAL;
   (void)hipSetDevice(ctx->device);
   (void)hipDeviceSynchronize();
-  (void)hipFree(ctx->partials);
-  (void)hipFree(ctx->counters);
+  (void)hipFree(ctx->xh);
+  (void)hipFree(ctx->hh);
   free(ctx);
   return CWEN_OK;
 }
@@ -73,7 +63,7 @@ int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *sc
   if (!ctx || !data || !out || ne0 <= 0 || ne1 <= 0) return CWEN_EINVAL;
   *out = nullptr;
   if (type != CWEN_T_Q4_0 && type != CWEN_T_Q4_0RS && type != CWEN_T_Q4_0RSI) return CWEN_ETYPE;
-  if (ne0 % Q4_TILE_K) return CWEN_EINVAL;
+  if (ne0 % Q4_K_ALIGN || ne0 > CWEN_KMAX) return CWEN_EINVAL;
   const bool split_scales = (type != CWEN_T_Q4_0);
   if (split_scales && !scales) return CWEN_EINVAL;
   CWEN_HIP_TRY(hipSetDevice(ctx->device));
@@ -95,6 +85,10 @@ int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *sc
   w->nrg = (ne1 + Q4_ROWS - 1) / Q4_ROWS;
   w->nkt = ne0 / Q4_TILE_K;
   w->bytes = (size_t)w->nrg * w->nkt * nside * Q4_TILE_BYTES;
+  if (w->bytes >= ((size_t)1 << 32)) {  // kernels address weights with 32-bit buffer offsets
+    free(w);
+    return CWEN_EINVAL;
+  }
   w->src_bytes = qbytes + sbytes;
   q4_choose_split(ctx, w);
 
@@ -153,35 +147,92 @@ static int check_out(const float *Y, int ys, int M, int B) {
   if (!Y || (B > 1 && ys < M) || ys < 0) return CWEN_EINVAL;
   return CWEN_OK;
 }
+static int check_w(const cwen_ctx *ctx, const cwen_weight *W) {
+  return (!ctx || !W || W->ctx != ctx) ? CWEN_EINVAL : CWEN_OK;
+}
+
+int cwen_act_to_f16(cwen_ctx *ctx, const float *X, int xs, void *Xh, int K, int B, void *stream) {
+  if (!ctx || !Xh || !aligned16(Xh) || K <= 0 || (K & 7)) return CWEN_EINVAL;
+  int rc = check_act(X, xs, K, B);
+  if (rc) return rc;
+  return act_to_f16(X, xs, (_Float16 *)Xh, K, B, (hipStream_t)stream);
+}
 
 int cwen_gemvb(cwen_ctx *ctx, const cwen_weight *W, int side, const float *X, int xs, float *Y,
                int ys, int B, void *stream) {
-  if (!ctx || !W || W->ctx != ctx) return CWEN_EINVAL;
-  if (side < 0 || side >= W->nside) return CWEN_EINVAL;
-  int rc = check_act(X, xs, W->ne0, B);
+  int rc = check_w(ctx, W);
   if (rc) return rc;
-  if ((rc = check_out(Y, ys, W->ne1, B))) return rc;
-  return q4_gemv_launch(ctx, W, 1, side, Q4_EPI_STORE, X, xs, Y, nullptr, ys, B,
-                        (hipStream_t)stream);
+  if (side < 0 || side >= W->nside) return CWEN_EINVAL;
+  if ((rc = check_act(X, xs, W->ne0, B)) || (rc = check_out(Y, ys, W->ne1, B))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
+  Q4Out o = {Y, nullptr, nullptr, ys, 0};
+  return q4_gemv_launch(W, 1, side, Q4_EPI_STORE, ctx->xh, o, B, st);
 }
 
 int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *YA,
                     float *YB, int ys, int B, void *stream) {
-  if (!ctx || !W || W->ctx != ctx || W->nside != 2) return CWEN_EINVAL;
-  int rc = check_act(X, xs, W->ne0, B);
+  int rc = check_w(ctx, W);
   if (rc) return rc;
-  if ((rc = check_out(YA, ys, W->ne1, B)) || (rc = check_out(YB, ys, W->ne1, B))) return rc;
-  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_STORE, X, xs, YA, YB, ys, B, (hipStream_t)stream);
+  if (W->nside != 2) return CWEN_EINVAL;
+  if ((rc = check_act(X, xs, W->ne0, B)) || (rc = check_out(YA, ys, W->ne1, B)) ||
+      (rc = check_out(YB, ys, W->ne1, B)))
+    return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
+  Q4Out o = {YA, YB, nullptr, ys, 0};
+  return q4_gemv_launch(W, 2, 0, Q4_EPI_PAIR, ctx->xh, o, B, st);
 }
 
 int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *H,
                       int hs, int B, void *stream) {
-  if (!ctx || !W || W->ctx != ctx || W->nside != 2) return CWEN_EINVAL;
-  int rc = check_act(X, xs, W->ne0, B);
+  int rc = check_w(ctx, W);
   if (rc) return rc;
-  if ((rc = check_out(H, hs, W->ne1, B))) return rc;
-  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_SWIGLU, X, xs, H, nullptr, hs, B,
-                        (hipStream_t)stream);
+  if (W->nside != 2) return CWEN_EINVAL;
+  if ((rc = check_act(X, xs, W->ne0, B)) || (rc = check_out(H, hs, W->ne1, B))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
+  Q4Out o = {H, nullptr, nullptr, hs, 0};
+  return q4_gemv_launch(W, 2, 0, Q4_EPI_SWIGLU, ctx->xh, o, B, st);
+}
+
+int cwen_gemvb_f16(cwen_ctx *ctx, const cwen_weight *W, int side, const void *Xh, float *Y,
+                   int ys, void *Yh, int accumulate, int B, void *stream) {
+  int rc = check_w(ctx, W);
+  if (rc) return rc;
+  if (side < 0 || side >= W->nside || !Xh || !aligned16(Xh) || B < 1 || B > CWEN_BMAX)
+    return CWEN_EINVAL;
+  if (!Y && !Yh) return CWEN_EINVAL;
+  if (Y && (rc = check_out(Y, ys, W->ne1, B))) return rc;
+  if (Yh && (W->ne1 & 7)) return CWEN_EINVAL;
+  Q4Out o = {Y, nullptr, (_Float16 *)Yh, ys, accumulate ? 1 : 0};
+  return q4_gemv_launch(W, 1, side, Q4_EPI_STORE, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
+}
+
+int cwen_gemvb_swiglu_f16(cwen_ctx *ctx, const cwen_weight *W, const void *Xh, float *H, int hs,
+                          void *Hh, int B, void *stream) {
+  int rc = check_w(ctx, W);
+  if (rc) return rc;
+  if (W->nside != 2 || !Xh || !aligned16(Xh) || B < 1 || B > CWEN_BMAX) return CWEN_EINVAL;
+  if (!H && !Hh) return CWEN_EINVAL;
+  if (H && (rc = check_out(H, hs, W->ne1, B))) return rc;
+  Q4Out o = {H, nullptr, (_Float16 *)Hh, hs, 0};
+  return q4_gemv_launch(W, 2, 0, Q4_EPI_SWIGLU, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
+}
+
+int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd, const float *X,
+                   int xs, float *Y, int ys, int B, void *stream) {
+  int rc;
+  if ((rc = check_w(ctx, Wgu)) || (rc = check_w(ctx, Wd))) return rc;
+  if (Wgu->nside != 2 || Wd->nside != 1 || Wd->ne0 != Wgu->ne1 || Wd->ne1 != Wgu->ne0)
+    return CWEN_EINVAL;
+  if ((rc = check_act(X, xs, Wgu->ne0, B)) || (rc = check_out(Y, ys, Wd->ne1, B))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = act_to_f16(X, xs, ctx->xh, Wgu->ne0, B, st))) return rc;
+  Q4Out o1 = {nullptr, nullptr, ctx->hh, 0, 0};
+  if ((rc = q4_gemv_launch(Wgu, 2, 0, Q4_EPI_SWIGLU, ctx->xh, o1, B, st))) return rc;
+  Q4Out o2 = {Y, nullptr, nullptr, ys, 1};
+  return q4_gemv_launch(Wd, 1, 0, Q4_EPI_STORE, ctx->hh, o2, B, st);
 }
 
 }  // extern "C"

@@ -16,14 +16,14 @@ constexpr int Q4_TILE_QS = 1024;
 constexpr int Q4_TILE_BYTES = 1152;
 constexpr int Q4_TILE_K = 128;
 constexpr int Q4_ROWS = 16;
+// K must be a multiple of one tile.
+constexpr int Q4_K_ALIGN = Q4_TILE_K;
 
 struct cwen_ctx {
   int device;
-  float *partials;          // split-K partial sums
-  size_t partials_floats;
-  int *counters;            // per row-tile arrival counters, kept at zero between calls
-  int ncounters;
-  int wg_target;            // workgroups a split-K launch aims for
+  int wg_target;            // workgroups a GEMV launch aims for
+  _Float16 *xh;             // f16 activation scratch [BMAX][KMAX]
+  _Float16 *hh;             // second f16 scratch (FFN hidden) [BMAX][KMAX]
 };
 
 struct cwen_weight {
@@ -35,7 +35,7 @@ struct cwen_weight {
   uint8_t *dev;             // tiled device data
   size_t bytes;             // device bytes of the tiled data
   size_t src_bytes;         // bytes of the reference layout (qs + scales)
-  int split, tps;           // split-K factor and K tiles per split (shape-only)
+  int split, tps;           // waves per workgroup and K tiles per wave (shape-only)
 };
 
 #define CWEN_HIP_TRY(expr)                                   \
@@ -44,10 +44,33 @@ struct cwen_weight {
     if (_e != hipSuccess) return CWEN_EHIP;                  \
   } while (0)
 
-// q4_gemv.hip
+// ------------------------------------------------------------ device helpers
+// gfx9 raw buffer resource: 32-bit offsets; loads past num_records return
+// zero without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+
+// run.c:378-384 silu_one: x * (1 / (1 + exp(-x)))
+__device__ __forceinline__ float silu_f(float x) { return x * (1.f / (1.f + expf(-x))); }
+
+// ------------------------------------------------------------ q4_gemv.hip
+enum { Q4_EPI_STORE = 0, Q4_EPI_PAIR = 1, Q4_EPI_SWIGLU = 2 };
+struct Q4Out {
+  float *y;          // f32 result (side A, or silu(A)*B) [c*ys + row], nullable
+  float *y1;         // f32 side B of a pair [c*ys + row] (PAIR only)
+  _Float16 *yh;      // f16 copy of the (accumulated) result [c*M + row], nullable
+  int ys;
+  int accumulate;    // y += result
+};
 int q4_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStream_t st);
 void q4_choose_split(const cwen_ctx *ctx, cwen_weight *w);
-enum { Q4_EPI_STORE = 0, Q4_EPI_SWIGLU = 1 };
-int q4_gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
-                   const float *X, int xs, float *Y0, float *Y1, int ys, int B,
-                   hipStream_t st);
+int q4_gemv_launch(const cwen_weight *w, int nsides, int side0, int epi, const _Float16 *xh,
+                   const Q4Out &out, int B, hipStream_t st);
+int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st);

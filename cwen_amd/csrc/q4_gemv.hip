@@ -11,32 +11,57 @@
 //    pair; the block's f16 scale is applied in f32 after the MFMA, so the
 //    only rounding beyond f32 accumulation is the f16 activation operand.
 //  * v_mfma_f32_16x16x32_f16: A = activations (16 columns x 32 K, one Q4
-//    block), B = weights (32 K x 16 rows).  Columns >= B are zero operands,
-//    so one kernel serves B = 1..16 and each column's arithmetic is the same
-//    whatever B is (block verify == serial decode, bit for bit).
-//  * A workgroup of 4 waves owns 4 row groups (64 rows) and one K range; the
-//    activation chunk is staged once in LDS (f32 -> f16) and shared by all
-//    4 waves.  Long K ranges are split across workgroups; the last
-//    workgroup of a row tile sums the partials in fixed split order, so the
-//    result is deterministic.
+//    block), B = weights (32 K x 16 rows).  Activations are f16 row-major
+//    [B][K]; a lane's A operand is 16 contiguous bytes of one column, read
+//    straight from L2.  Columns >= B lie past the buffer range and load as
+//    zeros, so one kernel serves B = 1..16 and a column's arithmetic never
+//    depends on B (block verify == serial decode, bit for bit).
+//  * One workgroup owns one 16-row group (both sides of an interleaved pair)
+//    and all of K; its waves split K and the partial sums are reduced through
+//    LDS in wave order.  There is no cross-workgroup synchronisation, and the
+//    reduction tree depends on the shape only.
+//  * Each wave keeps a ring of PF tiles in flight (weights + activation
+//    operands) with unconditional, fixed-order buffer loads, so the in-order
+//    load counter only waits for the tile being consumed.
 #include "cwen_internal.h"
 
 namespace {
 
-constexpr int WAVES = 4;
-constexpr int CH = 4;  // K tiles per LDS chunk == weight prefetch depth
+constexpr int PF = 4;  // tiles in flight per wave
 
 // Nibble position holding operand element e (see unpack8): unpack8 yields
 // elements in nibble order 0,4,1,5,2,6,3,7.
 __constant__ int kNibPos[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 
+// (q & mask) | magic in one VOP3 op.  gfx9 VOP3 takes no literal and reads at
+// most one scalar, so the mask comes from an SGPR and the magic from a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t q, uint32_t mask_s, uint32_t magic_v) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(q), "s"(mask_s), "v"(magic_v));
+  return r;
+}
+
 // 8 nibbles -> 8 exact f16 values (n - 8), element e taken from nibble kNibPos[e].
-__device__ __forceinline__ half8_t unpack8(uint32_t q) {
+struct Unpack {
+  uint32_t lo, hi;   // SGPR masks 0x000F000F, 0x00F000F0
+  uint32_t magic;    // VGPR 0x64006400
+};
+// Materialise the constants once, opaque to the compiler, so the loop does
+// not rebuild them per use.
+__device__ __forceinline__ Unpack unpack_consts() {
+  Unpack u;
+  asm volatile("s_mov_b32 %0, 0x000f000f" : "=s"(u.lo));
+  asm volatile("s_mov_b32 %0, 0x00f000f0" : "=s"(u.hi));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(u.magic));
+  return u;
+}
+
+__device__ __forceinline__ half8_t unpack8(uint32_t q, const Unpack &u) {
   const uint32_t q2 = q >> 8;
-  const uint32_t t0 = (q & 0x000F000Fu) | 0x64006400u;   // 1024 + n0, 1024 + n4
-  const uint32_t t1 = (q & 0x00F000F0u) | 0x64006400u;   // 1024 + 16 n1, 1024 + 16 n5
-  const uint32_t t2 = (q2 & 0x000F000Fu) | 0x64006400u;  // 1024 + n2, 1024 + n6
-  const uint32_t t3 = (q2 & 0x00F000F0u) | 0x64006400u;  // 1024 + 16 n3, 1024 + 16 n7
+  const uint32_t t0 = and_or(q, u.lo, u.magic);    // 1024 + n0, 1024 + n4
+  const uint32_t t1 = and_or(q, u.hi, u.magic);    // 1024 + 16 n1, 1024 + 16 n5
+  const uint32_t t2 = and_or(q2, u.lo, u.magic);   // 1024 + n2, 1024 + n6
+  const uint32_t t3 = and_or(q2, u.hi, u.magic);   // 1024 + 16 n3, 1024 + 16 n7
   const half2_t k1032 = {(_Float16)1032.0f, (_Float16)1032.0f};
   const half2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
   const half2_t k72 = {(_Float16)-72.0f, (_Float16)-72.0f};
@@ -50,172 +75,143 @@ __device__ __forceinline__ half8_t unpack8(uint32_t q) {
   return r;
 }
 
-__device__ __forceinline__ float h2f(uint32_t bits16) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
-}
-
-__device__ __forceinline__ float silu_f(float x) { return x * (1.f / (1.f + expf(-x))); }
-
 struct Q4Params {
-  const uint8_t *w;   // tiled weights
-  int nsw;            // sides stored per tile position (1 or 2)
-  int side0;          // first side computed
-  int M, nrg, nkt;
-  const float *X;
-  int xs, B;
-  float *Y0, *Y1;
-  int ys;
-  int S, tps;         // split-K
-  float *part;
-  int *cnt;
+  const uint8_t *w;    // tiled weights
+  uint32_t wbytes;     // bytes of the tiled weights (buffer range)
+  int nsw;             // sides stored per tile position (1 or 2)
+  int side0;           // first side computed
+  int M, nkt;
+  const _Float16 *xh;  // activations f16 [B][K]
+  uint32_t xbytes;     // B*K*2 (buffer range: columns >= B read as zero)
+  int B;
+  Q4Out out;
 };
 
-template <int NS, int EPI>
-__global__ __launch_bounds__(256) void q4_gemv_kernel(Q4Params p) {
-  __shared__ uint4 act[CH * 4 * 64];  // [tile][block][lane] f16 x 8
-  __shared__ int s_last;
+template <int NS, int EPI, int W>
+__global__ __launch_bounds__(64 * W) void q4_gemv_kernel(Q4Params p) {
+  __shared__ floatx4_t red[W][NS][64];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // Wave index as a scalar: the K range and the loop trip count are then
+  // provably wave-uniform, which keeps the loop's load-counter waits exact.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
-  const int rt = blockIdx.x / p.S;
-  const int sp = blockIdx.x - rt * p.S;
-  const int rg = rt * WAVES + wave;
-  const bool rows_on = rg < p.nrg;
-  const int kt0 = sp * p.tps;
-  const int nt = min(p.nkt, kt0 + p.tps) - kt0;
-  const bool act_on = n < p.B;
+  const int rg = blockIdx.x;
+  const int t0 = (wave * p.nkt) / W;
+  const int nt = ((wave + 1) * p.nkt) / W - t0;  // >= 1 (host keeps W <= nkt)
 
-  const size_t tstride = (size_t)p.nsw * Q4_TILE_BYTES;
-  const uint8_t *wb[NS];
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.wbytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.xh, p.xbytes);
+
+  const uint32_t tstride = (uint32_t)p.nsw * Q4_TILE_BYTES;
+  uint32_t wofs[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s)
-    wb[s] = p.w + (((size_t)(rows_on ? rg : 0) * p.nkt + kt0) * p.nsw + p.side0 + s) * Q4_TILE_BYTES;
+    wofs[s] = (((uint32_t)rg * p.nkt + t0) * p.nsw + p.side0 + s) * Q4_TILE_BYTES;
+  const uint32_t lq = lane * 16, ls = Q4_TILE_QS + n * 8;
+  // A operand of block m of tile t: column n, K run 32m + 8g .. +7.
+  const uint32_t xlane = ((uint32_t)n * (uint32_t)(p.nkt * Q4_TILE_K) + t0 * Q4_TILE_K + g * 8) * 2;
 
-  uint4 wq[CH][NS];
-  uint2 wsc[CH][NS];
+  uint4 wq[PF][NS];
+  uint2 wsc[PF][NS];
+  uint4 xa[PF][4];
 #pragma unroll
-  for (int i = 0; i < CH; ++i)
+  for (int i = 0; i < PF; ++i) {
+    const uint32_t t = (uint32_t)(i < nt ? i : nt - 1);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      if (rows_on && i < nt) {
-        const uint8_t *t = wb[s] + (size_t)i * tstride;
-        wq[i][s] = *(const uint4 *)(t + lane * 16);
-        wsc[i][s] = *(const uint2 *)(t + Q4_TILE_QS + n * 8);
-      } else {
-        wq[i][s] = make_uint4(0, 0, 0, 0);
-        wsc[i][s] = make_uint2(0, 0);
-      }
+      wq[i][s] = bload16(wr, wofs[s] + t * tstride + lq);
+      wsc[i][s] = bload8(wr, wofs[s] + t * tstride + ls);
     }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xa[i][m] = bload16(xr, xlane + t * (Q4_TILE_K * 2) + m * 64);
+    // Issue the ring in slot order: the loop consumes slot 0 first.
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   floatx4_t acc[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) acc[s] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
   const floatx4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 
-  for (int ch0 = 0; ch0 < nt; ch0 += CH) {
-    const int chn = min(CH, nt - ch0);
-    __syncthreads();
-    // Stage X[b][k] for this chunk as f16 MFMA A-operands: slot (tile, block, g, c).
-    {
-      const int nslot = chn * 16 * p.B;
-      for (int i = tid; i < nslot; i += 256) {
-        const int gg = i & 3, m = (i >> 2) & 3;
-        const int rest = i >> 4;
-        const int tt = rest % chn, c = rest / chn;
-        const int k0 = ((kt0 + ch0 + tt) * 4 + m) * 32 + gg * 8;
-        const float4 *src = (const float4 *)(p.X + (size_t)c * p.xs + k0);
-        const float4 v0 = src[0], v1 = src[1];
-        half8_t h;
-        h[0] = (_Float16)v0.x; h[1] = (_Float16)v0.y; h[2] = (_Float16)v0.z; h[3] = (_Float16)v0.w;
-        h[4] = (_Float16)v1.x; h[5] = (_Float16)v1.y; h[6] = (_Float16)v1.z; h[7] = (_Float16)v1.w;
-        act[(tt * 4 + m) * 64 + gg * 16 + c] = __builtin_bit_cast(uint4, h);
-      }
-    }
-    __syncthreads();
-    if (!rows_on) continue;
+  const Unpack uc = unpack_consts();
+
+  for (int tb = 0; tb < nt; tb += PF) {
 #pragma unroll
-    for (int tt = 0; tt < CH; ++tt) {
-      if (tt < chn) {
-        uint4 q[NS];
-        uint2 sc[NS];
+    for (int j = 0; j < PF; ++j) {
+      // Ring overrun past this wave's range (last round only): loads still
+      // issue (clamped) to keep the counter schedule fixed; compute is skipped.
+      if (tb + j < nt) {
+        half8_t b[NS][4];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) { q[s] = wq[tt][s]; sc[s] = wsc[tt][s]; }
-        const int tn = ch0 + tt + CH;
-        if (tn < nt) {
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const uint8_t *t = wb[s] + (size_t)tn * tstride;
-            wq[tt][s] = *(const uint4 *)(t + lane * 16);
-            wsc[tt][s] = *(const uint2 *)(t + Q4_TILE_QS + n * 8);
-          }
-        }
-        half8_t a[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          if (act_on) a[m] = __builtin_bit_cast(half8_t, act[(tt * 4 + m) * 64 + lane]);
-          else a[m] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+        for (int s = 0; s < NS; ++s) {
+          b[s][0] = unpack8(wq[j][s].x, uc);
+          b[s][1] = unpack8(wq[j][s].y, uc);
+          b[s][2] = unpack8(wq[j][s].z, uc);
+          b[s][3] = unpack8(wq[j][s].w, uc);
         }
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          const uint32_t qd[4] = {q[s].x, q[s].y, q[s].z, q[s].w};
-          const float d[4] = {h2f(sc[s].x & 0xffffu), h2f(sc[s].x >> 16),
-                              h2f(sc[s].y & 0xffffu), h2f(sc[s].y >> 16)};
+          const half2_t d01 = __builtin_bit_cast(half2_t, wsc[j][s].x);
+          const half2_t d23 = __builtin_bit_cast(half2_t, wsc[j][s].y);
+          const float d[4] = {(float)d01[0], (float)d01[1], (float)d23[0], (float)d23[1]};
 #pragma unroll
           for (int m = 0; m < 4; ++m) {
-            const floatx4_t pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], unpack8(qd[m]), zero4, 0, 0, 0);
+            const floatx4_t pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(half8_t, xa[j][m]), b[s][m], zero4, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[s][r] = __builtin_fmaf(pm[r], d[m], acc[s][r]);
           }
         }
       }
-    }
-  }
-
-  // Split-K: publish partials; the last workgroup of this row tile reduces in split order.
-  if (p.S > 1) {
-    if (rows_on) {
+      // Refill this slot only after its registers are consumed, so the new
+      // loads can land in the same registers.
+      {
+        const int tn0 = tb + j + PF;
+        const uint32_t tn = (uint32_t)(tn0 < nt ? tn0 : nt - 1);
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        float *dst = p.part + ((((size_t)rg * p.S + sp) * NS + s) * 64 + lane) * 4;
-        *(floatx4_t *)dst = acc[s];
-      }
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&p.cnt[rt], 1) == p.S - 1);
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    if (rows_on) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        floatx4_t sum = *(volatile floatx4_t *)(p.part + ((((size_t)rg * p.S + 0) * NS + s) * 64 + lane) * 4);
-        for (int k = 1; k < p.S; ++k) {
-          const floatx4_t v =
-              *(volatile floatx4_t *)(p.part + ((((size_t)rg * p.S + k) * NS + s) * 64 + lane) * 4);
-          sum += v;
+        for (int s = 0; s < NS; ++s) {
+          wq[j][s] = bload16(wr, wofs[s] + tn * tstride + lq);
+          wsc[j][s] = bload8(wr, wofs[s] + tn * tstride + ls);
         }
-        acc[s] = sum;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) xa[j][m] = bload16(xr, xlane + tn * (Q4_TILE_K * 2) + m * 64);
       }
+      // Keep slots in issue order so a later slot's decode is not hoisted
+      // above this slot's loads.
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (tid == 0) p.cnt[rt] = 0;
   }
 
-  if (!rows_on) return;
+  // Fixed-order reduction of the waves' K-partials.
+#pragma unroll
+  for (int s = 0; s < NS; ++s) red[wave][s][lane] = acc[s];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    floatx4_t v = red[0][s][lane];
+#pragma unroll
+    for (int w = 1; w < W; ++w) v += red[w][s][lane];
+    acc[s] = v;
+  }
+
   const int row = rg * Q4_ROWS + n;
   if (row >= p.M) return;
+  const Q4Out &o = p.out;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int c = g * 4 + r;
-    if (c < p.B) {
-      if (EPI == Q4_EPI_SWIGLU) {
-        p.Y0[(size_t)c * p.ys + row] = silu_f(acc[0][r]) * acc[NS - 1][r];
-      } else {
-        p.Y0[(size_t)c * p.ys + row] = acc[0][r];
-        if (NS == 2) p.Y1[(size_t)c * p.ys + row] = acc[NS - 1][r];
-      }
+    if (c >= p.B) continue;
+    float v = (EPI == Q4_EPI_SWIGLU) ? silu_f(acc[0][r]) * acc[NS - 1][r] : acc[0][r];
+    if (o.y) {
+      float *dst = o.y + (size_t)c * o.ys + row;
+      if (o.accumulate) v += *dst;
+      *dst = v;
     }
+    if (o.yh) o.yh[(size_t)c * p.M + row] = (_Float16)v;
+    if (EPI == Q4_EPI_PAIR) o.y1[(size_t)c * o.ys + row] = acc[NS - 1][r];
   }
 }
 
@@ -275,6 +271,28 @@ __global__ void q4_repack_kernel(uint8_t *dst, const uint8_t *src, const uint16_
   }
 }
 
+template <int NS, int EPI>
+int launch_w(const Q4Params &p, int waves, int nrg, hipStream_t st) {
+  const dim3 grid((unsigned)nrg);
+  switch (waves) {
+    case 2: hipLaunchKernelGGL((q4_gemv_kernel<NS, EPI, 2>), grid, dim3(128), 0, st, p); break;
+    case 4: hipLaunchKernelGGL((q4_gemv_kernel<NS, EPI, 4>), grid, dim3(256), 0, st, p); break;
+    case 8: hipLaunchKernelGGL((q4_gemv_kernel<NS, EPI, 8>), grid, dim3(512), 0, st, p); break;
+    default: return CWEN_EINVAL;
+  }
+  return CWEN_OK;
+}
+
+__global__ void act_to_f16_kernel(const float *x, int xs, _Float16 *xh, int K, int B) {
+  const int k4 = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int c = blockIdx.y;
+  if (k4 >= K || c >= B) return;
+  const float4 v = *(const float4 *)(x + (size_t)c * xs + k4);
+  const half2_t a = {(_Float16)v.x, (_Float16)v.y}, b = {(_Float16)v.z, (_Float16)v.w};
+  *(uint2 *)(xh + (size_t)c * K + k4) = make_uint2(__builtin_bit_cast(uint32_t, a),
+                                                   __builtin_bit_cast(uint32_t, b));
+}
+
 }  // namespace
 
 int q4_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStream_t st) {
@@ -287,53 +305,44 @@ int q4_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStrea
   return CWEN_OK;
 }
 
-// Split-K choice depends on the shape only (never on B), so every column of
-// every call on this weight uses the same reduction tree.
+// Waves per workgroup: enough row groups x waves to fill the chip while each
+// wave keeps several K tiles.  Shape-only, so the reduction tree (and hence
+// every output bit) never depends on B.
 void q4_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
-  const int nrt = (w->nrg + WAVES - 1) / WAVES;
-  int S = (ctx->wg_target + nrt / 2) / nrt;
-  const int smax = w->nkt / 4 > 1 ? w->nkt / 4 : 1;
-  if (S < 1) S = 1;
-  if (S > smax) S = smax;
-  const int tps = (w->nkt + S - 1) / S;
-  w->tps = tps;
-  w->split = (w->nkt + tps - 1) / tps;
+  int waves = 2;
+  while (waves < 8 && (long)w->nrg * waves < ctx->wg_target && w->nkt / (waves * 2) >= 4) waves *= 2;
+  if (waves > w->nkt) waves = 2;
+  w->split = waves;
+  w->tps = (w->nkt + waves - 1) / waves;
 }
 
-int q4_gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
-                   const float *X, int xs, float *Y0, float *Y1, int ys, int B,
-                   hipStream_t st) {
+int q4_gemv_launch(const cwen_weight *w, int nsides, int side0, int epi, const _Float16 *xh,
+                   const Q4Out &out, int B, hipStream_t st) {
   Q4Params p;
   p.w = w->dev;
+  p.wbytes = (uint32_t)w->bytes;
   p.nsw = w->nside;
   p.side0 = side0;
   p.M = w->ne1;
-  p.nrg = w->nrg;
   p.nkt = w->nkt;
-  p.X = X;
-  p.xs = xs;
+  p.xh = xh;
+  p.xbytes = (uint32_t)((size_t)B * w->ne0 * 2);
   p.B = B;
-  p.Y0 = Y0;
-  p.Y1 = Y1;
-  p.ys = ys;
-  p.S = w->split;
-  p.tps = w->tps;
-  p.part = ctx->partials;
-  p.cnt = ctx->counters;
-  const int nrt = (w->nrg + WAVES - 1) / WAVES;
-  if (p.S > 1) {
-    const size_t need = (size_t)nrt * WAVES * p.S * nsides * 256;
-    if (need > ctx->partials_floats || nrt > ctx->ncounters) return CWEN_ESCRATCH;
-  }
-  const dim3 grid((unsigned)(nrt * p.S)), block(256);
-  if (nsides == 1 && epi == Q4_EPI_STORE)
-    hipLaunchKernelGGL((q4_gemv_kernel<1, Q4_EPI_STORE>), grid, block, 0, st, p);
-  else if (nsides == 2 && epi == Q4_EPI_STORE)
-    hipLaunchKernelGGL((q4_gemv_kernel<2, Q4_EPI_STORE>), grid, block, 0, st, p);
-  else if (nsides == 2 && epi == Q4_EPI_SWIGLU)
-    hipLaunchKernelGGL((q4_gemv_kernel<2, Q4_EPI_SWIGLU>), grid, block, 0, st, p);
-  else
-    return CWEN_EINVAL;
+  p.out = out;
+  int rc;
+  if (nsides == 1 && epi == Q4_EPI_STORE) rc = launch_w<1, Q4_EPI_STORE>(p, w->split, w->nrg, st);
+  else if (nsides == 2 && epi == Q4_EPI_PAIR) rc = launch_w<2, Q4_EPI_PAIR>(p, w->split, w->nrg, st);
+  else if (nsides == 2 && epi == Q4_EPI_SWIGLU) rc = launch_w<2, Q4_EPI_SWIGLU>(p, w->split, w->nrg, st);
+  else return CWEN_EINVAL;
+  if (rc) return rc;
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}
+
+int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st) {
+  const int threads = 256;
+  const dim3 grid((unsigned)((K / 4 + threads - 1) / threads), (unsigned)B);
+  hipLaunchKernelGGL(act_to_f16_kernel, grid, dim3(threads), 0, st, x, xs, xh, K, B);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }

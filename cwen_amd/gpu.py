@@ -32,6 +32,10 @@ SIGNATURES = [
     ("cwen_gemvb", _I, [_VP, _VP, _I, _VP, _I, _VP, _I, _I, _VP]),
     ("cwen_gemvb_pair", _I, [_VP, _VP, _VP, _I, _VP, _VP, _I, _I, _VP]),
     ("cwen_gemvb_swiglu", _I, [_VP, _VP, _VP, _I, _VP, _I, _I, _VP]),
+    ("cwen_mlp_block", _I, [_VP, _VP, _VP, _VP, _I, _VP, _I, _I, _VP]),
+    ("cwen_act_to_f16", _I, [_VP, _VP, _I, _VP, _I, _I, _VP]),
+    ("cwen_gemvb_f16", _I, [_VP, _VP, _I, _VP, _VP, _I, _VP, _I, _I, _VP]),
+    ("cwen_gemvb_swiglu_f16", _I, [_VP, _VP, _VP, _VP, _I, _VP, _I, _VP]),
 ]
 
 
@@ -63,8 +67,10 @@ def check(fn: str, rc: int) -> None:
         raise CwenError(fn, rc)
 
 
-def _ptr(t) -> int:
-    """Device pointer of a torch tensor (or raw int)."""
+def _ptr(t) -> int | None:
+    """Device pointer of a torch tensor (or raw int, or None)."""
+    if t is None:
+        return None
     return t if isinstance(t, int) else t.data_ptr()
 
 
@@ -148,3 +154,31 @@ def gemvb_swiglu(ctx: Context, W: Weight, X, H, B: int, xs: int | None = None,
     hs = W.M if hs is None else hs
     check("cwen_gemvb_swiglu", lib().cwen_gemvb_swiglu(ctx.h, W.h, _ptr(X), xs, _ptr(H), hs, B,
                                                        _stream(stream)))
+
+
+def mlp_block(ctx: Context, Wgu: Weight, Wd: Weight, X, Y, B: int, xs: int | None = None,
+              ys: int | None = None, stream=None) -> None:
+    """Y += down(silu(gate X) * (up X)) -- the block FFN (mlp_blk)."""
+    xs = Wgu.K if xs is None else xs
+    ys = Wd.M if ys is None else ys
+    check("cwen_mlp_block", lib().cwen_mlp_block(ctx.h, Wgu.h, Wd.h, _ptr(X), xs, _ptr(Y), ys, B,
+                                                 _stream(stream)))
+
+
+def act_to_f16(ctx: Context, X, Xh, K: int, B: int, xs: int | None = None, stream=None) -> None:
+    xs = K if xs is None else xs
+    check("cwen_act_to_f16", lib().cwen_act_to_f16(ctx.h, _ptr(X), xs, _ptr(Xh), K, B, _stream(stream)))
+
+
+def gemvb_f16(ctx: Context, W: Weight, Xh, Y, B: int, side: int = 0, Yh=None, accumulate: bool = False,
+              ys: int | None = None, stream=None) -> None:
+    ys = W.M if ys is None else ys
+    check("cwen_gemvb_f16", lib().cwen_gemvb_f16(ctx.h, W.h, side, _ptr(Xh), _ptr(Y), ys, _ptr(Yh),
+                                                 int(accumulate), B, _stream(stream)))
+
+
+def gemvb_swiglu_f16(ctx: Context, W: Weight, Xh, H, B: int, Hh=None, hs: int | None = None,
+                     stream=None) -> None:
+    hs = W.M if hs is None else hs
+    check("cwen_gemvb_swiglu_f16", lib().cwen_gemvb_swiglu_f16(ctx.h, W.h, _ptr(Xh), _ptr(H), hs, _ptr(Hh),
+                                                               B, _stream(stream)))

@@ -36,6 +36,9 @@ extern "C" {
 #define CWEN_ETYPE    (-4)   /* weight type not supported by this call   */
 #define CWEN_ESCRATCH (-5)   /* a shape exceeds the context's scratch    */
 
+/* Largest K (inputs) of a weight; sizes the context's f16 activation scratch. */
+#define CWEN_KMAX 65536
+
 /* ggml / CWENR weight type ids -- the same numeric ids as run.c:97-103 */
 #define CWEN_T_F32      0
 #define CWEN_T_Q4_0     2    /* GGUF 18-byte blocks {f16 d; u8 qs[16]}          */
@@ -54,8 +57,9 @@ typedef struct cwen_weight cwen_weight;  /* one device-resident weight matrix  *
 /* Library version string, e.g. "cwen-gpu 0.1 gfx950". */
 const char *cwen_version(void);
 
-/* Create a context on HIP device `device`: selects it, allocates the split-K
- * scratch.  Replaces alloc_state's scratch part (run.c:3928-4005). */
+/* Create a context on HIP device `device`: selects it and allocates the f16
+ * activation scratch (2 x 16 x CWEN_KMAX halves).  Replaces the block scratch
+ * part of alloc_state (run.c:3942-3963). */
 int cwen_ctx_create(int device, cwen_ctx **out);
 int cwen_ctx_destroy(cwen_ctx *ctx);
 
@@ -81,7 +85,8 @@ int cwen_weight_info(const cwen_weight *w, int *type, int *ne0, int *ne1,
  * Per output the arithmetic does not depend on B or on the other columns,
  * so a column computed in a block is bit-identical to the same column
  * computed alone.  Replaces gemvb (run.c:1577-1680) and, at B=1, gemv
- * (run.c:1419-1527). */
+ * (run.c:1419-1527).  X is converted to the f16 operand format in the
+ * context's scratch first (a second, small launch on the same stream). */
 int cwen_gemvb(cwen_ctx *ctx, const cwen_weight *W, int side,
                const float *X, int xs, float *Y, int ys, int B, void *stream);
 
@@ -96,6 +101,28 @@ int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs,
  * gemvb and silu_mul (run.c:2677-2680). */
 int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs,
                       float *H, int hs, int B, void *stream);
+
+/* The block FFN, mlp_blk (run.c:2677-2683): Y_b += W_down . (silu(W_gate . X_b)
+ * * (W_up . X_b)) for b < B, with Wgu a Q4_0RSI gate/up pair and Wd the down
+ * projection.  The hidden activations never leave the device in f32: the
+ * gate/up launch writes them straight into the down launch's operand format. */
+int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd,
+                   const float *X, int xs, float *Y, int ys, int B, void *stream);
+
+/* ---- f16 activation operands ----
+ * The kernels read activations as IEEE half, row-major [B][K] with row stride
+ * exactly K (2-byte elements, 16-byte aligned rows).  These entry points let a
+ * caller keep activations in that format between GEMVs; no reference
+ * counterpart (the reference keeps f32 everywhere and its AVX kernels read f32). */
+int cwen_act_to_f16(cwen_ctx *ctx, const float *X, int xs, void *Xh, int K, int B,
+                    void *stream);
+/* Y (f32, nullable) = or += W . Xh; Yh (f16 [B][M], nullable) gets the f32 result
+ * rounded to half (after accumulation when `accumulate` is set). */
+int cwen_gemvb_f16(cwen_ctx *ctx, const cwen_weight *W, int side, const void *Xh,
+                   float *Y, int ys, void *Yh, int accumulate, int B, void *stream);
+/* SwiGLU pair from f16 operands; H (f32, nullable), Hh (f16 [B][M], nullable). */
+int cwen_gemvb_swiglu_f16(cwen_ctx *ctx, const cwen_weight *W, const void *Xh,
+                          float *H, int hs, void *Hh, int B, void *stream);
 
 #ifdef __cplusplus
 }

@@ -50,7 +50,7 @@ def _run(env, W, X, side=0, mode="single"):
     return H.cpu().numpy()
 
 
-SHAPES = [(16, 128), (20, 256), (100, 512), (48, 5120), (1024, 1024), (5120, 5120)]
+SHAPES = [(16, 512), (20, 1024), (100, 512), (48, 5120), (1024, 1024), (5120, 5120)]
 
 
 @pytest.mark.parametrize("M,K", SHAPES)
@@ -66,7 +66,7 @@ def test_rs_parity(env, oracle, M, K):
         assert rel_err(got, want) <= TOL, (M, K, B, rel_err(got, want))
 
 
-@pytest.mark.parametrize("M,K", [(64, 256), (5120, 5120)])
+@pytest.mark.parametrize("M,K", [(64, 512), (5120, 5120)])
 def test_gguf_parity(env, oracle, M, K):
     torch, gpu, ctx = env
     blk = synth.q4_gguf(102, M, K)
@@ -77,7 +77,7 @@ def test_gguf_parity(env, oracle, M, K):
         assert rel_err(got, oracle.gemvb(T_Q4_0, blk, None, K, M, X)) <= TOL
 
 
-@pytest.mark.parametrize("M,K", [(40, 256), (1000, 2048)])
+@pytest.mark.parametrize("M,K", [(40, 512), (1000, 2048)])
 def test_rsi_single_pair_swiglu(env, oracle, M, K):
     torch, gpu, ctx = env
     qs, sc = synth.q4_rsi(103, M, K)
@@ -153,7 +153,7 @@ def test_strided_activations_and_outputs(env, oracle):
 
 def test_argument_errors(env):
     torch, gpu, ctx = env
-    M, K = 32, 256
+    M, K = 32, 512
     qs, sc = synth.q4_rs(108, M, K)
     W = gpu.Weight(ctx, T_RS, qs, sc, K, M)
     X = torch.zeros(17, K, device="cuda")
