@@ -17,6 +17,8 @@ int env_int(const char *name, int dflt, int lo, int hi) {
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 constexpr size_t kScratchHalves = (size_t)CWEN_BMAX * CWEN_KMAX;
+constexpr size_t kPartialFloats = (size_t)8 << 20;   // 32 MiB of split-K partials
+constexpr int kCounters = 1 << 16;
 
 }  // namespace
 
@@ -34,15 +36,23 @@ int cwen_ctx_create(int device, cwen_ctx **out) {
   cwen_ctx *c = (cwen_ctx *)calloc(1, sizeof(cwen_ctx));
   if (!c) return CWEN_ENOMEM;
   c->device = device;
-  c->wg_target = env_int("CWEN_GEMV_WG_TARGET", 2048, 64, 65536);
+  c->wg_target = env_int("CWEN_GEMV_WG_TARGET", 512, 64, 65536);
   if (hipMalloc((void **)&c->xh, kScratchHalves * 2) != hipSuccess) {
     free(c);
     return CWEN_ENOMEM;
   }
-  if (hipMalloc((void **)&c->hh, kScratchHalves * 2) != hipSuccess) {
-    (void)hipFree(c->xh);
-    free(c);
+  if (hipMalloc((void **)&c->hh, kScratchHalves * 2) != hipSuccess ||
+      hipMalloc((void **)&c->partials, kPartialFloats * sizeof(float)) != hipSuccess ||
+      hipMalloc((void **)&c->counters, kCounters * sizeof(int)) != hipSuccess) {
+    cwen_ctx_destroy(c);
     return CWEN_ENOMEM;
+  }
+  c->partials_floats = kPartialFloats;
+  c->ncounters = kCounters;
+  if (hipMemset(c->counters, 0, kCounters * sizeof(int)) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess) {
+    cwen_ctx_destroy(c);
+    return CWEN_EHIP;
   }
   *out = c;
   return CWEN_OK;
@@ -52,8 +62,10 @@ int cwen_ctx_destroy(cwen_ctx *ctx) {
   if (!ctx) return CWEN_EINVAL;
   (void)hipSetDevice(ctx->device);
   (void)hipDeviceSynchronize();
-  (void)hipFree(ctx->xh);
-  (void)hipFree(ctx->hh);
+  if (ctx->xh) (void)hipFree(ctx->xh);
+  if (ctx->hh) (void)hipFree(ctx->hh);
+  if (ctx->partials) (void)hipFree(ctx->partials);
+  if (ctx->counters) (void)hipFree(ctx->counters);
   free(ctx);
   return CWEN_OK;
 }
@@ -167,7 +179,7 @@ int cwen_gemvb(cwen_ctx *ctx, const cwen_weight *W, int side, const float *X, in
   hipStream_t st = (hipStream_t)stream;
   if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
   Q4Out o = {Y, nullptr, nullptr, ys, 0};
-  return q4_gemv_launch(W, 1, side, Q4_EPI_STORE, ctx->xh, o, B, st);
+  return q4_gemv_launch(ctx, W, 1, side, Q4_EPI_STORE, ctx->xh, o, B, st);
 }
 
 int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *YA,
@@ -181,7 +193,7 @@ int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs,
   hipStream_t st = (hipStream_t)stream;
   if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
   Q4Out o = {YA, YB, nullptr, ys, 0};
-  return q4_gemv_launch(W, 2, 0, Q4_EPI_PAIR, ctx->xh, o, B, st);
+  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_PAIR, ctx->xh, o, B, st);
 }
 
 int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *H,
@@ -193,7 +205,7 @@ int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int x
   hipStream_t st = (hipStream_t)stream;
   if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
   Q4Out o = {H, nullptr, nullptr, hs, 0};
-  return q4_gemv_launch(W, 2, 0, Q4_EPI_SWIGLU, ctx->xh, o, B, st);
+  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_SWIGLU, ctx->xh, o, B, st);
 }
 
 int cwen_gemvb_f16(cwen_ctx *ctx, const cwen_weight *W, int side, const void *Xh, float *Y,
@@ -206,7 +218,7 @@ int cwen_gemvb_f16(cwen_ctx *ctx, const cwen_weight *W, int side, const void *Xh
   if (Y && (rc = check_out(Y, ys, W->ne1, B))) return rc;
   if (Yh && (W->ne1 & 7)) return CWEN_EINVAL;
   Q4Out o = {Y, nullptr, (_Float16 *)Yh, ys, accumulate ? 1 : 0};
-  return q4_gemv_launch(W, 1, side, Q4_EPI_STORE, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
+  return q4_gemv_launch(ctx, W, 1, side, Q4_EPI_STORE, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
 }
 
 int cwen_gemvb_swiglu_f16(cwen_ctx *ctx, const cwen_weight *W, const void *Xh, float *H, int hs,
@@ -217,7 +229,7 @@ int cwen_gemvb_swiglu_f16(cwen_ctx *ctx, const cwen_weight *W, const void *Xh, f
   if (!H && !Hh) return CWEN_EINVAL;
   if (H && (rc = check_out(H, hs, W->ne1, B))) return rc;
   Q4Out o = {H, nullptr, (_Float16 *)Hh, hs, 0};
-  return q4_gemv_launch(W, 2, 0, Q4_EPI_SWIGLU, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
+  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_SWIGLU, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
 }
 
 int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd, const float *X,
@@ -230,9 +242,9 @@ int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd,
   hipStream_t st = (hipStream_t)stream;
   if ((rc = act_to_f16(X, xs, ctx->xh, Wgu->ne0, B, st))) return rc;
   Q4Out o1 = {nullptr, nullptr, ctx->hh, 0, 0};
-  if ((rc = q4_gemv_launch(Wgu, 2, 0, Q4_EPI_SWIGLU, ctx->xh, o1, B, st))) return rc;
+  if ((rc = q4_gemv_launch(ctx, Wgu, 2, 0, Q4_EPI_SWIGLU, ctx->xh, o1, B, st))) return rc;
   Q4Out o2 = {Y, nullptr, nullptr, ys, 1};
-  return q4_gemv_launch(Wd, 1, 0, Q4_EPI_STORE, ctx->hh, o2, B, st);
+  return q4_gemv_launch(ctx, Wd, 1, 0, Q4_EPI_STORE, ctx->hh, o2, B, st);
 }
 
 }  // extern "C"

@@ -16,14 +16,18 @@ constexpr int Q4_TILE_QS = 1024;
 constexpr int Q4_TILE_BYTES = 1152;
 constexpr int Q4_TILE_K = 128;
 constexpr int Q4_ROWS = 16;
-// K must be a multiple of one tile.
-constexpr int Q4_K_ALIGN = Q4_TILE_K;
+// K must be a multiple of 4 tiles (one staging round of the GEMV).
+constexpr int Q4_K_ALIGN = 4 * Q4_TILE_K;
 
 struct cwen_ctx {
   int device;
   int wg_target;            // workgroups a GEMV launch aims for
   _Float16 *xh;             // f16 activation scratch [BMAX][KMAX]
   _Float16 *hh;             // second f16 scratch (FFN hidden) [BMAX][KMAX]
+  float *partials;          // split-K partial sums
+  size_t partials_floats;
+  int *counters;            // per row-tile arrival counters, zero between launches
+  int ncounters;
 };
 
 struct cwen_weight {
@@ -35,7 +39,8 @@ struct cwen_weight {
   uint8_t *dev;             // tiled device data
   size_t bytes;             // device bytes of the tiled data
   size_t src_bytes;         // bytes of the reference layout (qs + scales)
-  int split, tps;           // waves per workgroup and K tiles per wave (shape-only)
+  int split, tps;           // K split across workgroups, K tiles per split (shape-only)
+  int rows;                 // row groups per wave (shape-only)
 };
 
 #define CWEN_HIP_TRY(expr)                                   \
@@ -71,6 +76,6 @@ struct Q4Out {
 };
 int q4_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStream_t st);
 void q4_choose_split(const cwen_ctx *ctx, cwen_weight *w);
-int q4_gemv_launch(const cwen_weight *w, int nsides, int side0, int epi, const _Float16 *xh,
-                   const Q4Out &out, int B, hipStream_t st);
+int q4_gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
+                   const _Float16 *xh, const Q4Out &out, int B, hipStream_t st);
 int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st);

@@ -169,7 +169,7 @@ def test_argument_errors(env):
         gpu.gemvb_swiglu(ctx, W, X, Y, 1)                  # needs a pair
     qs2, sc2 = synth.q4_rs(108, M, 96)
     with pytest.raises(gpu.CwenError):
-        gpu.Weight(ctx, T_RS, qs2, sc2, 96, M)             # K not a multiple of 128
+        gpu.Weight(ctx, T_RS, qs2, sc2, 96, M)             # K not a multiple of 512
     with pytest.raises(gpu.CwenError):
         gpu.Weight(ctx, 3, qs, sc, K, M)                   # Q4_1 is not a supported type
 
