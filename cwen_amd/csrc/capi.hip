@@ -95,8 +95,8 @@ int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *sc
   w->ne1 = ne1;
   w->nside = nside;
   w->nrg = (ne1 + Q4_ROWS - 1) / Q4_ROWS;
-  w->nkt = ne0 / Q4_TILE_K;
-  w->bytes = (size_t)w->nrg * w->nkt * nside * Q4_TILE_BYTES;
+  w->nst = ne0 / Q4_ST_K;
+  w->bytes = (size_t)w->nrg * w->nst * nside * Q4_ST_BYTES;
   if (w->bytes >= ((size_t)1 << 32)) {  // kernels address weights with 32-bit buffer offsets
     free(w);
     return CWEN_EINVAL;

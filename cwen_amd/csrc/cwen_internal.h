@@ -8,16 +8,20 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-// Q4 tile: 16 rows x 4 blocks of 32 weights (128 K).  1024 bytes of nibbles
-// in MFMA operand order (lane l = 16*g + n holds 16 bytes; dword m carries
-// the 8 weights k = 8g..8g+7 of block m of row n) followed by 128 bytes of
-// f16 scales laid out [n][m].
-constexpr int Q4_TILE_QS = 1024;
-constexpr int Q4_TILE_BYTES = 1152;
+// Q4 super-tile: 16 rows x 16 blocks of 32 weights (512 K) of one weight
+// stream.  Four 1024-byte nibble tiles (tile u covers K 128u..128u+127) in
+// MFMA operand order -- lane l = 16*g + n holds 16 bytes, dword m carrying
+// the 8 weights k = 8m..8m+7 of block g of row n -- followed by 512 bytes of
+// f16 scales, lane l holding the scales of its block in tiles 0..3.
 constexpr int Q4_TILE_K = 128;
+constexpr int Q4_TILE_QS = 1024;
+constexpr int Q4_ST_TILES = 4;
+constexpr int Q4_ST_K = Q4_ST_TILES * Q4_TILE_K;            // 512
+constexpr int Q4_ST_QS = Q4_ST_TILES * Q4_TILE_QS;          // 4096
+constexpr int Q4_ST_BYTES = Q4_ST_QS + 64 * 8;              // 4608
 constexpr int Q4_ROWS = 16;
-// K must be a multiple of 4 tiles (one staging round of the GEMV).
-constexpr int Q4_K_ALIGN = 4 * Q4_TILE_K;
+// K must be a whole number of super-tiles.
+constexpr int Q4_K_ALIGN = Q4_ST_K;
 
 struct cwen_ctx {
   int device;
@@ -35,11 +39,11 @@ struct cwen_weight {
   int type;                 // CWEN_T_*
   int ne0, ne1;             // K, M
   int nside;                // 2 for an interleaved pair, else 1
-  int nrg, nkt;             // 16-row groups, 128-wide K tiles
+  int nrg, nst;             // 16-row groups, 512-wide K super-tiles
   uint8_t *dev;             // tiled device data
   size_t bytes;             // device bytes of the tiled data
   size_t src_bytes;         // bytes of the reference layout (qs + scales)
-  int split, tps;           // K split across workgroups, K tiles per split (shape-only)
+  int split, rps;           // K split across workgroups, super-tiles per split (shape-only)
   int rows;                 // row groups per wave (shape-only)
 };
 
@@ -55,11 +59,13 @@ struct cwen_weight {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+// `voff` is the per-lane offset (the part the range check sees); `soff` a
+// wave-uniform offset carried in a scalar register.
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
-__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
 
 // run.c:378-384 silu_one: x * (1 / (1 + exp(-x)))
