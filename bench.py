@@ -31,6 +31,8 @@ METRIC = "verified tok/s + HBM GB/s (% of peak), Q4_0 27B-shape verify B=1/8/16"
 H, I = 5120, 17408
 PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
 NCOPIES = 4
+COPY_BYTES = 256 << 20     # calibration copy for the counter profile
+TRAFFIC_FILE = "q4_gemv_swiglu_ffn_b8_traffic.json"
 
 
 def ffn_bytes(B: int) -> tuple[int, int]:
@@ -50,6 +52,44 @@ def make_weights(seed: int, copy: int):
     gq, gs = synth.q4_rsi(seed, I, H, key=2 * copy)
     dq, ds = synth.q4_rs(seed, H, I, key=2 * copy + 1)
     return gq, gs, dq, ds
+
+
+def time_launches(fn, n: int, warmup: int, stream) -> float:
+    """Mean ms per launch of `fn(i)` over n back-to-back launches."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(n):
+        fn(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def calibrate_copy(nbytes: int = COPY_BYTES, reps: int = 3) -> None:
+    """A plain device copy of known size (torch's copy kernel), run so that a
+    counter profile of this process can scale FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+        torch.cuda.synchronize()
+    del src, dst
+
+
+def load_traffic() -> dict | None:
+    """HBM bytes per launch of the headline kernel from the committed counter
+    profile (FETCH_SIZE + WRITE_SIZE, each scaled by the copy calibration)."""
+    f = ROOT / "profiles" / TRAFFIC_FILE
+    try:
+        d = json.loads(f.read_text())
+        return {"bytes": int(d["traffic_bytes"]), "source": f"profiles/{TRAFFIC_FILE}"}
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def gpu_leg(steps: int, warmup: int, Bs: list[int]) -> dict:
@@ -86,20 +126,14 @@ def gpu_leg(steps: int, warmup: int, Bs: list[int]) -> dict:
         t1.record(stream)
         torch.cuda.synchronize()
         ms_step = t0.elapsed_time(t1) / steps
-        # Per-launch timing of the two GEMV kernels mlp_block runs (same entry
-        # points, f16 operands), events on the launch stream.
+        # Average launch duration of each of the two GEMV kernels mlp_block
+        # runs (same entry points, f16 operands): `steps` back-to-back
+        # launches of one kernel between two events on the launch stream.
         gpu.act_to_f16(ctx, X, Xh, H, B, stream=stream)
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-        for i in range(steps):
-            c = i % NCOPIES
-            evs[i][0].record(stream)
-            gpu.gemvb_swiglu_f16(ctx, Wgu[c], Xh, None, B, Hh=Hh, stream=stream)
-            evs[i][1].record(stream)
-            gpu.gemvb_f16(ctx, Wd[c], Hh, Y, B, accumulate=True, stream=stream)
-            evs[i][2].record(stream)
-        torch.cuda.synchronize()
-        l1_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
-        l2_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+        l1_ms = time_launches(lambda i: gpu.gemvb_swiglu_f16(ctx, Wgu[i % NCOPIES], Xh, None, B, Hh=Hh,
+                                                             stream=stream), steps, warmup, stream)
+        l2_ms = time_launches(lambda i: gpu.gemvb_f16(ctx, Wd[i % NCOPIES], Hh, Y, B, accumulate=True,
+                                                      stream=stream), steps, warmup, stream)
         b1, b2 = ffn_bytes(B)
         out[B] = {
             "ms_per_step": ms_step,
@@ -184,6 +218,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--Bs", default="8,1,16",
                     help="comma-separated block sizes; the first is the headline (must include 8)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a 256 MiB device copy (for FETCH_SIZE/WRITE_SIZE calibration)")
     ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--B", type=int, default=8, help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -197,7 +233,10 @@ def main() -> int:
     if 8 not in Bs:
         print("bench.py: --Bs must include the headline B=8", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        calibrate_copy()
     res = gpu_leg(args.steps, args.warmup, Bs)
+    traffic = load_traffic()
     h = res[8]
     b1, _ = ffn_bytes(8)
     line = {
@@ -226,13 +265,14 @@ def main() -> int:
                       for B, r in sorted(res.items())},
         },
         "roofline": {
-            "kernel": "q4_gemv_kernel<2,SWIGLU,W> (gate/up pair + SwiGLU), B=8",
+            "kernel": "q4_gemv_kernel<2,1,2,8> (Q4_0 RSI gate/up pair + SwiGLU, 8 staged columns), B=8",
             "bound": "hbm",
             "achieved": round(h["swiglu_gbs"], 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(h["swiglu_gbs"] / PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": None if traffic is None else traffic["bytes"],
+            "traffic_source": None if traffic is None else traffic["source"],
             "algorithmic_bytes": b1,
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_leg(8),
