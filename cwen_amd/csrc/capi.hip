@@ -43,13 +43,18 @@ int cwen_ctx_create(int device, cwen_ctx **out) {
   }
   if (hipMalloc((void **)&c->hh, kScratchHalves * 2) != hipSuccess ||
       hipMalloc((void **)&c->partials, kPartialFloats * sizeof(float)) != hipSuccess ||
-      hipMalloc((void **)&c->counters, kCounters * sizeof(int)) != hipSuccess) {
+      hipMalloc((void **)&c->counters, kCounters * sizeof(int)) != hipSuccess ||
+      hipMalloc((void **)&c->amax_keys, CWEN_BMAX * sizeof(unsigned long long)) != hipSuccess ||
+      hipMalloc((void **)&c->amax_cnt, sizeof(int)) != hipSuccess ||
+      hipMalloc((void **)&c->res, (2 + CWEN_BMAX) * sizeof(int)) != hipSuccess) {
     cwen_ctx_destroy(c);
     return CWEN_ENOMEM;
   }
   c->partials_floats = kPartialFloats;
   c->ncounters = kCounters;
   if (hipMemset(c->counters, 0, kCounters * sizeof(int)) != hipSuccess ||
+      hipMemset(c->amax_keys, 0, CWEN_BMAX * sizeof(unsigned long long)) != hipSuccess ||
+      hipMemset(c->amax_cnt, 0, sizeof(int)) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {
     cwen_ctx_destroy(c);
     return CWEN_EHIP;
@@ -66,6 +71,9 @@ int cwen_ctx_destroy(cwen_ctx *ctx) {
   if (ctx->hh) (void)hipFree(ctx->hh);
   if (ctx->partials) (void)hipFree(ctx->partials);
   if (ctx->counters) (void)hipFree(ctx->counters);
+  if (ctx->amax_keys) (void)hipFree(ctx->amax_keys);
+  if (ctx->amax_cnt) (void)hipFree(ctx->amax_cnt);
+  if (ctx->res) (void)hipFree(ctx->res);
   free(ctx);
   return CWEN_OK;
 }
@@ -74,35 +82,41 @@ int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *sc
                        int ne0, int ne1, cwen_weight **out) {
   if (!ctx || !data || !out || ne0 <= 0 || ne1 <= 0) return CWEN_EINVAL;
   *out = nullptr;
-  if (type != CWEN_T_Q4_0 && type != CWEN_T_Q4_0RS && type != CWEN_T_Q4_0RSI) return CWEN_ETYPE;
+  const int fmt = gemv_fmt_of(type);
+  if (fmt < 0) return CWEN_ETYPE;
   if (ne0 % Q4_K_ALIGN || ne0 > CWEN_KMAX) return CWEN_EINVAL;
-  const bool split_scales = (type != CWEN_T_Q4_0);
+  const bool split_scales = (type == CWEN_T_Q4_0RS || type == CWEN_T_Q4_0RSI);
   if (split_scales && !scales) return CWEN_EINVAL;
   CWEN_HIP_TRY(hipSetDevice(ctx->device));
 
   const size_t nblk = (size_t)(ne0 / 32) * ne1;
   size_t qbytes = 0, sbytes = 0;
   int nside = 1;
-  if (type == CWEN_T_Q4_0) qbytes = nblk * 18;
-  else if (type == CWEN_T_Q4_0RS) { qbytes = nblk * 16; sbytes = nblk * 2; }
-  else { qbytes = nblk * 32; sbytes = nblk * 4; nside = 2; }
+  switch (type) {
+    case CWEN_T_Q4_0: qbytes = nblk * 18; break;
+    case CWEN_T_Q4_0RS: qbytes = nblk * 16; sbytes = nblk * 2; break;
+    case CWEN_T_Q4_0RSI: qbytes = nblk * 32; sbytes = nblk * 4; nside = 2; break;
+    case CWEN_T_Q6_K: qbytes = (size_t)(ne0 / 256) * ne1 * 210; break;
+    default: qbytes = nblk * 34; break;  // Q8_0
+  }
 
   cwen_weight *w = (cwen_weight *)calloc(1, sizeof(cwen_weight));
   if (!w) return CWEN_ENOMEM;
   w->ctx = ctx;
   w->type = type;
+  w->fmt = fmt;
   w->ne0 = ne0;
   w->ne1 = ne1;
   w->nside = nside;
   w->nrg = (ne1 + Q4_ROWS - 1) / Q4_ROWS;
   w->nst = ne0 / Q4_ST_K;
-  w->bytes = (size_t)w->nrg * w->nst * nside * Q4_ST_BYTES;
+  w->bytes = (size_t)w->nrg * w->nst * nside * gemv_st_bytes(fmt);
   if (w->bytes >= ((size_t)1 << 32)) {  // kernels address weights with 32-bit buffer offsets
     free(w);
     return CWEN_EINVAL;
   }
   w->src_bytes = qbytes + sbytes;
-  q4_choose_split(ctx, w);
+  gemv_choose_split(ctx, w);
 
   uint8_t *dsrc = nullptr;
   uint16_t *dsc = nullptr;
@@ -115,7 +129,7 @@ int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *sc
     rc = CWEN_EHIP;
     goto fail;
   }
-  rc = q4_repack(w, dsrc, dsc, nullptr);
+  rc = gemv_repack(w, dsrc, dsc, nullptr);
   if (rc != CWEN_OK) goto fail;
   if (hipDeviceSynchronize() != hipSuccess) { rc = CWEN_EHIP; goto fail; }
   (void)hipFree(dsrc);
@@ -178,8 +192,8 @@ int cwen_gemvb(cwen_ctx *ctx, const cwen_weight *W, int side, const float *X, in
   if ((rc = check_act(X, xs, W->ne0, B)) || (rc = check_out(Y, ys, W->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
   if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
-  Q4Out o = {Y, nullptr, nullptr, ys, 0};
-  return q4_gemv_launch(ctx, W, 1, side, Q4_EPI_STORE, ctx->xh, o, B, st);
+  GemvOut o = {Y, nullptr, nullptr, ys, 0};
+  return gemv_launch(ctx, W, 1, side, GEMV_EPI_STORE, ctx->xh, o, B, st);
 }
 
 int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *YA,
@@ -192,8 +206,8 @@ int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs,
     return rc;
   hipStream_t st = (hipStream_t)stream;
   if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
-  Q4Out o = {YA, YB, nullptr, ys, 0};
-  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_PAIR, ctx->xh, o, B, st);
+  GemvOut o = {YA, YB, nullptr, ys, 0};
+  return gemv_launch(ctx, W, 2, 0, GEMV_EPI_PAIR, ctx->xh, o, B, st);
 }
 
 int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *H,
@@ -204,8 +218,8 @@ int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int x
   if ((rc = check_act(X, xs, W->ne0, B)) || (rc = check_out(H, hs, W->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
   if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
-  Q4Out o = {H, nullptr, nullptr, hs, 0};
-  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_SWIGLU, ctx->xh, o, B, st);
+  GemvOut o = {H, nullptr, nullptr, hs, 0};
+  return gemv_launch(ctx, W, 2, 0, GEMV_EPI_SWIGLU, ctx->xh, o, B, st);
 }
 
 int cwen_gemvb_f16(cwen_ctx *ctx, const cwen_weight *W, int side, const void *Xh, float *Y,
@@ -217,8 +231,8 @@ int cwen_gemvb_f16(cwen_ctx *ctx, const cwen_weight *W, int side, const void *Xh
   if (!Y && !Yh) return CWEN_EINVAL;
   if (Y && (rc = check_out(Y, ys, W->ne1, B))) return rc;
   if (Yh && (W->ne1 & 7)) return CWEN_EINVAL;
-  Q4Out o = {Y, nullptr, (_Float16 *)Yh, ys, accumulate ? 1 : 0};
-  return q4_gemv_launch(ctx, W, 1, side, Q4_EPI_STORE, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
+  GemvOut o = {Y, nullptr, (_Float16 *)Yh, ys, accumulate ? 1 : 0};
+  return gemv_launch(ctx, W, 1, side, GEMV_EPI_STORE, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
 }
 
 int cwen_gemvb_swiglu_f16(cwen_ctx *ctx, const cwen_weight *W, const void *Xh, float *H, int hs,
@@ -228,8 +242,8 @@ int cwen_gemvb_swiglu_f16(cwen_ctx *ctx, const cwen_weight *W, const void *Xh, f
   if (W->nside != 2 || !Xh || !aligned16(Xh) || B < 1 || B > CWEN_BMAX) return CWEN_EINVAL;
   if (!H && !Hh) return CWEN_EINVAL;
   if (H && (rc = check_out(H, hs, W->ne1, B))) return rc;
-  Q4Out o = {H, nullptr, (_Float16 *)Hh, hs, 0};
-  return q4_gemv_launch(ctx, W, 2, 0, Q4_EPI_SWIGLU, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
+  GemvOut o = {H, nullptr, (_Float16 *)Hh, hs, 0};
+  return gemv_launch(ctx, W, 2, 0, GEMV_EPI_SWIGLU, (const _Float16 *)Xh, o, B, (hipStream_t)stream);
 }
 
 int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd, const float *X,
@@ -241,10 +255,33 @@ int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd,
   if ((rc = check_act(X, xs, Wgu->ne0, B)) || (rc = check_out(Y, ys, Wd->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
   if ((rc = act_to_f16(X, xs, ctx->xh, Wgu->ne0, B, st))) return rc;
-  Q4Out o1 = {nullptr, nullptr, ctx->hh, 0, 0};
-  if ((rc = q4_gemv_launch(ctx, Wgu, 2, 0, Q4_EPI_SWIGLU, ctx->xh, o1, B, st))) return rc;
-  Q4Out o2 = {Y, nullptr, nullptr, ys, 1};
-  return q4_gemv_launch(ctx, Wd, 1, 0, Q4_EPI_STORE, ctx->hh, o2, B, st);
+  GemvOut o1 = {nullptr, nullptr, ctx->hh, 0, 0};
+  if ((rc = gemv_launch(ctx, Wgu, 2, 0, GEMV_EPI_SWIGLU, ctx->xh, o1, B, st))) return rc;
+  GemvOut o2 = {Y, nullptr, nullptr, ys, 1};
+  return gemv_launch(ctx, Wd, 1, 0, GEMV_EPI_STORE, ctx->hh, o2, B, st);
+}
+
+int cwen_head_verify(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, int B,
+                     const int *drafts, int E, float *logits, int ls, int *res, void *stream) {
+  int rc = check_w(ctx, W);
+  if (rc) return rc;
+  if (W->nside != 1 || !res) return CWEN_EINVAL;
+  if ((rc = check_act(X, xs, W->ne0, B))) return rc;
+  if (E < 0 || E > B - 1 || (E > 0 && !drafts)) return CWEN_EINVAL;
+  if (logits && (rc = check_out(logits, ls, W->ne1, B))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
+  GemvOut o = {logits, nullptr, nullptr, ls, 0, {ctx->amax_keys, ctx->amax_cnt, drafts, E, res}};
+  return gemv_launch(ctx, W, 1, 0, GEMV_EPI_ARGMAX, ctx->xh, o, B, st);
+}
+
+int cwen_argmax_walk(cwen_ctx *ctx, const float *logits, int ls, int V, int B, const int *drafts,
+                     int E, int *res, void *stream) {
+  if (!ctx || !logits || !res || V < 1 || B < 1 || B > CWEN_BMAX) return CWEN_EINVAL;
+  if ((B > 1 && ls < V) || ls < 0) return CWEN_EINVAL;
+  if (E < 0 || E > B - 1 || (E > 0 && !drafts)) return CWEN_EINVAL;
+  const ArgmaxOut a = {ctx->amax_keys, ctx->amax_cnt, drafts, E, res};
+  return argmax_walk_launch(logits, ls, V, B, a, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -8,20 +8,18 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-// Q4 super-tile: 16 rows x 16 blocks of 32 weights (512 K) of one weight
-// stream.  Four 1024-byte nibble tiles (tile u covers K 128u..128u+127) in
-// MFMA operand order -- lane l = 16*g + n holds 16 bytes, dword m carrying
-// the 8 weights k = 8m..8m+7 of block g of row n -- followed by 512 bytes of
-// f16 scales, lane l holding the scales of its block in tiles 0..3.
+// Weight super-tile: 16 rows x 512 K of one weight stream, four 128-K tiles
+// in MFMA operand order (lane l = 16*g + n of a wave owns 32-weight block g of
+// row n in each tile) followed by the format's scales.  The per-format byte
+// layouts are described in gemv.hip.
 constexpr int Q4_TILE_K = 128;
-constexpr int Q4_TILE_QS = 1024;
 constexpr int Q4_ST_TILES = 4;
 constexpr int Q4_ST_K = Q4_ST_TILES * Q4_TILE_K;            // 512
-constexpr int Q4_ST_QS = Q4_ST_TILES * Q4_TILE_QS;          // 4096
-constexpr int Q4_ST_BYTES = Q4_ST_QS + 64 * 8;              // 4608
 constexpr int Q4_ROWS = 16;
 // K must be a whole number of super-tiles.
 constexpr int Q4_K_ALIGN = Q4_ST_K;
+
+enum { GEMV_Q4 = 0, GEMV_Q6K = 1, GEMV_Q8 = 2 };
 
 struct cwen_ctx {
   int device;
@@ -32,11 +30,15 @@ struct cwen_ctx {
   size_t partials_floats;
   int *counters;            // per row-tile arrival counters, zero between launches
   int ncounters;
+  unsigned long long *amax_keys;  // per-column argmax keys [CWEN_BMAX], zero between launches
+  int *amax_cnt;            // argmax arrival counter, zero between launches
+  int *res;                 // device result slots of the verify entry points [2 + CWEN_BMAX]
 };
 
 struct cwen_weight {
   cwen_ctx *ctx;
   int type;                 // CWEN_T_*
+  int fmt;                  // GEMV_Q4 / GEMV_Q6K / GEMV_Q8
   int ne0, ne1;             // K, M
   int nside;                // 2 for an interleaved pair, else 1
   int nrg, nst;             // 16-row groups, 512-wide K super-tiles
@@ -71,17 +73,28 @@ __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff,
 // run.c:378-384 silu_one: x * (1 / (1 + exp(-x)))
 __device__ __forceinline__ float silu_f(float x) { return x * (1.f / (1.f + expf(-x))); }
 
-// ------------------------------------------------------------ q4_gemv.hip
-enum { Q4_EPI_STORE = 0, Q4_EPI_PAIR = 1, Q4_EPI_SWIGLU = 2 };
-struct Q4Out {
-  float *y;          // f32 result (side A, or silu(A)*B) [c*ys + row], nullable
+// ------------------------------------------------------------ gemv.hip
+enum { GEMV_EPI_STORE = 0, GEMV_EPI_PAIR = 1, GEMV_EPI_SWIGLU = 2, GEMV_EPI_ARGMAX = 3 };
+struct ArgmaxOut {
+  unsigned long long *keys;  // per-column keys, zero between launches
+  int *cnt;                  // arrival counter, zero between launches
+  const int *drafts;         // device draft ids [E]
+  int E;
+  int *out;                  // device: k, bonus, argmax of columns 0..B-1
+};
+struct GemvOut {
+  float *y;          // f32 result (side A, or silu(A)*B, or logits) [c*ys + row], nullable
   float *y1;         // f32 side B of a pair [c*ys + row] (PAIR only)
   _Float16 *yh;      // f16 copy of the (accumulated) result [c*M + row], nullable
   int ys;
   int accumulate;    // y += result
+  ArgmaxOut am;      // ARGMAX only
 };
-int q4_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStream_t st);
-void q4_choose_split(const cwen_ctx *ctx, cwen_weight *w);
-int q4_gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
-                   const _Float16 *xh, const Q4Out &out, int B, hipStream_t st);
+int gemv_fmt_of(int type);
+size_t gemv_st_bytes(int fmt);
+int gemv_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStream_t st);
+void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w);
+int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
+                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st);
 int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st);
+int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &a, hipStream_t st);

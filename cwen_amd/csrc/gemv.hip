@@ -1,0 +1,911 @@
+// Batched quantized GEMV for a verify block of B = 1..16 activation columns:
+// Q4_0 (GGUF, CWENR RS and RSI), Q6_K and Q8_0 weights.
+//
+// Reference semantics: gemvb / gemv_row / dot_q4_bcol / dot_q4_0rsi_2mat /
+// dot_q6_K / dot_q8_0 / mlp_blk (run.c:1577-1680, 1360-1387, 1529-1571,
+// 886-975, 1160-1274, 2677-2683): Y[b][i] = sum_k w_ik * X[b][k] with
+//   Q4_0  w = (n - 8) * d_blk             (32-weight blocks, f16 d)
+//   Q6_K  w = (q6 - 32) * d_sb * sc_sub   (256-weight super-blocks, f16 d,
+//                                          int8 scale per 16 weights)
+//   Q8_0  w = q8 * d_blk                  (32-weight blocks, f16 d)
+// and, for the LM head, the per-column argmax and greedy prefix walk of
+// argmax_of and generate_tokens_spec (run.c:2647-2668, 4954-4956).
+//
+// Design (gfx950):
+//  * Weights are repacked once at upload into super-tiles of 16 rows x 512 K
+//    per weight stream, laid out in MFMA operand order.  A super-tile holds
+//    four 128-K tiles; in tile u, lane l = 16g + n of a wave owns 32-weight
+//    block g of row n, so each 16-byte load of a wave moves 1 KB and no byte
+//    is fetched twice.  The per-format bytes are the reference's exactly
+//    (18 B / 32 Q4_0 weights, 210 B / 256 Q6_K weights, 34 B / 32 Q8_0
+//    weights); only their order changes:
+//      Q4_0  4608 B: 4 x 1 KB nibble tiles | 512 B scales (lane: its block's
+//            f16 scale in tiles 0..3)
+//      Q6_K  6720 B: 4 x 1 KB low-nibble tiles | 2 x 1 KB high-bit tile pairs
+//            | 512 B int8 sub-scales, stored + 128 (lane: its 2 sub-blocks
+//            in tiles 0..3) | 64 B f16 d [row][super-block]
+//      Q8_0  8704 B: 4 x 2 KB int8 tiles, stored + 128 (lane: two 16-byte
+//            halves) | 512 B scales
+//  * v_mfma_f32_16x16x32_f16, A = activations (16 columns x 32 K), B =
+//    weights (32 K x 16 rows).  MFMA m of a tile takes K run m (8 weights) of
+//    each lane's block, so a lane's B operand always belongs to one scale
+//    group and the scale is folded into the f16 weights.  Integers become
+//    f16 exactly through the magic-exponent trick ((bits | 0x6400) is
+//    1024 + bits); the product with the scale is the one rounding (relative
+//    2^-12), the same order as the f16 activation rounding.  The MFMA
+//    accumulates in f32.
+//  * Activations are f16 row-major [B][K].  A workgroup's 4 waves take
+//    different rows over the same K range and share the activation chunk,
+//    staged once per workgroup in LDS (double-buffered).  One staging load
+//    moves one column's 1 KB of a super-tile; the LDS slot of 16-byte unit u
+//    of column c is c*64 + (u ^ c), which keeps both the column-wise writes
+//    and the MFMA operand reads free of bank conflicts.  Only the first CB
+//    columns (CB = 4, 8 or 16, the smallest >= B) are staged; columns in
+//    [B, CB) lie past the buffer range and load as zeros.  Output column c
+//    depends on activation column c alone, so the unstaged columns only feed
+//    discarded outputs, and a column's arithmetic never depends on B (block
+//    verify == serial decode, bit for bit).
+//  * Long K is split across workgroups.  Each writes its partial sums with
+//    agent-scope atomic stores, bumps a per-row-tile counter, and the last
+//    arriver sums the partials in split order: deterministic, with no cache
+//    writeback/invalidate.  The split depends on the shape only.
+//  * Each wave keeps one super-tile per weight stream in flight; every global
+//    load in the loop is unconditional and issued in a fixed order (scales,
+//    staging, then tiles), so the in-order load counter only waits for the
+//    data being consumed.
+#include <type_traits>
+
+#include "cwen_internal.h"
+
+namespace {
+
+constexpr int TILES = Q4_ST_TILES;  // tiles per round: one super-tile per stream
+constexpr int WAVES = 4;            // waves per workgroup
+
+// K-run order inside a dword: the nibble unpack yields elements from nibbles
+// 0,4,1,5,2,6,3,7, so the repack stores weight e of a run at kNibPos[e].
+__constant__ int kNibPos[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+
+// Per-format layout of one 16-row x 512-K super-tile of one weight stream.
+template <int FMT> struct Fmt;
+template <> struct Fmt<GEMV_Q4> {
+  static constexpr uint32_t ST_BYTES = 4608, SC_OFS = 4096;
+  static constexpr int TV = 1;                 // 16-byte loads per tile per lane
+};
+template <> struct Fmt<GEMV_Q6K> {
+  static constexpr uint32_t ST_BYTES = 6720, HI_OFS = 4096, SC_OFS = 6144, D_OFS = 6656;
+  static constexpr int TV = 1;
+};
+template <> struct Fmt<GEMV_Q8> {
+  static constexpr uint32_t ST_BYTES = 8704, SC_OFS = 8192;
+  static constexpr int TV = 2;
+};
+
+// (q & mask) | magic in one VOP3 op.  gfx9 VOP3 takes no literal and reads at
+// most one scalar, so the mask comes from an SGPR and the magic from a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t q, uint32_t mask_s, uint32_t magic_v) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(q), "s"(mask_s), "v"(magic_v));
+  return r;
+}
+
+struct Unpack {
+  uint32_t lo, hi;     // SGPR masks 0x000F000F, 0x00F000F0
+  uint32_t h0, h1;     // SGPR masks 0x00300030, 0x03000300 (Q6_K high bits)
+  uint32_t magic;      // VGPR 0x64006400
+};
+// Materialise the constants once, opaque to the compiler, so the loop does
+// not rebuild them per use.
+__device__ __forceinline__ Unpack unpack_consts() {
+  Unpack u;
+  asm volatile("s_mov_b32 %0, 0x000f000f" : "=s"(u.lo));
+  asm volatile("s_mov_b32 %0, 0x00f000f0" : "=s"(u.hi));
+  asm volatile("s_mov_b32 %0, 0x00300030" : "=s"(u.h0));
+  asm volatile("s_mov_b32 %0, 0x03000300" : "=s"(u.h1));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(u.magic));
+  return u;
+}
+
+__device__ __forceinline__ half8_t pack8(half2_t h0, half2_t h1, half2_t h2, half2_t h3) {
+  half8_t r;
+  r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
+  r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
+  return r;
+}
+__device__ __forceinline__ half2_t h2c(float v) { return (half2_t){(_Float16)v, (_Float16)v}; }
+
+// Q4_0: 8 nibbles -> 8 f16 weights (n - 8) * d.  (n - 8) is exact; the
+// product with the block scale is the one rounding.
+__device__ __forceinline__ half8_t unpack8_q4(uint32_t q, const Unpack &u, half2_t dd) {
+  const uint32_t q2 = q >> 8;
+  const uint32_t t0 = and_or(q, u.lo, u.magic);    // 1024 + n0, 1024 + n4
+  const uint32_t t1 = and_or(q, u.hi, u.magic);    // 1024 + 16 n1, 1024 + 16 n5
+  const uint32_t t2 = and_or(q2, u.lo, u.magic);   // 1024 + n2, 1024 + n6
+  const uint32_t t3 = and_or(q2, u.hi, u.magic);   // 1024 + 16 n3, 1024 + 16 n7
+  const half2_t h0 = (__builtin_bit_cast(half2_t, t0) - h2c(1032.f)) * dd;
+  const half2_t h1 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t1), h2c(0.0625f), h2c(-72.f)) * dd;
+  const half2_t h2 = (__builtin_bit_cast(half2_t, t2) - h2c(1032.f)) * dd;
+  const half2_t h3 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t3), h2c(0.0625f), h2c(-72.f)) * dd;
+  return pack8(h0, h1, h2, h3);
+}
+
+// Q6_K: low nibbles as Q4_0 plus the 2 high bits of each weight, laid out in
+// `h` so that one masked OR drops them above the nibble: weight e's bits sit
+// at 4-5 / 20-21 (e = 0, 1), 8-9 / 24-25 (e = 2, 3) and, after h >> 2, the
+// same places for e = 4..7.  The 6-bit value is exact in f16; q6 - 32 too.
+__device__ __forceinline__ half8_t unpack8_q6(uint32_t q, uint32_t h, const Unpack &u, half2_t dd) {
+  const uint32_t q2 = q >> 8, hs = h >> 2;
+  const uint32_t t0 = and_or(h, u.h0, and_or(q, u.lo, u.magic));    // 1024 + q6
+  const uint32_t t1 = and_or(h, u.h1, and_or(q, u.hi, u.magic));    // 1024 + 16 q6
+  const uint32_t t2 = and_or(hs, u.h0, and_or(q2, u.lo, u.magic));
+  const uint32_t t3 = and_or(hs, u.h1, and_or(q2, u.hi, u.magic));
+  const half2_t h0 = (__builtin_bit_cast(half2_t, t0) - h2c(1056.f)) * dd;
+  const half2_t h1 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t1), h2c(0.0625f), h2c(-96.f)) * dd;
+  const half2_t h2 = (__builtin_bit_cast(half2_t, t2) - h2c(1056.f)) * dd;
+  const half2_t h3 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t3), h2c(0.0625f), h2c(-96.f)) * dd;
+  return pack8(h0, h1, h2, h3);
+}
+// The high bits of K run 2r+1 are stored rotated right by 8 in the dword of
+// run 2r (their bits are exactly the ones run 2r leaves free).
+__device__ __forceinline__ uint32_t rotl8(uint32_t h) { return __builtin_amdgcn_alignbit(h, h, 24); }
+
+// Q8_0: 8 bytes (stored q + 128) -> 8 f16 weights q * d.
+__device__ __forceinline__ half8_t unpack8_q8(uint32_t a, uint32_t b, uint32_t magic, half2_t dd) {
+  // v_perm: bytes 0-3 come from the second operand, 4-7 from the first.
+  // magic = 0x64006400: bytes 5 and 7 are 0x64, the f16 exponent of 1024.
+  const uint32_t t0 = __builtin_amdgcn_perm(magic, a, 0x07010500u);  // 1024 + u0, 1024 + u1
+  const uint32_t t1 = __builtin_amdgcn_perm(magic, a, 0x07030502u);
+  const uint32_t t2 = __builtin_amdgcn_perm(magic, b, 0x07010500u);
+  const uint32_t t3 = __builtin_amdgcn_perm(magic, b, 0x07030502u);
+  const half2_t h0 = (__builtin_bit_cast(half2_t, t0) - h2c(1152.f)) * dd;
+  const half2_t h1 = (__builtin_bit_cast(half2_t, t1) - h2c(1152.f)) * dd;
+  const half2_t h2 = (__builtin_bit_cast(half2_t, t2) - h2c(1152.f)) * dd;
+  const half2_t h3 = (__builtin_bit_cast(half2_t, t3) - h2c(1152.f)) * dd;
+  return pack8(h0, h1, h2, h3);
+}
+
+// f16 in the low (hi = false) or high half of `w`, broadcast to both halves.
+__device__ __forceinline__ half2_t bcast_half(uint32_t w, bool hi) {
+  return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(w, w, hi ? 0x03020302u : 0x01000100u));
+}
+// Two int8 (stored + 128) in bytes b, b+1 of w -> f16 pair, exactly.
+__device__ __forceinline__ half2_t i8pair(uint32_t w, uint32_t magic, bool upper) {
+  const uint32_t t = __builtin_amdgcn_perm(magic, w, upper ? 0x07030502u : 0x07010500u);
+  return __builtin_bit_cast(half2_t, t) - h2c(1152.f);
+}
+
+// LDS hand-off barrier: waits for this wave's LDS writes only, not for its
+// outstanding global loads (unlike __syncthreads(), whose release fence
+// drains the load counter).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // gfx9 encoding: lgkmcnt(0), vmcnt/expcnt unchanged
+  __builtin_amdgcn_s_barrier();
+}
+
+// Total order on (logit, row) for the argmax: larger logit first, then the
+// lower row.  NaN ranks as -inf and -0 as +0, so the maximum key is the first
+// index of the maximum over the non-NaN logits -- argmax_of's strict '>' scan.
+// A NaN in row 0 makes argmax_of return 0; that row gets the top key.
+__device__ __forceinline__ unsigned long long amax_key(float v, int row) {
+  if (row == 0 && v != v) return ~0ull;
+  if (v != v) v = -__builtin_inff();
+  if (v == 0.f) v = 0.f;
+  uint32_t x = __builtin_bit_cast(uint32_t, v);
+  x = (x & 0x80000000u) ? ~x : (x | 0x80000000u);
+  return ((unsigned long long)x << 32) | (0xFFFFFFFFu - (uint32_t)row);
+}
+__device__ __forceinline__ int amax_row(unsigned long long key) { return (int)(0xFFFFFFFFu - (uint32_t)key); }
+
+// Publish per-column argmax keys (atomic max, order-free), then the last
+// workgroup to arrive reads the column maxima, runs the greedy walk over the
+// drafts and clears the slots.  Runs with all 64*WAVES threads; `key[c]` is
+// valid in threads c < 16 of the calling workgroup.
+__device__ void argmax_finish(const unsigned long long *key, int B, const ArgmaxOut &a, int tid, int *s_flag) {
+  if (tid < B && key[tid] != 0)
+    __hip_atomic_fetch_max(a.keys + tid, key[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // maxima performed
+  __syncthreads();
+  if (tid == 0)
+    *s_flag = __hip_atomic_fetch_add(a.cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x * gridDim.y - 1;
+  __syncthreads();
+  if (!*s_flag) return;
+  if (tid == 0) {
+    int am[CWEN_BMAX];
+    for (int c = 0; c < B; ++c) {
+      am[c] = amax_row(__hip_atomic_load(a.keys + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      __hip_atomic_store(a.keys + c, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // run.c:4954-4956: k = longest prefix with argmax(row k) == draft k.
+    int k = 0;
+    while (k < a.E && am[k] == a.drafts[k]) ++k;
+    a.out[0] = k;
+    a.out[1] = am[k];
+    for (int c = 0; c < B; ++c) a.out[2 + c] = am[c];
+    __hip_atomic_store(a.cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+struct GemvParams {
+  const uint8_t *w;    // super-tiled weights
+  uint32_t wbytes;     // bytes of the tiled weights (buffer range)
+  int nsw;             // sides stored per super-tile position (1 or 2)
+  int side0;           // first side computed (NS == 1)
+  int M, nrg, nst;
+  int S, rps;          // K split across workgroups, super-tiles (rounds) per split
+  const _Float16 *xh;  // activations f16 [B][K]
+  uint32_t xbytes;     // B*K*2 (buffer range: columns >= B read as zero)
+  int K, B;
+  float *part;         // split-K partials
+  int *cnt;            // per row-tile arrival counters (zero between launches)
+  GemvOut out;
+};
+
+// FMT: weight format.  NS: sides per row group (2 = both halves of an
+// interleaved pair).  R: row groups per wave; each wave carries R*NS weight
+// streams.  EPI: epilogue.  CB: activation columns staged (4, 8 or 16; >= B).
+template <int FMT, int NS, int R, int EPI, int CB>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
+  using F = Fmt<FMT>;
+  constexpr int NSET = NS * R;
+  constexpr int XL = CB / WAVES;            // staging loads per wave per round
+  constexpr int TV = F::TV;
+  __shared__ uint4 act[2][16 * 64];         // [buf][column c][unit u ^ c], f16 x 8 per unit
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  // Wave index as a scalar: loop bounds and addresses are then provably
+  // wave-uniform, which keeps the loop's load-counter waits exact.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int rt = blockIdx.x / p.S;
+  const int sp = blockIdx.x - rt * p.S;
+  const int st0 = sp * p.rps;
+  const int nround = min(p.nst - st0, p.rps);
+
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.wbytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.xh, p.xbytes);
+
+  // Weight streams of this wave: set q = r*NS + s is row group rgs[r], side s.
+  const uint32_t sstride = (uint32_t)p.nsw * F::ST_BYTES;
+  uint32_t wofs[NSET];
+  int rgs[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    rgs[r] = (rt * WAVES + wave) * R + r;
+    const int rgc = rgs[r] < p.nrg ? rgs[r] : p.nrg - 1;  // idle streams read a valid tile
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      wofs[r * NS + s] = (((uint32_t)rgc * p.nst + st0) * p.nsw + (NS == 2 ? s : p.side0)) * F::ST_BYTES;
+  }
+  const uint32_t lq = lane * 16, ls = F::SC_OFS + lane * 8;
+
+  // Activation staging: this wave copies columns c = wave + WAVES*i; lane
+  // copies 16-byte unit `lane` of the column's 512-K chunk.
+  const uint32_t xround = Q4_ST_K * 2;
+  uint32_t xofs[XL];
+  int xslot[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int c = wave + WAVES * i;
+    xofs[i] = (uint32_t)c * (uint32_t)p.K * 2 + (uint32_t)st0 * xround + lane * 16;  // per lane: range-checked
+    xslot[i] = c * 64 + (lane ^ c);
+  }
+
+  // Loads of one round's weight data.  Tile u, vector v of a stream.
+  auto tile_ofs = [&](int u, int v) -> uint32_t {
+    return FMT == GEMV_Q8 ? lq + u * 2048 + v * 1024 : lq + u * 1024;
+  };
+
+  uint4 xs[XL];
+  uint4 wq[TILES][NSET][TV];
+  uint2 sc[NSET];
+  uint32_t dq[NSET];          // Q6_K: f16 d of the round's two super-blocks
+  uint4 hq[2][NSET];          // Q6_K: high bits of tile pairs (0,1) and (2,3)
+#pragma unroll
+  for (int q = 0; q < NSET; ++q) {
+    sc[q] = bload8(wr, ls, wofs[q]);
+    if constexpr (FMT == GEMV_Q6K) dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q], 0);
+  }
+#pragma unroll
+  for (int i = 0; i < XL; ++i) xs[i] = bload16(xr, xofs[i]);
+#pragma unroll
+  for (int j = 0; j < TILES; ++j) {
+#pragma unroll
+    for (int q = 0; q < NSET; ++q)
+#pragma unroll
+      for (int v = 0; v < TV; ++v) wq[j][q][v] = bload16(wr, tile_ofs(j, v), wofs[q]);
+    if constexpr (FMT == GEMV_Q6K) {
+      if (j & 1) {
+#pragma unroll
+        for (int q = 0; q < NSET; ++q) hq[j >> 1][q] = bload16(wr, F::HI_OFS + (j >> 1) * 1024 + lq, wofs[q]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // issue the ring in slot order
+  }
+#pragma unroll
+  for (int i = 0; i < XL; ++i) act[0][xslot[i]] = xs[i];
+  lds_barrier();
+
+  const Unpack uc = unpack_consts();
+  floatx4_t acc[NSET][2];
+#pragma unroll
+  for (int q = 0; q < NSET; ++q) acc[q][0] = acc[q][1] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+  // LDS unit of MFMA m of tile 0 for this lane (column n, K run 4g + m); tile
+  // j adds 16 units, which stay clear of the XOR (n < 16).
+  int aslot[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) aslot[m] = n * 64 + ((4 * g + m) ^ n);
+
+  // One round = one super-tile per stream.  The LDS buffer index is a
+  // template constant (the loop is unrolled by two), so every LDS address is
+  // a lane base plus an immediate.
+  auto round = [&](int rd, auto cur_c) __attribute__((always_inline)) {
+    constexpr int cur = decltype(cur_c)::value;
+    // Next round's super-tile (the last round re-reads its own, harmlessly).
+    const uint32_t nr = (uint32_t)(rd + 1 < nround ? rd + 1 : rd);
+    // Scales of this round: dd[q][tile][half] (Q4_0 / Q8_0: one per block,
+    // both halves equal; Q6_K: one per 16-weight sub-block).
+    half2_t dd[NSET][TILES][2];
+#pragma unroll
+    for (int q = 0; q < NSET; ++q) {
+      if constexpr (FMT == GEMV_Q6K) {
+        // sub-scale (exact in f16) * d, rounded once to f16
+        const half2_t d0 = bcast_half(dq[q], false), d1 = bcast_half(dq[q], true);
+#pragma unroll
+        for (int u = 0; u < TILES; ++u) {
+          const half2_t s2 = i8pair(u < 2 ? sc[q].x : sc[q].y, uc.magic, u & 1);
+          const half2_t ds = s2 * (u < 2 ? d0 : d1);
+          dd[q][u][0] = (half2_t){ds[0], ds[0]};
+          dd[q][u][1] = (half2_t){ds[1], ds[1]};
+        }
+      } else {
+        dd[q][0][0] = dd[q][0][1] = bcast_half(sc[q].x, false);
+        dd[q][1][0] = dd[q][1][1] = bcast_half(sc[q].x, true);
+        dd[q][2][0] = dd[q][2][1] = bcast_half(sc[q].y, false);
+        dd[q][3][0] = dd[q][3][1] = bcast_half(sc[q].y, true);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NSET; ++q) {
+      sc[q] = bload8(wr, ls, wofs[q] + nr * sstride);
+      if constexpr (FMT == GEMV_Q6K)
+        dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q] + nr * sstride, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < XL; ++i) xs[i] = bload16(xr, xofs[i], nr * xround);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < TILES; ++j) {
+      half8_t b[NSET][4];
+#pragma unroll
+      for (int q = 0; q < NSET; ++q) {
+        if constexpr (FMT == GEMV_Q4) {
+          b[q][0] = unpack8_q4(wq[j][q][0].x, uc, dd[q][j][0]);
+          b[q][1] = unpack8_q4(wq[j][q][0].y, uc, dd[q][j][0]);
+          b[q][2] = unpack8_q4(wq[j][q][0].z, uc, dd[q][j][0]);
+          b[q][3] = unpack8_q4(wq[j][q][0].w, uc, dd[q][j][0]);
+        } else if constexpr (FMT == GEMV_Q6K) {
+          const uint4 &h4 = hq[j >> 1][q];
+          const uint32_t ha = (j & 1) ? h4.z : h4.x;   // runs 0, 1
+          const uint32_t hb = (j & 1) ? h4.w : h4.y;   // runs 2, 3
+          b[q][0] = unpack8_q6(wq[j][q][0].x, ha, uc, dd[q][j][0]);
+          b[q][1] = unpack8_q6(wq[j][q][0].y, rotl8(ha), uc, dd[q][j][0]);
+          b[q][2] = unpack8_q6(wq[j][q][0].z, hb, uc, dd[q][j][1]);
+          b[q][3] = unpack8_q6(wq[j][q][0].w, rotl8(hb), uc, dd[q][j][1]);
+        } else {
+          b[q][0] = unpack8_q8(wq[j][q][0].x, wq[j][q][0].y, uc.magic, dd[q][j][0]);
+          b[q][1] = unpack8_q8(wq[j][q][0].z, wq[j][q][0].w, uc.magic, dd[q][j][0]);
+          b[q][2] = unpack8_q8(wq[j][q][1].x, wq[j][q][1].y, uc.magic, dd[q][j][0]);
+          b[q][3] = unpack8_q8(wq[j][q][1].z, wq[j][q][1].w, uc.magic, dd[q][j][0]);
+        }
+      }
+      // Refill the slots once their registers are consumed, so the loads
+      // land in the same registers (no loop-carried copies, no counter drain).
+#pragma unroll
+      for (int q = 0; q < NSET; ++q)
+#pragma unroll
+        for (int v = 0; v < TV; ++v) wq[j][q][v] = bload16(wr, tile_ofs(j, v), wofs[q] + nr * sstride);
+      if constexpr (FMT == GEMV_Q6K) {
+        if (j & 1) {
+#pragma unroll
+          for (int q = 0; q < NSET; ++q)
+            hq[j >> 1][q] = bload16(wr, F::HI_OFS + (j >> 1) * 1024 + lq, wofs[q] + nr * sstride);
+        }
+      }
+      half8_t a[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) a[m] = __builtin_bit_cast(half8_t, act[cur][aslot[m] + 16 * j]);
+#pragma unroll
+      for (int q = 0; q < NSET; ++q)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          acc[q][m & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b[q][m], acc[q][m & 1], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // keep slots in issue order
+    }
+#pragma unroll
+    for (int i = 0; i < XL; ++i) act[cur ^ 1][xslot[i]] = xs[i];
+    lds_barrier();
+  };
+  int rd = 0;
+  for (; rd + 1 < nround; rd += 2) {
+    round(rd, std::integral_constant<int, 0>{});
+    round(rd + 1, std::integral_constant<int, 1>{});
+  }
+  if (rd < nround) round(rd, std::integral_constant<int, 0>{});
+
+  floatx4_t res[NSET];
+#pragma unroll
+  for (int q = 0; q < NSET; ++q) res[q] = acc[q][0] + acc[q][1];
+
+  if (EPI != GEMV_EPI_ARGMAX && p.S > 1) {
+    // Publish this split's partials.  Agent-scope atomic stores reach the
+    // device coherence point; the wait makes them complete before the
+    // counter bump, and the last arriver reads them the same way.
+    const bool cols_on = g * 4 < p.B;
+    uint64_t *part = (uint64_t *)p.part;
+#pragma unroll
+    for (int q = 0; q < NSET; ++q) {
+      const size_t base = ((((size_t)rt * WAVES + wave) * NSET + q) * p.S + sp) * 128 + lane * 2;
+      if (cols_on) {
+        __hip_atomic_store(part + base, __builtin_bit_cast(uint64_t, (float2){res[q][0], res[q][1]}),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part + base + 1, __builtin_bit_cast(uint64_t, (float2){res[q][2], res[q][3]}),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // stores acknowledged
+    __builtin_amdgcn_s_barrier();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(p.cnt + rt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.S - 1;
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (!s_last) return;
+    // Sum the splits in split order.  The loads of a chunk of KCH splits are
+    // all issued before the first is consumed, so the reduction costs one
+    // memory round trip per chunk, not one per split.
+    constexpr int KCH = 8;
+#pragma unroll
+    for (int q = 0; q < NSET; ++q) res[q] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    if (cols_on) {
+      for (int k0 = 0; k0 < p.S; k0 += KCH) {
+        uint64_t lo[NSET][KCH], hi[NSET][KCH];
+#pragma unroll
+        for (int q = 0; q < NSET; ++q) {
+          const size_t base = ((((size_t)rt * WAVES + wave) * NSET + q) * p.S) * 128 + lane * 2;
+#pragma unroll
+          for (int u = 0; u < KCH; ++u) {
+            const size_t k = (size_t)min(k0 + u, p.S - 1);
+            lo[q][u] = __hip_atomic_load(part + base + k * 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            hi[q][u] = __hip_atomic_load(part + base + k * 128 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < NSET; ++q)
+#pragma unroll
+          for (int u = 0; u < KCH; ++u)
+            if (k0 + u < p.S) {
+              const float2 a = __builtin_bit_cast(float2, lo[q][u]);
+              const float2 b = __builtin_bit_cast(float2, hi[q][u]);
+              res[q] += (floatx4_t){a.x, a.y, b.x, b.y};
+            }
+      }
+    }
+    if (tid == 0) __hip_atomic_store(p.cnt + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  const GemvOut &o = p.out;
+  if constexpr (EPI == GEMV_EPI_ARGMAX) {
+    // Logits (optional), then the per-column argmax over this workgroup's
+    // rows: lane (g, n) holds row n of each row group for columns 4g..4g+3.
+    __shared__ unsigned long long s_key[WAVES][16];
+    unsigned long long best[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = rgs[r] * Q4_ROWS + n;
+      if (rgs[r] >= p.nrg || row >= p.M) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = g * 4 + e;
+        if (c < p.B && o.y) o.y[(size_t)c * o.ys + row] = res[r][e];
+        const unsigned long long k = amax_key(res[r][e], row);
+        best[e] = k > best[e] ? k : best[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int sh = 1; sh < 16; sh <<= 1) {
+        const unsigned long long other = __shfl_xor(best[e], sh, 16);
+        best[e] = other > best[e] ? other : best[e];
+      }
+    }
+    if (n == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s_key[wave][g * 4 + e] = best[e];
+    }
+    __syncthreads();
+    __shared__ unsigned long long s_col[16];
+    if (tid < 16) {
+      unsigned long long k = s_key[0][tid];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) k = s_key[w][tid] > k ? s_key[w][tid] : k;
+      s_col[tid] = k;
+    }
+    __syncthreads();
+    argmax_finish(s_col, p.B, o.am, tid, &s_last);
+    return;
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = rgs[r] * Q4_ROWS + n;
+    if (rgs[r] >= p.nrg || row >= p.M) continue;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a0 = res[r * NS][e];
+      v[e] = (EPI == GEMV_EPI_SWIGLU) ? silu_f(a0) * res[r * NS + NS - 1][e] : a0;
+    }
+    if (o.y && o.accumulate) {  // all residual loads in flight together
+      float old[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = g * 4 + e;
+        old[e] = c < p.B ? o.y[(size_t)c * o.ys + row] : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += old[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = g * 4 + e;
+      if (c >= p.B) continue;
+      if (o.y) o.y[(size_t)c * o.ys + row] = v[e];
+      if (o.yh) o.yh[(size_t)c * p.M + row] = (_Float16)v[e];
+      if (EPI == GEMV_EPI_PAIR) o.y1[(size_t)c * o.ys + row] = res[r * NS + NS - 1][e];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ repack
+// One thread per (row group, super-tile, side, lane).  Rows past M get zero
+// weights (zero scales).
+
+// Q4_0 family: lane l = 16g + n gets, for each tile u, block g of that tile
+// for row n -- 4 dwords, dword j holding K run j (weights 8j..8j+7 of the
+// block) in kNibPos order -- and the 4 blocks' f16 scales.
+__global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_t *sc, int type,
+                                 int M, int K, int nrg, int nst, int nsw) {
+  const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t total = (size_t)nrg * nst * nsw * 64;
+  if (id >= total) return;
+  const int lane = (int)(id & 63);
+  size_t t = id >> 6;
+  const int side = (int)(t % nsw); t /= nsw;
+  const int st = (int)(t % nst);
+  const int rg = (int)(t / nst);
+  const int n = lane & 15, g = lane >> 4;
+  const int row = rg * Q4_ROWS + n;
+  const int nb = K / 32;
+  uint8_t *stile = dst + (((size_t)rg * nst + st) * nsw + side) * Fmt<GEMV_Q4>::ST_BYTES;
+  uint16_t d[TILES];
+  for (int u = 0; u < TILES; ++u) {
+    const int blk = (st * TILES + u) * 4 + g;
+    const uint8_t *qs = nullptr;
+    d[u] = 0;
+    if (row < M) {
+      const size_t bi = (size_t)row * nb + blk;
+      if (type == CWEN_T_Q4_0) {
+        const uint8_t *b = src + bi * 18;
+        d[u] = (uint16_t)(b[0] | (b[1] << 8));
+        qs = b + 2;
+      } else if (type == CWEN_T_Q4_0RS) {
+        qs = src + bi * 16;
+        d[u] = sc[bi];
+      } else {  // Q4_0RSI
+        qs = src + bi * 32 + side * 16;
+        d[u] = sc[bi * 2 + side];
+      }
+    }
+    uint32_t out[4];
+    for (int j = 0; j < 4; ++j) {
+      uint32_t word = 0;
+      for (int e = 0; e < 8; ++e) {
+        const int k = j * 8 + e;  // weight index inside the 32-weight block
+        uint32_t nib = 8;
+        if (qs) nib = (k < 16) ? (qs[k] & 0xFu) : (qs[k - 16] >> 4);
+        word |= nib << (4 * kNibPos[e]);
+      }
+      out[j] = word;
+    }
+    *(uint4 *)(stile + u * 1024 + lane * 16) = make_uint4(out[0], out[1], out[2], out[3]);
+  }
+  *(uint2 *)(stile + Fmt<GEMV_Q4>::SC_OFS + lane * 8) =
+      make_uint2((uint32_t)d[0] | ((uint32_t)d[1] << 16), (uint32_t)d[2] | ((uint32_t)d[3] << 16));
+}
+
+// Q6_K (run.c:115, 1212-1229): weight j of a super-block (j = 0..255) is
+// q6 = (nibble of ql[64h + l + 32(t&1)], low for t < 2) | ((qh[32h + l] >> 2t) & 3) << 4
+// with h = j/128, t = (j%128)/32, l = j%32, times d * sc[j/16].
+__device__ inline int q6_value(const uint8_t *b, int j) {
+  const int h = j >> 7, r = j & 127, t = r >> 5, l = r & 31;
+  const uint8_t qlb = b[64 * h + l + 32 * (t & 1)];
+  const int nib = (t < 2) ? (qlb & 0xF) : (qlb >> 4);
+  const int hb = (b[128 + 32 * h + l] >> (2 * t)) & 3;
+  return nib | (hb << 4);
+}
+// Bit position of weight e's high pair in the run's dword (see unpack8_q6).
+__constant__ int kQ6HiPos[8] = {4, 20, 8, 24, 6, 22, 10, 26};
+
+__global__ void repack_q6k_kernel(uint8_t *dst, const uint8_t *src, int M, int K, int nrg, int nst) {
+  const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t total = (size_t)nrg * nst * 64;
+  if (id >= total) return;
+  const int lane = (int)(id & 63);
+  const size_t t = id >> 6;
+  const int st = (int)(t % nst);
+  const int rg = (int)(t / nst);
+  const int n = lane & 15, g = lane >> 4;
+  const int row = rg * Q4_ROWS + n;
+  const int nsb = K / 256;
+  using F = Fmt<GEMV_Q6K>;
+  uint8_t *stile = dst + ((size_t)rg * nst + st) * F::ST_BYTES;
+  uint8_t scb[8];
+  uint32_t hiw[TILES][2];
+  for (int u = 0; u < TILES; ++u) {
+    const int k0 = st * Q4_ST_K + u * Q4_TILE_K + g * 32;   // first K of the lane's block
+    const uint8_t *b = (row < M) ? src + ((size_t)row * nsb + k0 / 256) * 210 : nullptr;
+    const int j0 = k0 & 255;
+    uint32_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+    for (int m = 0; m < 4; ++m)
+      for (int e = 0; e < 8; ++e) {
+        const int v = b ? q6_value(b, j0 + 8 * m + e) : 32;   // 32: weight 0
+        lo[m] |= (uint32_t)(v & 15) << (4 * kNibPos[e]);
+        hi[m] |= (uint32_t)(v >> 4) << kQ6HiPos[e];
+      }
+    *(uint4 *)(stile + u * 1024 + lane * 16) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    // runs 2r+1 rotated right by 8 into the free bits of run 2r
+    hiw[u][0] = hi[0] | ((hi[1] >> 8) | (hi[1] << 24));
+    hiw[u][1] = hi[2] | ((hi[3] >> 8) | (hi[3] << 24));
+    for (int h = 0; h < 2; ++h) {
+      const int sub = (j0 >> 4) + h;
+      scb[u * 2 + h] = (uint8_t)((b ? (int)(int8_t)b[192 + sub] : 0) + 128);
+    }
+  }
+  for (int p = 0; p < 2; ++p)
+    *(uint4 *)(stile + F::HI_OFS + p * 1024 + lane * 16) =
+        make_uint4(hiw[2 * p][0], hiw[2 * p][1], hiw[2 * p + 1][0], hiw[2 * p + 1][1]);
+  uint2 scw;
+  scw.x = scb[0] | (scb[1] << 8) | (scb[2] << 16) | ((uint32_t)scb[3] << 24);
+  scw.y = scb[4] | (scb[5] << 8) | (scb[6] << 16) | ((uint32_t)scb[7] << 24);
+  *(uint2 *)(stile + F::SC_OFS + lane * 8) = scw;
+  if (g == 0) {  // d of the super-tile's two super-blocks for row n
+    uint16_t d0 = 0, d1 = 0;
+    if (row < M) {
+      const uint8_t *b0 = src + ((size_t)row * nsb + st * 2) * 210;
+      d0 = (uint16_t)(b0[208] | (b0[209] << 8));
+      d1 = (uint16_t)(b0[210 + 208] | (b0[210 + 209] << 8));
+    }
+    *(uint32_t *)(stile + F::D_OFS + n * 4) = (uint32_t)d0 | ((uint32_t)d1 << 16);
+  }
+}
+
+// Q8_0 (run.c:106, 1248-1274): lane l = 16g + n gets block g of each tile
+// for row n as two 16-byte halves (bytes stored q + 128), and the 4 blocks'
+// f16 scales.
+__global__ void repack_q8_kernel(uint8_t *dst, const uint8_t *src, int M, int K, int nrg, int nst) {
+  const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t total = (size_t)nrg * nst * 64;
+  if (id >= total) return;
+  const int lane = (int)(id & 63);
+  const size_t t = id >> 6;
+  const int st = (int)(t % nst);
+  const int rg = (int)(t / nst);
+  const int n = lane & 15, g = lane >> 4;
+  const int row = rg * Q4_ROWS + n;
+  const int nb = K / 32;
+  using F = Fmt<GEMV_Q8>;
+  uint8_t *stile = dst + ((size_t)rg * nst + st) * F::ST_BYTES;
+  uint16_t d[TILES];
+  for (int u = 0; u < TILES; ++u) {
+    const int blk = (st * TILES + u) * 4 + g;
+    const uint8_t *b = (row < M) ? src + ((size_t)row * nb + blk) * 34 : nullptr;
+    d[u] = b ? (uint16_t)(b[0] | (b[1] << 8)) : 0;
+    uint8_t v[32];
+    for (int k = 0; k < 32; ++k) v[k] = (uint8_t)((b ? (int)(int8_t)b[2 + k] : 0) + 128);
+    for (int h = 0; h < 2; ++h) {
+      uint32_t w4[4];
+      for (int i = 0; i < 4; ++i)
+        w4[i] = v[16 * h + 4 * i] | (v[16 * h + 4 * i + 1] << 8) | (v[16 * h + 4 * i + 2] << 16) |
+                ((uint32_t)v[16 * h + 4 * i + 3] << 24);
+      *(uint4 *)(stile + u * 2048 + h * 1024 + lane * 16) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    }
+  }
+  *(uint2 *)(stile + F::SC_OFS + lane * 8) =
+      make_uint2((uint32_t)d[0] | ((uint32_t)d[1] << 16), (uint32_t)d[2] | ((uint32_t)d[3] << 16));
+}
+
+__global__ void act_to_f16_kernel(const float *x, int xs, _Float16 *xh, int K, int B) {
+  const int k4 = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int c = blockIdx.y;
+  if (k4 >= K || c >= B) return;
+  const float4 v = *(const float4 *)(x + (size_t)c * xs + k4);
+  const half2_t a = {(_Float16)v.x, (_Float16)v.y}, b = {(_Float16)v.z, (_Float16)v.w};
+  *(uint2 *)(xh + (size_t)c * K + k4) = make_uint2(__builtin_bit_cast(uint32_t, a),
+                                                   __builtin_bit_cast(uint32_t, b));
+}
+
+// Argmax of B rows of given logits plus the walk: grid (chunks, B); each
+// workgroup scans one chunk of one row.
+constexpr int AM_CHUNK = 8192;
+__global__ __launch_bounds__(256) void argmax_walk_kernel(const float *lg, long ls, int V, int B, ArgmaxOut a) {
+  __shared__ unsigned long long s_k[256];
+  __shared__ unsigned long long s_col[CWEN_BMAX];
+  __shared__ int s_flag;
+  const int tid = threadIdx.x;
+  const int b = blockIdx.y;
+  const int i0 = blockIdx.x * AM_CHUNK;
+  const int i1 = min(V, i0 + AM_CHUNK);
+  const float *row = lg + (size_t)b * ls;
+  unsigned long long best = 0;
+  for (int i = i0 + tid; i < i1; i += 256) {
+    const unsigned long long k = amax_key(row[i], i);
+    best = k > best ? k : best;
+  }
+  s_k[tid] = best;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) s_k[tid] = s_k[tid + s] > s_k[tid] ? s_k[tid + s] : s_k[tid];
+    __syncthreads();
+  }
+  // Only column b carries a key; the others stay 0 (no-op maxima).
+  if (tid < CWEN_BMAX) s_col[tid] = tid == b ? s_k[0] : 0ull;
+  __syncthreads();
+  argmax_finish(s_col, B, a, tid, &s_flag);
+}
+
+template <int FMT, int NS, int R, int EPI, int CB>
+void launch_one(const GemvParams &p, int nrt, hipStream_t st) {
+  hipLaunchKernelGGL((gemv_kernel<FMT, NS, R, EPI, CB>), dim3((unsigned)(nrt * p.S)), dim3(64 * WAVES), 0,
+                     st, p);
+}
+
+template <int FMT, int NS, int R, int EPI>
+void launch_cb(const GemvParams &p, int nrt, hipStream_t st) {
+  if (p.B <= 4) launch_one<FMT, NS, R, EPI, 4>(p, nrt, st);
+  else if (p.B <= 8) launch_one<FMT, NS, R, EPI, 8>(p, nrt, st);
+  else launch_one<FMT, NS, R, EPI, 16>(p, nrt, st);
+}
+
+template <int FMT>
+int launch_fmt(const GemvParams &p, int nrt, int R, int nsides, int epi, hipStream_t st) {
+  if (nsides == 1 && epi == GEMV_EPI_STORE) {
+    if (R == 2) launch_cb<FMT, 1, 2, GEMV_EPI_STORE>(p, nrt, st);
+    else launch_cb<FMT, 1, 1, GEMV_EPI_STORE>(p, nrt, st);
+  } else if (nsides == 1 && epi == GEMV_EPI_ARGMAX) {
+    if (R == 2) launch_cb<FMT, 1, 2, GEMV_EPI_ARGMAX>(p, nrt, st);
+    else launch_cb<FMT, 1, 1, GEMV_EPI_ARGMAX>(p, nrt, st);
+  } else {
+    return CWEN_EINVAL;
+  }
+  return CWEN_OK;
+}
+
+}  // namespace
+
+int gemv_fmt_of(int type) {
+  switch (type) {
+    case CWEN_T_Q4_0: case CWEN_T_Q4_0RS: case CWEN_T_Q4_0RSI: return GEMV_Q4;
+    case CWEN_T_Q6_K: return GEMV_Q6K;
+    case CWEN_T_Q8_0: return GEMV_Q8;
+    default: return -1;
+  }
+}
+
+size_t gemv_st_bytes(int fmt) {
+  return fmt == GEMV_Q4 ? Fmt<GEMV_Q4>::ST_BYTES : fmt == GEMV_Q6K ? Fmt<GEMV_Q6K>::ST_BYTES
+                                                                   : Fmt<GEMV_Q8>::ST_BYTES;
+}
+
+int gemv_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStream_t st) {
+  const size_t threads = (size_t)w->nrg * w->nst * w->nside * 64;
+  const int blk = 256;
+  const size_t grid = (threads + blk - 1) / blk;
+  if (w->fmt == GEMV_Q4)
+    hipLaunchKernelGGL(repack_q4_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, dsc,
+                       w->type, w->ne1, w->ne0, w->nrg, w->nst, w->nside);
+  else if (w->fmt == GEMV_Q6K)
+    hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, w->ne1,
+                       w->ne0, w->nrg, w->nst);
+  else
+    hipLaunchKernelGGL(repack_q8_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, w->ne1,
+                       w->ne0, w->nrg, w->nst);
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}
+
+// Launch shape from the weight's shape only (never from B), so every output
+// bit is independent of the block size.  rows: row groups per wave for
+// single-sided use; split: K split across workgroups; rps: super-tiles per split.
+void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
+  const int R = (w->nside == 1 && w->nrg >= 2 * WAVES * 32) ? 2 : 1;
+  // A pair is computed two-sided (R = 1); single-side calls on it use R = 1 too.
+  const int Rs = (w->nside == 1) ? R : 1;
+  const int nrt = (w->nrg + WAVES * Rs - 1) / (WAVES * Rs);
+  const int nrd = w->nst;                            // rounds of K
+  int S = (ctx->wg_target + nrt - 1) / nrt;
+  if (S > nrd / 2) S = nrd / 2;                      // keep >= 2 rounds per split
+  if (S < 1) S = 1;
+  const int rps = (nrd + S - 1) / S;
+  w->rows = Rs;
+  w->rps = rps;
+  w->split = (nrd + rps - 1) / rps;
+}
+
+int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
+                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st) {
+  GemvParams p;
+  p.w = w->dev;
+  p.wbytes = (uint32_t)w->bytes;
+  p.nsw = w->nside;
+  p.side0 = side0;
+  p.M = w->ne1;
+  p.nrg = w->nrg;
+  p.nst = w->nst;
+  p.S = w->split;
+  p.rps = w->rps;
+  p.xh = xh;
+  p.xbytes = (uint32_t)((size_t)B * w->ne0 * 2);
+  p.K = w->ne0;
+  p.B = B;
+  p.part = ctx->partials;
+  p.cnt = ctx->counters;
+  p.out = out;
+  const int R = w->rows;
+  const int nrt = (w->nrg + WAVES * R - 1) / (WAVES * R);
+  if (epi == GEMV_EPI_ARGMAX) {
+    // The argmax needs final row values in one workgroup: no K split.
+    if (p.S != 1) {
+      p.S = 1;
+      p.rps = w->nst;
+    }
+  } else if (p.S > 1) {
+    const size_t need = (size_t)nrt * WAVES * R * nsides * p.S * 256;
+    if (need > ctx->partials_floats || nrt > ctx->ncounters) return CWEN_ESCRATCH;
+  }
+  int rc = CWEN_EINVAL;
+  if (w->fmt == GEMV_Q4) {
+    if (nsides == 2 && epi == GEMV_EPI_PAIR) {
+      launch_cb<GEMV_Q4, 2, 1, GEMV_EPI_PAIR>(p, nrt, st);
+      rc = CWEN_OK;
+    } else if (nsides == 2 && epi == GEMV_EPI_SWIGLU) {
+      launch_cb<GEMV_Q4, 2, 1, GEMV_EPI_SWIGLU>(p, nrt, st);
+      rc = CWEN_OK;
+    } else {
+      rc = launch_fmt<GEMV_Q4>(p, nrt, R, nsides, epi, st);
+    }
+  } else if (w->fmt == GEMV_Q6K) {
+    rc = launch_fmt<GEMV_Q6K>(p, nrt, R, nsides, epi, st);
+  } else if (w->fmt == GEMV_Q8) {
+    rc = launch_fmt<GEMV_Q8>(p, nrt, R, nsides, epi, st);
+  }
+  if (rc) return rc;
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}
+
+int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st) {
+  const int threads = 256;
+  const dim3 grid((unsigned)((K / 4 + threads - 1) / threads), (unsigned)B);
+  hipLaunchKernelGGL(act_to_f16_kernel, grid, dim3(threads), 0, st, x, xs, xh, K, B);
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}
+
+int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &a, hipStream_t st) {
+  const dim3 grid((unsigned)((V + AM_CHUNK - 1) / AM_CHUNK), (unsigned)B);
+  hipLaunchKernelGGL(argmax_walk_kernel, grid, dim3(256), 0, st, lg, ls, V, B, a);
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}

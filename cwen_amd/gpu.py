@@ -36,6 +36,8 @@ SIGNATURES = [
     ("cwen_act_to_f16", _I, [_VP, _VP, _I, _VP, _I, _I, _VP]),
     ("cwen_gemvb_f16", _I, [_VP, _VP, _I, _VP, _VP, _I, _VP, _I, _I, _VP]),
     ("cwen_gemvb_swiglu_f16", _I, [_VP, _VP, _VP, _VP, _I, _VP, _I, _VP]),
+    ("cwen_head_verify", _I, [_VP, _VP, _VP, _I, _I, _VP, _I, _VP, _I, _VP, _VP]),
+    ("cwen_argmax_walk", _I, [_VP, _VP, _I, _I, _I, _VP, _I, _VP, _VP]),
 ]
 
 
@@ -182,3 +184,20 @@ def gemvb_swiglu_f16(ctx: Context, W: Weight, Xh, H, B: int, Hh=None, hs: int | 
     hs = W.M if hs is None else hs
     check("cwen_gemvb_swiglu_f16", lib().cwen_gemvb_swiglu_f16(ctx.h, W.h, _ptr(Xh), _ptr(H), hs, _ptr(Hh),
                                                                B, _stream(stream)))
+
+
+def head_verify(ctx: Context, W: Weight, X, B: int, res, drafts=None, E: int = 0, logits=None,
+                xs: int | None = None, ls: int | None = None, stream=None) -> None:
+    """Head GEMV + per-column argmax + greedy walk; res (device int32 [2+B]) gets
+    k, bonus, argmax of each column."""
+    xs = W.K if xs is None else xs
+    ls = W.M if ls is None else ls
+    check("cwen_head_verify", lib().cwen_head_verify(ctx.h, W.h, _ptr(X), xs, B, _ptr(drafts), E,
+                                                     _ptr(logits), ls, _ptr(res), _stream(stream)))
+
+
+def argmax_walk(ctx: Context, logits, V: int, B: int, res, drafts=None, E: int = 0, ls: int | None = None,
+                stream=None) -> None:
+    ls = V if ls is None else ls
+    check("cwen_argmax_walk", lib().cwen_argmax_walk(ctx.h, _ptr(logits), ls, V, B, _ptr(drafts), E,
+                                                     _ptr(res), _stream(stream)))

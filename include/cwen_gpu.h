@@ -65,6 +65,8 @@ int cwen_ctx_destroy(cwen_ctx *ctx);
 
 /* Upload one weight matrix given in a reference layout in HOST memory and
  * repack it on the device into the tile layout the kernels stream.
+ * Types: Q4_0, Q4_0RS, Q4_0RSI, Q6_K, Q8_0; ne0 (K) must be a multiple of 512
+ * and at most CWEN_KMAX.
  * `data`/`scales` are what the reference's Tensor.data / Tensor.scales point
  * at (run.c:132): for Q4_0RS and Q4_0RSI `scales` is the f16 scale channel,
  * for the self-contained GGUF types it is NULL.  ne0 = K (inputs), ne1 = M
@@ -108,6 +110,27 @@ int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int x
  * gate/up launch writes them straight into the down launch's operand format. */
 int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd,
                    const float *X, int xs, float *Y, int ys, int B, void *stream);
+
+/* LM head + acceptance of one verify block, on the device.  logits_b = W . X_b
+ * for b < B (W: the output head, M = vocab rows, any uploaded single-sided
+ * type), then the per-column argmax -- argmax_of (run.c:2647-2668): the first
+ * index of the maximum, NaN logits ignored, 0 when logit 0 is NaN -- and the
+ * greedy prefix walk of generate_tokens_spec (run.c:4954-4956): k = the
+ * longest prefix with argmax(row k) == drafts[k], k <= E, bonus =
+ * argmax(row k).  `drafts` (device, E <= B-1 ids) is blk[1..E] of the
+ * reference.  Writes the DEVICE int array res: res[0] = k, res[1] = bonus,
+ * res[2 + b] = argmax(row b).  `logits` (device f32 [b*ls + v], nullable)
+ * receives the logits; with NULL they never leave the chip.  Replaces
+ * gemvb(&output, ...) of forward_block (run.c:2773-2777) + argmax_of + the
+ * walk loop. */
+int cwen_head_verify(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, int B,
+                     const int *drafts, int E, float *logits, int ls, int *res, void *stream);
+
+/* The same argmax + walk over given device logits [b*ls + v], v < V: the
+ * reference's argmax_of per row and the walk loop (run.c:2647-2668,
+ * 4954-4956), res as for cwen_head_verify. */
+int cwen_argmax_walk(cwen_ctx *ctx, const float *logits, int ls, int V, int B, const int *drafts,
+                     int E, int *res, void *stream);
 
 /* ---- f16 activation operands ----
  * The kernels read activations as IEEE half, row-major [B][K] with row stride
