@@ -284,4 +284,85 @@ int cwen_argmax_walk(cwen_ctx *ctx, const float *logits, int ls, int V, int B, c
   return argmax_walk_launch(logits, ls, V, B, a, (hipStream_t)stream);
 }
 
+int cwen_gdn_create(cwen_ctx *ctx, int nkh, int nvh, int dk, cwen_gdn **out) {
+  if (!ctx || !out || nkh <= 0 || nvh <= 0 || nvh % nkh || dk != 128) return CWEN_EINVAL;
+  *out = nullptr;
+  CWEN_HIP_TRY(hipSetDevice(ctx->device));
+  cwen_gdn *g = (cwen_gdn *)calloc(1, sizeof(cwen_gdn));
+  if (!g) return CWEN_ENOMEM;
+  g->ctx = ctx;
+  g->nkh = nkh; g->nvh = nvh; g->dk = dk;
+  g->C = (2 * nkh + nvh) * dk;
+  g->nslot = CWEN_BMAX + 1;
+  const size_t sf = (size_t)nvh * dk * dk, hf = (size_t)g->C * 3;
+  if (hipMalloc((void **)&g->S, sf * g->nslot * sizeof(float)) != hipSuccess ||
+      hipMalloc((void **)&g->H, hf * g->nslot * sizeof(float)) != hipSuccess) {
+    if (g->S) (void)hipFree(g->S);
+    free(g);
+    return CWEN_ENOMEM;
+  }
+  if (hipMemset(g->S, 0, sf * sizeof(float)) != hipSuccess ||
+      hipMemset(g->H, 0, hf * sizeof(float)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    cwen_gdn_free(g);
+    return CWEN_EHIP;
+  }
+  *out = g;
+  return CWEN_OK;
+}
+
+int cwen_gdn_free(cwen_gdn *g) {
+  if (!g) return CWEN_EINVAL;
+  (void)hipSetDevice(g->ctx->device);
+  (void)hipDeviceSynchronize();
+  if (g->S) (void)hipFree(g->S);
+  if (g->H) (void)hipFree(g->H);
+  free(g);
+  return CWEN_OK;
+}
+
+int cwen_gdn_set_state(cwen_gdn *g, const float *S, const float *hist) {
+  if (!g) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipSetDevice(g->ctx->device));
+  const size_t sf = (size_t)g->nvh * g->dk * g->dk, hf = (size_t)g->C * 3;
+  float *Sd = g->S + (size_t)g->cur * sf, *Hd = g->H + (size_t)g->cur * hf;
+  if (S) CWEN_HIP_TRY(hipMemcpy(Sd, S, sf * sizeof(float), hipMemcpyHostToDevice));
+  else CWEN_HIP_TRY(hipMemset(Sd, 0, sf * sizeof(float)));
+  if (hist) CWEN_HIP_TRY(hipMemcpy(Hd, hist, hf * sizeof(float), hipMemcpyHostToDevice));
+  else CWEN_HIP_TRY(hipMemset(Hd, 0, hf * sizeof(float)));
+  CWEN_HIP_TRY(hipDeviceSynchronize());
+  g->last_B = 0;
+  return CWEN_OK;
+}
+
+int cwen_gdn_get_state(cwen_gdn *g, int pos, float *S, float *hist) {
+  if (!g || pos < 0 || pos > g->last_B) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipSetDevice(g->ctx->device));
+  CWEN_HIP_TRY(hipDeviceSynchronize());
+  const size_t sf = (size_t)g->nvh * g->dk * g->dk, hf = (size_t)g->C * 3;
+  const int slot = (g->cur + pos) % g->nslot;
+  if (S) CWEN_HIP_TRY(hipMemcpy(S, g->S + (size_t)slot * sf, sf * sizeof(float), hipMemcpyDeviceToHost));
+  if (hist) CWEN_HIP_TRY(hipMemcpy(hist, g->H + (size_t)slot * hf, hf * sizeof(float), hipMemcpyDeviceToHost));
+  return CWEN_OK;
+}
+
+int cwen_gdn_block(cwen_ctx *ctx, cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
+                   const float *decay, const float *beta, int gs, const float *kw, const float *wn,
+                   float *out, int os, int B, void *stream) {
+  if (!ctx || !g || g->ctx != ctx || B < 1 || B > CWEN_BMAX) return CWEN_EINVAL;
+  if (!qkv || !z || !decay || !beta || !kw || !wn || !out) return CWEN_EINVAL;
+  const int zh = g->nvh * g->dk;
+  if ((B > 1 && (qs < g->C || zs < zh || gs < g->nvh || os < zh)) || qs < 0 || zs < 0 || gs < 0 || os < 0)
+    return CWEN_EINVAL;
+  int rc = gdn_block_launch(g, qkv, qs, z, zs, decay, beta, gs, kw, wn, out, os, B, (hipStream_t)stream);
+  if (rc == CWEN_OK) g->last_B = B;
+  return rc;
+}
+
+int cwen_gdn_commit(cwen_gdn *g, int n) {
+  if (!g || n < 0 || n > g->last_B) return CWEN_EINVAL;
+  g->cur = (g->cur + n) % g->nslot;
+  g->last_B = 0;
+  return CWEN_OK;
+}
+
 }  // extern "C"

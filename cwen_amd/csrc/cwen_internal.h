@@ -49,6 +49,16 @@ struct cwen_weight {
   int rows;                 // row groups per wave (shape-only)
 };
 
+// GatedDeltaNet layer state: a ring of nslot snapshots of the recurrent state
+// [nvh][dk][dk] and the conv history [C][3]; slot `cur` is the current state.
+struct cwen_gdn {
+  cwen_ctx *ctx;
+  int nkh, nvh, dk, C;
+  int nslot, cur;
+  int last_B;               // positions of the last block (commit bound)
+  float *S, *H;             // device slot rings
+};
+
 #define CWEN_HIP_TRY(expr)                                   \
   do {                                                       \
     hipError_t _e = (expr);                                  \
@@ -98,3 +108,8 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
                 const _Float16 *xh, const GemvOut &out, int B, hipStream_t st);
 int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st);
 int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &a, hipStream_t st);
+
+// ------------------------------------------------------------ gdn.hip
+int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
+                     const float *decay, const float *beta, int gs, const float *kw, const float *wn,
+                     float *out, int os, int B, hipStream_t st);

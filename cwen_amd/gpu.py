@@ -38,6 +38,12 @@ SIGNATURES = [
     ("cwen_gemvb_swiglu_f16", _I, [_VP, _VP, _VP, _VP, _I, _VP, _I, _VP]),
     ("cwen_head_verify", _I, [_VP, _VP, _VP, _I, _I, _VP, _I, _VP, _I, _VP, _VP]),
     ("cwen_argmax_walk", _I, [_VP, _VP, _I, _I, _I, _VP, _I, _VP, _VP]),
+    ("cwen_gdn_create", _I, [_VP, _I, _I, _I, C.POINTER(_VP)]),
+    ("cwen_gdn_free", _I, [_VP]),
+    ("cwen_gdn_set_state", _I, [_VP, _VP, _VP]),
+    ("cwen_gdn_get_state", _I, [_VP, _I, _VP, _VP]),
+    ("cwen_gdn_block", _I, [_VP, _VP, _VP, _I, _VP, _I, _VP, _VP, _I, _VP, _VP, _VP, _I, _I, _VP]),
+    ("cwen_gdn_commit", _I, [_VP, _I]),
 ]
 
 
@@ -201,3 +207,47 @@ def argmax_walk(ctx: Context, logits, V: int, B: int, res, drafts=None, E: int =
     ls = V if ls is None else ls
     check("cwen_argmax_walk", lib().cwen_argmax_walk(ctx.h, _ptr(logits), ls, V, B, _ptr(drafts), E,
                                                      _ptr(res), _stream(stream)))
+
+
+class GDN:
+    """One GatedDeltaNet layer's device state with its snapshot ring."""
+
+    def __init__(self, ctx: Context, nkh: int, nvh: int, dk: int = 128):
+        h = C.c_void_p()
+        check("cwen_gdn_create", lib().cwen_gdn_create(ctx.h, nkh, nvh, dk, C.byref(h)))
+        self.h, self.ctx, self.nkh, self.nvh, self.dk = h, ctx, nkh, nvh, dk
+        self.C = (2 * nkh + nvh) * dk
+
+    def set_state(self, S: np.ndarray | None, hist: np.ndarray | None) -> None:
+        S = None if S is None else np.ascontiguousarray(S, dtype=np.float32)
+        hist = None if hist is None else np.ascontiguousarray(hist, dtype=np.float32)
+        check("cwen_gdn_set_state", lib().cwen_gdn_set_state(
+            self.h, None if S is None else S.ctypes.data, None if hist is None else hist.ctypes.data))
+
+    def get_state(self, pos: int = 0) -> tuple[np.ndarray, np.ndarray]:
+        S = np.empty((self.nvh, self.dk, self.dk), dtype=np.float32)
+        hist = np.empty((self.C, 3), dtype=np.float32)
+        check("cwen_gdn_get_state", lib().cwen_gdn_get_state(self.h, pos, S.ctypes.data, hist.ctypes.data))
+        return S, hist
+
+    def block(self, qkv, z, decay, beta, kw, wn, out, B: int, qs=None, zs=None, gs=None, os_=None,
+              stream=None) -> None:
+        zh = self.nvh * self.dk
+        check("cwen_gdn_block", lib().cwen_gdn_block(
+            self.ctx.h, self.h, _ptr(qkv), self.C if qs is None else qs, _ptr(z), zh if zs is None else zs,
+            _ptr(decay), _ptr(beta), self.nvh if gs is None else gs, _ptr(kw), _ptr(wn), _ptr(out),
+            zh if os_ is None else os_, B, _stream(stream)))
+
+    def commit(self, n: int) -> None:
+        check("cwen_gdn_commit", lib().cwen_gdn_commit(self.h, n))
+
+    def free(self) -> None:
+        if self.h:
+            lib().cwen_gdn_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -132,6 +132,41 @@ int cwen_head_verify(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs
 int cwen_argmax_walk(cwen_ctx *ctx, const float *logits, int ls, int V, int B, const int *drafts,
                      int E, int *res, void *stream);
 
+/* ---- GatedDeltaNet block verify ----
+ * One linear-attention layer's recurrent state [nvh][dk][dk] (row = key
+ * dimension) and conv history [C][3], C = (2*nkh + nvh)*dk, device-resident
+ * in a ring of CWEN_BMAX+1 snapshot slots.  Replaces one layer's Srec/Cstate
+ * and the snapshot copies SnapS/SnapC (run.c:171-172, 204, 3931-3932,
+ * 2787-2809).  dk must be 128 and nvh a multiple of nkh (key head of value
+ * head hv: hv % nkh, run.c:2027). */
+typedef struct cwen_gdn cwen_gdn;
+int cwen_gdn_create(cwen_ctx *ctx, int nkh, int nvh, int dk, cwen_gdn **out);
+int cwen_gdn_free(cwen_gdn *g);
+/* Current state from HOST arrays (NULL = zeros).  Synchronous. */
+int cwen_gdn_set_state(cwen_gdn *g, const float *S, const float *hist);
+/* Copy state `pos` to HOST arrays (either may be NULL): 0 = the current
+ * state, p >= 1 = the snapshot after position p-1 of the last block (before
+ * it is committed).  Synchronous. */
+int cwen_gdn_get_state(cwen_gdn *g, int pos, float *S, float *hist);
+/* B positions of a verify block, in order, each exactly conv1d_update then
+ * gdn_step of the reference (run.c:2183-2200, 2014-2180) as called by
+ * layer_linear_blk (run.c:2700-2704): qkv (device, [b*qs + c]) is the raw
+ * mixed q|k|v row before the conv, z [b*zs + i] the gate row, decay
+ * [b*gs + hv] the log-domain decay (g = exp(decay)) and beta [b*gs + hv],
+ * kw [C][4] the conv taps, wn [dk] the gated-norm weight; out [b*os + i]
+ * receives the gated-RMSNorm output (nvh*dk per position).  The state after
+ * each position is kept as a snapshot; the current state does not move until
+ * cwen_gdn_commit. */
+int cwen_gdn_block(cwen_ctx *ctx, cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
+                   const float *decay, const float *beta, int gs, const float *kw, const float *wn,
+                   float *out, int os, int B, void *stream);
+/* Accept the first n positions (0..B) of the last block: the current state
+ * becomes the snapshot after position n-1 (n = 0 keeps the state from
+ * before the block).  Host-side index move, no device work.  Replaces
+ * snap_load + the replaying forward_block of a short walk (run.c:4975-4988)
+ * for this layer. */
+int cwen_gdn_commit(cwen_gdn *g, int n);
+
 /* ---- f16 activation operands ----
  * The kernels read activations as IEEE half, row-major [B][K] with row stride
  * exactly K (2-byte elements, 16-byte aligned rows).  These entry points let a
