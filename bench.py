@@ -148,6 +148,102 @@ def gpu_leg(steps: int, warmup: int, Bs: list[int]) -> dict:
     return out
 
 
+# ---------------------------------------------------------------- other configs
+C0_BYTES = 5120 * 160 * 18 + 5120 * 4 + 5120 * 4          # W + x + y
+C2_V = 151936
+C2_BYTES = C2_V * 20 * 210 + 8 * 5120 * 4 + 8 * C2_V * 4  # W + x + logits
+C3_BYTES = 29_445_632                                      # S + 8 snapshots + inputs + history + out
+
+
+def _stats(ms: list[float]) -> dict:
+    return {"median_ms": float(np.median(ms)), "min_ms": float(np.min(ms))}
+
+
+def time_each(fn, n: int, warmup: int, stream) -> list[float]:
+    """Per-launch ms of fn(i) (events around each launch on the launch stream)."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    for i in range(n):
+        ev[i].record(stream)
+        fn(i)
+    ev[n].record(stream)
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
+
+
+def extra_leg(steps: int, warmup: int) -> dict:
+    """c0 GGUF Q4_0 GEMV B=1, c2 Q6_K head + argmax + walk at B=8, c3 GDN block
+    at B=8: average launch time over back-to-back launches (rotating enough
+    copies that each launch streams from HBM), GB/s from the algorithmic bytes."""
+    import torch
+    from cwen_amd import gpu, synth
+    ctx = gpu.Context(0)
+    stream = torch.cuda.current_stream()
+    out = {}
+
+    # c0: 24 copies x 14.7 MB > 256 MB MALL
+    Ws = [gpu.Weight(ctx, gpu.T_Q4_0, synth.q4_gguf(0, 5120, 5120, key=c), None, 5120, 5120) for c in range(24)]
+    x = torch.from_numpy(synth.activations(0, 1, 5120)).cuda()
+    xh = torch.empty(1, 5120, dtype=torch.float16, device="cuda")
+    y = torch.empty(1, 5120, device="cuda")
+    gpu.act_to_f16(ctx, x, xh, 5120, 1, stream=stream)
+    ms = time_launches(lambda i: gpu.gemvb_f16(ctx, Ws[i % len(Ws)], xh, y, 1, stream=stream), steps, warmup,
+                       stream)
+    ms32 = time_launches(lambda i: gpu.gemvb(ctx, Ws[i % len(Ws)], x, y, 1, stream=stream), steps, warmup,
+                         stream)
+    out["c0_q4_0_gguf_5120x5120_b1"] = {"ms": ms, "GB_s": C0_BYTES / (ms * 1e-3) / 1e9,
+                                        "frac_of_peak": C0_BYTES / (ms * 1e-3) / 1e9 / PEAK_GBS,
+                                        "launches": "q4 GEMV on f16 x (one launch)",
+                                        "ms_f32_entry": ms32}
+    del Ws
+
+    # c2: 638 MB head (> MALL), B=8, drafts = argmax w.p. 0.6
+    W = gpu.Weight(ctx, gpu.T_Q6_K, synth.q6_k(0, C2_V, 5120), None, 5120, C2_V)
+    X = torch.from_numpy(synth.activations(0, 8, 5120)).cuda()
+    lg = torch.empty(8, C2_V, device="cuda")
+    res = torch.zeros(10, dtype=torch.int32, device="cuda")
+    gpu.head_verify(ctx, W, X, 8, res, logits=lg, stream=stream)
+    am = res[2:].cpu().numpy()
+    rng = np.random.default_rng(0)
+    drafts = np.where(rng.random(7) < 0.6, am[0:7], rng.integers(0, C2_V, 7)).astype(np.int32)
+    dd = torch.from_numpy(drafts).cuda()
+    ms = time_launches(lambda i: gpu.head_verify(ctx, W, X, 8, res, drafts=dd, E=7, logits=lg, stream=stream),
+                       max(steps // 2, 5), 2, stream)
+    kb = res[:2].cpu().numpy()
+    out["c2_q6_k_head_151936x5120_b8_walk"] = {"ms": ms, "GB_s": C2_BYTES / (ms * 1e-3) / 1e9,
+                                               "frac_of_peak": C2_BYTES / (ms * 1e-3) / 1e9 / PEAK_GBS,
+                                               "k": int(kb[0]), "bonus": int(kb[1]),
+                                               "launches": "act_to_f16 + Q6_K GEMV with fused argmax/walk"}
+    del W
+
+    # c3: 8 layer states x 55 MB rotated, B=8
+    B, nkh, nvh = 8, 16, 48
+    g = np.random.default_rng(0)
+    Cch = (2 * nkh + nvh) * 128
+    Gs = []
+    for _ in range(8):
+        G = gpu.GDN(ctx, nkh, nvh)
+        G.set_state((0.01 * g.standard_normal((nvh, 128, 128))).astype(np.float32),
+                    g.standard_normal((Cch, 3)).astype(np.float32))
+        Gs.append(G)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+    qkv, z = t(g.standard_normal((B, Cch))), t(g.standard_normal((B, nvh * 128)))
+    decay = t(np.log(g.uniform(1e-3, 1, (B, nvh))))
+    beta = t(1 / (1 + np.exp(-g.standard_normal((B, nvh)))))
+    kw, wn = t(0.5 * g.standard_normal((Cch, 4))), t(1 + 0.1 * g.standard_normal(128))
+    o = torch.empty(B, nvh * 128, device="cuda")
+    ms = time_launches(lambda i: Gs[i % 8].block(qkv, z, decay, beta, kw, wn, o, B, stream=stream),
+                       steps, warmup, stream)
+    out["c3_gdn_48x128_b8"] = {"ms": ms, "GB_s": C3_BYTES / (ms * 1e-3) / 1e9,
+                               "frac_of_peak": C3_BYTES / (ms * 1e-3) / 1e9 / PEAK_GBS,
+                               "launches": "gdn block (conv + delta rule + snapshots)"}
+    for G in Gs:
+        G.free()
+    return {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in out.items()}
+
+
 def cpu_child(B: int, reps: int) -> None:
     """CPU baseline leg: the reference engine's own mlp_blk kernels (gemvb x3 +
     silu_mul, run.c:2677-2681), compiled from its run.c (oracle/_ref); the
@@ -218,6 +314,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--Bs", default="8,1,16",
                     help="comma-separated block sizes; the first is the headline (must include 8)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the c0/c2/c3 kernel measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a 256 MiB device copy (for FETCH_SIZE/WRITE_SIZE calibration)")
     ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
@@ -236,6 +333,7 @@ def main() -> int:
     if args.calibrate_copy:
         calibrate_copy()
     res = gpu_leg(args.steps, args.warmup, Bs)
+    extra = None if args.no_extra else extra_leg(args.steps, args.warmup)
     traffic = load_traffic()
     h = res[8]
     b1, _ = ffn_bytes(8)
@@ -276,6 +374,7 @@ def main() -> int:
             "algorithmic_bytes": b1,
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_leg(8),
+        "other_configs": extra,
     }
     print(json.dumps(line))
     return 0

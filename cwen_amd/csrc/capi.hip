@@ -296,9 +296,10 @@ int cwen_gdn_create(cwen_ctx *ctx, int nkh, int nvh, int dk, cwen_gdn **out) {
   g->nslot = CWEN_BMAX + 1;
   const size_t sf = (size_t)nvh * dk * dk, hf = (size_t)g->C * 3;
   if (hipMalloc((void **)&g->S, sf * g->nslot * sizeof(float)) != hipSuccess ||
-      hipMalloc((void **)&g->H, hf * g->nslot * sizeof(float)) != hipSuccess) {
-    if (g->S) (void)hipFree(g->S);
-    free(g);
+      hipMalloc((void **)&g->H, hf * g->nslot * sizeof(float)) != hipSuccess ||
+      hipMalloc((void **)&g->xc, (size_t)CWEN_BMAX * g->C * sizeof(float)) != hipSuccess ||
+      hipMalloc((void **)&g->ob, (size_t)CWEN_BMAX * nvh * dk * sizeof(float)) != hipSuccess) {
+    cwen_gdn_free(g);
     return CWEN_ENOMEM;
   }
   if (hipMemset(g->S, 0, sf * sizeof(float)) != hipSuccess ||
@@ -316,6 +317,8 @@ int cwen_gdn_free(cwen_gdn *g) {
   (void)hipDeviceSynchronize();
   if (g->S) (void)hipFree(g->S);
   if (g->H) (void)hipFree(g->H);
+  if (g->xc) (void)hipFree(g->xc);
+  if (g->ob) (void)hipFree(g->ob);
   free(g);
   return CWEN_OK;
 }
@@ -350,6 +353,7 @@ int cwen_gdn_block(cwen_ctx *ctx, cwen_gdn *g, const float *qkv, int qs, const f
                    float *out, int os, int B, void *stream) {
   if (!ctx || !g || g->ctx != ctx || B < 1 || B > CWEN_BMAX) return CWEN_EINVAL;
   if (!qkv || !z || !decay || !beta || !kw || !wn || !out) return CWEN_EINVAL;
+  if (!aligned16(kw) || !aligned16(wn) || !aligned16(out) || (os & 3)) return CWEN_EINVAL;
   const int zh = g->nvh * g->dk;
   if ((B > 1 && (qs < g->C || zs < zh || gs < g->nvh || os < zh)) || qs < 0 || zs < 0 || gs < 0 || os < 0)
     return CWEN_EINVAL;

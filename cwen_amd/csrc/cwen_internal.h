@@ -57,6 +57,7 @@ struct cwen_gdn {
   int nslot, cur;
   int last_B;               // positions of the last block (commit bound)
   float *S, *H;             // device slot rings
+  float *xc, *ob;           // scratch: post-conv values [BMAX][C], pre-norm outputs [BMAX][nvh*dk]
 };
 
 #define CWEN_HIP_TRY(expr)                                   \

@@ -17,26 +17,56 @@
 //   gated RMSNorm: out = wn * o * (1/sqrt(mean(o^2) + 1e-6)) * silu(z)
 // S is [hv][i][j], row i the key dimension, as in the reference.
 //
-// Design (gfx950): one workgroup per value head, 256 threads; thread t owns
-// column j = t/2 and rows 64*(t&1) .. +63 of the head's 128 x 128 state in 64
-// VGPRs for the whole block.  The delta rule is column-local (sk[j], delta[j]
-// and o[j] read only column j), so a position costs two lane shuffles and one
-// block-wide sum (the RMSNorm).  Inputs of all B positions are staged in LDS
-// up front.  After each position the state is stored to snapshot slot
-// (cur + 1 + b) mod NSLOT, the conv history likewise, so accepting the first
-// n positions is the host-side move cur += n: rollback reads nothing.
+// Design (gfx950): three launches on the caller's stream.
+//  1. conv: one thread per channel runs the B positions in order, writes the
+//     post-SiLU values to scratch and the history after every position to
+//     the snapshot ring.
+//  2. recurrence: the delta rule is column-local (sk[j], delta[j] and o[j]
+//     read only column j), so a head's 128 columns split over 8 single-wave
+//     workgroups of 16 columns; 384 workgroups keep the per-position state
+//     snapshot (3 MB per position) spread over the whole chip.  A lane owns a
+//     4-column x 8-row block in registers for the whole block; a column sum
+//     is a 16-lane DPP reduction.  The state after each position is stored
+//     to snapshot slot (cur + 1 + b) mod NSLOT.
+//  3. norm: one wave per (position, value head) applies the gated RMSNorm.
+// Accepting the first n positions is then the host-side move cur += n:
+// rollback reads nothing.  Every position runs the same instructions whatever
+// B is, so a block of B equals B single-position blocks bit for bit.
 #include "cwen_internal.h"
 
 namespace {
 
 constexpr int DK = 128;
-constexpr int THREADS = 256;
 constexpr int MAXB = CWEN_BMAX;
+constexpr int COLS = 16;            // columns of a head per recurrence workgroup
+
+__device__ __forceinline__ float silu_ref(float x) { return x * (1.f / (1.f + expf(-x))); }
+
+// Cross-lane sums on DPP row permutes (no LDS round trip).
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over each aligned row of 16 lanes: quad xor 1, quad xor 2, half-row
+// mirror, row mirror.
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  return v + dpp<0x140>(v);
+}
+// Sum over the wave (wave-uniform result).
+__device__ __forceinline__ float sum64(float v) {
+  const int b = __builtin_bit_cast(int, sum16(v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+}
 
 struct GdnParams {
-  const float *S_in;     // state slot read [nvh][DK][DK]
-  float *S_slots;        // slot ring base
-  const float *H_in;     // conv history slot read [C][3]
+  const float *S_in;          // state slot read [nvh][DK][DK]
+  float *S_slots;             // slot ring base
+  const float *H_in;          // conv history slot read [C][3]
   float *H_slots;
   size_t s_floats, h_floats;  // floats per slot
   int cur, nslot;
@@ -46,116 +76,120 @@ struct GdnParams {
   const float *kw;            // conv weights [C][4]
   const float *wn;            // gated-norm weight [DK]
   float *out; int os;         // [B][os]
+  float *xc;                  // scratch: post-conv values [B][C]
+  float *ob;                  // scratch: pre-norm outputs [B][nvh*DK]
   int nkh, nvh, C, B;
 };
 
-__device__ __forceinline__ float silu_ref(float x) { return x * (1.f / (1.f + expf(-x))); }
+// 1. conv: thread = channel.  All loads of a channel are issued before its
+// first use.
+__global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= p.C) return;
+  const float4 w = *(const float4 *)(p.kw + (size_t)c * 4);
+  float h0 = p.H_in[(size_t)c * 3 + 0], h1 = p.H_in[(size_t)c * 3 + 1], h2 = p.H_in[(size_t)c * 3 + 2];
+  float raw[MAXB];
+#pragma unroll
+  for (int b = 0; b < MAXB; ++b) raw[b] = b < p.B ? p.qkv[(size_t)b * p.qs + c] : 0.f;
+#pragma unroll
+  for (int b = 0; b < MAXB; ++b) {
+    if (b >= p.B) break;
+    const float cur = raw[b];
+    // ((st0*w0 + st1*w1) + st2*w2) + cur*w3, each product and sum rounded
+    const float x = __fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(h0, w.x), __fmul_rn(h1, w.y)), __fmul_rn(h2, w.z)),
+                              __fmul_rn(cur, w.w));
+    h0 = h1; h1 = h2; h2 = cur;
+    p.xc[(size_t)b * p.C + c] = silu_ref(x);
+    float *hs = p.H_slots + (size_t)((p.cur + 1 + b) % p.nslot) * p.h_floats + (size_t)c * 3;
+    hs[0] = h0; hs[1] = h1; hs[2] = h2;
+  }
+}
 
-__global__ __launch_bounds__(THREADS) void gdn_block_kernel(GdnParams p) {
-  // post-conv inputs of this head for every position: q | k | v, then z
-  __shared__ float xin[MAXB][3 * DK];
-  __shared__ float zin[MAXB][DK];
-  __shared__ float red[THREADS / 64];
-  const int tid = threadIdx.x;
-  const int hv = blockIdx.x;
+// 2. recurrence: workgroup (hv, slice) = one wave, columns
+// slice*16 .. slice*16+15 of head hv.  Lane: row group rg = lane & 15 (rows
+// 8rg..8rg+7), column group cg = lane >> 4 (4 columns).
+__global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
+  __shared__ __align__(16) float qk[MAXB][2 * DK];   // normalised q | k per position
+  __shared__ __align__(16) float vs[MAXB][COLS];
+  __shared__ float s_g[MAXB], s_beta[MAXB];
+  const int lane = threadIdx.x;
+  const int hv = blockIdx.x / (DK / COLS);
+  const int slice = blockIdx.x % (DK / COLS);
   const int hk = hv % p.nkh;
   const int B = p.B;
+  const int rg = lane & 15, cg = lane >> 4;
+  const int i0 = rg * 8, j0 = slice * COLS + cg * 4;
 
-  // ---- conv over the B positions for the head's q, k, v channels.
-  // Local channel lc: 0..127 q of key head hk, 128..255 k, 256..383 v of hv.
-  // The q/k channels of key head hk are shared by nvh/nkh value heads; the
-  // one with hv == hk owns their history.
-  for (int lc = tid; lc < 3 * DK; lc += THREADS) {
-    const int part = lc / DK, i = lc % DK;
-    const int c = part == 0 ? hk * DK + i : part == 1 ? (p.nkh + hk) * DK + i : 2 * p.nkh * DK + hv * DK + i;
-    const bool owner = part == 2 || hv == hk;
-    const float w0 = p.kw[(size_t)c * 4 + 0], w1 = p.kw[(size_t)c * 4 + 1];
-    const float w2 = p.kw[(size_t)c * 4 + 2], w3 = p.kw[(size_t)c * 4 + 3];
-    float h0 = p.H_in[(size_t)c * 3 + 0], h1 = p.H_in[(size_t)c * 3 + 1], h2 = p.H_in[(size_t)c * 3 + 2];
-    for (int b = 0; b < B; ++b) {
-      const float cur = p.qkv[(size_t)b * p.qs + c];
-      // ((st0*w0 + st1*w1) + st2*w2) + cur*w3, each product and sum rounded
-      const float x = __fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(h0, w0), __fmul_rn(h1, w1)), __fmul_rn(h2, w2)),
-                                __fmul_rn(cur, w3));
-      h0 = h1; h1 = h2; h2 = cur;
-      xin[b][lc] = silu_ref(x);
-      if (owner) {
-        float *hs = p.H_slots + (size_t)((p.cur + 1 + b) % p.nslot) * p.h_floats + (size_t)c * 3;
-        hs[0] = h0; hs[1] = h1; hs[2] = h2;
-      }
-    }
-  }
-  for (int e = tid; e < B * DK; e += THREADS) zin[e / DK][e % DK] = p.z[(size_t)(e / DK) * p.zs + hv * DK + e % DK];
-  __syncthreads();
-
-  // ---- l2norm of q and k per position: wave w takes positions w, w+4, ...
+  float4 s[8];
   {
-    const int wave = tid >> 6, lane = tid & 63;
-    for (int b = wave; b < B; b += THREADS / 64) {
+    const float *Sh = p.S_in + (size_t)hv * DK * DK;
 #pragma unroll
-      for (int part = 0; part < 2; ++part) {
-        float *x = &xin[b][part * DK];
-        const float a = x[lane], c = x[lane + 64];
-        float ss = a * a + c * c;
-#pragma unroll
-        for (int sh = 32; sh > 0; sh >>= 1) ss += __shfl_xor(ss, sh);
-        const float s = 1.f / sqrtf(ss + 1e-6f);
-        x[lane] = a * s;
-        x[lane + 64] = c * s;
-      }
-    }
+    for (int r = 0; r < 8; ++r) s[r] = *(const float4 *)(Sh + (size_t)(i0 + r) * DK + j0);
+  }
+  if (lane < B) {
+    s_g[lane] = expf(p.decay[(size_t)lane * p.gs + hv]);
+    s_beta[lane] = p.beta[(size_t)lane * p.gs + hv];
+  }
+  for (int e = lane; e < B * COLS; e += 64)
+    vs[e / COLS][e % COLS] = p.xc[(size_t)(e / COLS) * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
+  // q and k of key head hk, l2-normalised per position
+  for (int b = 0; b < B; ++b) {
+    const float *xq = p.xc + (size_t)b * p.C + hk * DK;
+    const float *xk = p.xc + (size_t)b * p.C + (p.nkh + hk) * DK;
+    const float q0 = xq[lane], q1 = xq[lane + 64], k0 = xk[lane], k1 = xk[lane + 64];
+    const float sq = 1.f / sqrtf(sum64(q0 * q0 + q1 * q1) + 1e-6f);
+    const float sk = 1.f / sqrtf(sum64(k0 * k0 + k1 * k1) + 1e-6f);
+    qk[b][lane] = q0 * sq; qk[b][lane + 64] = q1 * sq;
+    qk[b][DK + lane] = k0 * sk; qk[b][DK + lane + 64] = k1 * sk;
   }
   __syncthreads();
 
-  // ---- the recurrence, state in registers
-  const int j = tid >> 1, hh = tid & 1;
-  const int i0 = hh * 64;
-  const float *Sh = p.S_in + (size_t)hv * DK * DK;
-  float s[64];
-#pragma unroll
-  for (int r = 0; r < 64; ++r) s[r] = Sh[(size_t)(i0 + r) * DK + j];
   const float scale = 1.f / sqrtf((float)DK);
-  const float wnj = p.wn[j];
-
   for (int b = 0; b < B; ++b) {
-    const float g = expf(p.decay[(size_t)b * p.gs + hv]);
-    const float beta = p.beta[(size_t)b * p.gs + hv];
-    const float *q = &xin[b][0], *k = &xin[b][DK];
-    const float vj = xin[b][2 * DK + j];
-    float sk = 0.f;
+    const float g = s_g[b], beta = s_beta[b];
+    const float4 qa = *(const float4 *)&qk[b][i0], qb = *(const float4 *)&qk[b][i0 + 4];
+    const float4 ka = *(const float4 *)&qk[b][DK + i0], kb = *(const float4 *)&qk[b][DK + i0 + 4];
+    const float kr[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+    const float qr[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    float4 sk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 64; ++r) {
-      s[r] *= g;
-      sk = fmaf(s[r], k[i0 + r], sk);
+    for (int r = 0; r < 8; ++r) {
+      s[r].x *= g; s[r].y *= g; s[r].z *= g; s[r].w *= g;
+      sk.x = fmaf(s[r].x, kr[r], sk.x); sk.y = fmaf(s[r].y, kr[r], sk.y);
+      sk.z = fmaf(s[r].z, kr[r], sk.z); sk.w = fmaf(s[r].w, kr[r], sk.w);
     }
-    sk += __shfl_xor(sk, 1);
-    const float delta = beta * (vj - sk);
-    float o = 0.f;
+    sk = (float4){sum16(sk.x), sum16(sk.y), sum16(sk.z), sum16(sk.w)};
+    const float4 v4 = *(const float4 *)&vs[b][cg * 4];
+    const float4 dl = {beta * (v4.x - sk.x), beta * (v4.y - sk.y), beta * (v4.z - sk.z), beta * (v4.w - sk.w)};
+    float4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 64; ++r) {
-      s[r] = fmaf(k[i0 + r], delta, s[r]);
-      o = fmaf(s[r], q[i0 + r], o);
+    for (int r = 0; r < 8; ++r) {
+      s[r].x = fmaf(kr[r], dl.x, s[r].x); s[r].y = fmaf(kr[r], dl.y, s[r].y);
+      s[r].z = fmaf(kr[r], dl.z, s[r].z); s[r].w = fmaf(kr[r], dl.w, s[r].w);
+      o.x = fmaf(s[r].x, qr[r], o.x); o.y = fmaf(s[r].y, qr[r], o.y);
+      o.z = fmaf(s[r].z, qr[r], o.z); o.w = fmaf(s[r].w, qr[r], o.w);
     }
-    o += __shfl_xor(o, 1);
-    o *= scale;
-    // snapshot after this position
+    o = (float4){sum16(o.x) * scale, sum16(o.y) * scale, sum16(o.z) * scale, sum16(o.w) * scale};
     float *So = p.S_slots + (size_t)((p.cur + 1 + b) % p.nslot) * p.s_floats + (size_t)hv * DK * DK;
 #pragma unroll
-    for (int r = 0; r < 64; ++r) So[(size_t)(i0 + r) * DK + j] = s[r];
-    // gated RMSNorm over the head's 128 outputs (each column held twice)
-    float ss = hh == 0 ? o * o : 0.f;
-#pragma unroll
-    for (int sh = 32; sh > 0; sh >>= 1) ss += __shfl_xor(ss, sh);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    const float tot = red[0] + red[1] + red[2] + red[3];
-    __syncthreads();
-    const float sc = 1.f / sqrtf(tot / DK + 1e-6f);
-    if (hh == 0) {
-      const float zj = zin[b][j];
-      p.out[(size_t)b * p.os + hv * DK + j] = wnj * o * sc * silu_ref(zj);
-    }
+    for (int r = 0; r < 8; ++r) *(float4 *)(So + (size_t)(i0 + r) * DK + j0) = s[r];
+    if (rg == 0) *(float4 *)(p.ob + (size_t)b * p.nvh * DK + hv * DK + j0) = o;
   }
+}
+
+// 3. gated RMSNorm: one wave per (position, value head).
+__global__ __launch_bounds__(64) void gdn_norm_kernel(GdnParams p) {
+  const int b = blockIdx.x / p.nvh, hv = blockIdx.x % p.nvh;
+  const int lane = threadIdx.x;
+  const float2 o = *(const float2 *)(p.ob + (size_t)b * p.nvh * DK + hv * DK + 2 * lane);
+  const float ss = sum64(o.x * o.x + o.y * o.y);
+  const float sc = 1.f / sqrtf(ss / DK + 1e-6f);
+  const float zx = p.z[(size_t)b * p.zs + hv * DK + 2 * lane], zy = p.z[(size_t)b * p.zs + hv * DK + 2 * lane + 1];
+  const float2 w = *(const float2 *)(p.wn + 2 * lane);
+  float2 r;
+  r.x = w.x * o.x * sc * silu_ref(zx);
+  r.y = w.y * o.y * sc * silu_ref(zy);
+  *(float2 *)(p.out + (size_t)b * p.os + hv * DK + 2 * lane) = r;
 }
 
 }  // namespace
@@ -177,8 +211,11 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
   p.decay = decay; p.beta = beta; p.gs = gs;
   p.kw = kw; p.wn = wn;
   p.out = out; p.os = os;
+  p.xc = g->xc; p.ob = g->ob;
   p.nkh = g->nkh; p.nvh = g->nvh; p.C = g->C; p.B = B;
-  hipLaunchKernelGGL(gdn_block_kernel, dim3((unsigned)g->nvh), dim3(THREADS), 0, st, p);
+  hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((g->C + 255) / 256)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(gdn_rec_kernel, dim3((unsigned)(g->nvh * (DK / COLS))), dim3(64), 0, st, p);
+  hipLaunchKernelGGL(gdn_norm_kernel, dim3((unsigned)(g->nvh * B)), dim3(64), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }

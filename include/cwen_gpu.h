@@ -154,7 +154,8 @@ int cwen_gdn_get_state(cwen_gdn *g, int pos, float *S, float *hist);
  * mixed q|k|v row before the conv, z [b*zs + i] the gate row, decay
  * [b*gs + hv] the log-domain decay (g = exp(decay)) and beta [b*gs + hv],
  * kw [C][4] the conv taps, wn [dk] the gated-norm weight; out [b*os + i]
- * receives the gated-RMSNorm output (nvh*dk per position).  The state after
+ * receives the gated-RMSNorm output (nvh*dk per position).  kw, wn and out
+ * must be 16-byte aligned and os a multiple of 4.  The state after
  * each position is kept as a snapshot; the current state does not move until
  * cwen_gdn_commit. */
 int cwen_gdn_block(cwen_ctx *ctx, cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
