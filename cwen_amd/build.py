@@ -17,6 +17,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libcwen_gpu.so"
+HOST_LIB = PKG / "libcwen_host.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -63,6 +64,18 @@ def build_gpu(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_host(verbose: bool = False) -> Path:
+    """The C host drivers (cwen_amd/host), linked against libcwen_gpu.so."""
+    src = PKG / "host" / "cwen_host.c"
+    tmp = HOST_LIB.with_suffix(".so.tmp")
+    _run(["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", "-fPIC", "-shared", f"-I{ROOT / 'include'}",
+          str(src), f"-L{PKG}", "-lcwen_gpu", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])
+    os.replace(tmp, HOST_LIB)
+    if verbose:
+        print(f"built {HOST_LIB}")
+    return HOST_LIB
+
+
 def build_oracle(verbose: bool = False) -> None:
     """Test infrastructure: the oracle restatement and, if the reference tree
     is present, the reference checker builds (oracle/Makefile)."""
@@ -75,5 +88,6 @@ def build_oracle(verbose: bool = False) -> None:
 
 if __name__ == "__main__":
     build_gpu(verbose=True)
+    build_host(verbose=True)
     if "--oracle" in sys.argv:
         build_oracle(verbose=True)

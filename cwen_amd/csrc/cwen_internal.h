@@ -113,4 +113,16 @@ int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &
 // ------------------------------------------------------------ gdn.hip
 int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
                      const float *decay, const float *beta, int gs, const float *kw, const float *wn,
-                     float *out, int os, int B, hipStream_t st);
+                     float *out, int os, int B, hipStream_t st, _Float16 *outh = nullptr, int ohs = 0,
+                     const float *A = nullptr, const float *dt = nullptr);
+
+// ------------------------------------------------------------ model.hip
+int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *toks, int B, int H, float *X,
+                 int xs, hipStream_t st);
+int rmsnorm_launch(const float *X, int xs, const float *w, int n, float eps, float *Y, int ys, _Float16 *Yh,
+                   int yhs, int B, hipStream_t st);
+size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B);
+int attention_launch(const float *qfull, const float *kx, const float *vx, int kvs, const float *qn,
+                     const float *kn, float *qbuf, float *K, float *V, int pbase, int B, int NH, int NKV,
+                     int npairs, int nrot, float theta, float eps, float *part, int max_ctx, _Float16 *yh,
+                     hipStream_t st);

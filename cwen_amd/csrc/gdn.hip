@@ -75,7 +75,9 @@ struct GdnParams {
   const float *decay, *beta; int gs;  // [B][gs]
   const float *kw;            // conv weights [C][4]
   const float *wn;            // gated-norm weight [DK]
-  float *out; int os;         // [B][os]
+  float *out; int os;         // [B][os], nullable
+  _Float16 *outh; int ohs;    // f16 copy [B][ohs], nullable
+  const float *A, *dt;        // raw gates when non-null: decay = A*softplus(decay + dt), beta = sigmoid(beta)
   float *xc;                  // scratch: post-conv values [B][C]
   float *ob;                  // scratch: pre-norm outputs [B][nvh*DK]
   int nkh, nvh, C, B;
@@ -127,8 +129,14 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
     for (int r = 0; r < 8; ++r) s[r] = *(const float4 *)(Sh + (size_t)(i0 + r) * DK + j0);
   }
   if (lane < B) {
-    s_g[lane] = expf(p.decay[(size_t)lane * p.gs + hv]);
-    s_beta[lane] = p.beta[(size_t)lane * p.gs + hv];
+    float dec = p.decay[(size_t)lane * p.gs + hv], bt = p.beta[(size_t)lane * p.gs + hv];
+    if (p.A) {  // run.c:2697-2698 (softplus, sigmoid: run.c:392-399)
+      const float x = dec + p.dt[hv];
+      dec = p.A[hv] * (x > 20.f ? x : logf(1.f + expf(x)));
+      bt = 1.f / (1.f + expf(-bt));
+    }
+    s_g[lane] = expf(dec);
+    s_beta[lane] = bt;
   }
   for (int e = lane; e < B * COLS; e += 64)
     vs[e / COLS][e % COLS] = p.xc[(size_t)(e / COLS) * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
@@ -189,14 +197,19 @@ __global__ __launch_bounds__(64) void gdn_norm_kernel(GdnParams p) {
   float2 r;
   r.x = w.x * o.x * sc * silu_ref(zx);
   r.y = w.y * o.y * sc * silu_ref(zy);
-  *(float2 *)(p.out + (size_t)b * p.os + hv * DK + 2 * lane) = r;
+  if (p.out) *(float2 *)(p.out + (size_t)b * p.os + hv * DK + 2 * lane) = r;
+  if (p.outh) {
+    const half2_t h = {(_Float16)r.x, (_Float16)r.y};
+    *(half2_t *)(p.outh + (size_t)b * p.ohs + hv * DK + 2 * lane) = h;
+  }
 }
 
 }  // namespace
 
 int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
                      const float *decay, const float *beta, int gs, const float *kw, const float *wn,
-                     float *out, int os, int B, hipStream_t st) {
+                     float *out, int os, int B, hipStream_t st, _Float16 *outh, int ohs, const float *A,
+                     const float *dt) {
   GdnParams p;
   p.s_floats = (size_t)g->nvh * DK * DK;
   p.h_floats = (size_t)g->C * 3;
@@ -211,6 +224,8 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
   p.decay = decay; p.beta = beta; p.gs = gs;
   p.kw = kw; p.wn = wn;
   p.out = out; p.os = os;
+  p.outh = outh; p.ohs = ohs;
+  p.A = A; p.dt = dt;
   p.xc = g->xc; p.ob = g->ob;
   p.nkh = g->nkh; p.nvh = g->nvh; p.C = g->C; p.B = B;
   hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((g->C + 255) / 256)), dim3(256), 0, st, p);

@@ -1,0 +1,375 @@
+// C ABI of the block-verify model: the hybrid GatedDeltaNet / gated-attention
+// decoder of the reference engine (run.c) resident on one device, with the
+// forward_block / verify / serial-step entry points.
+//
+// Reference: forward_block 2752-2779, layer_linear_blk 2685-2712,
+// layer_full_blk 2714-2745, mlp_blk 2677-2683, forward_ex 2594-2645,
+// prefill_forward 4823-4857, the verify walk of generate_tokens_spec
+// 4950-5009.
+#include <stdlib.h>
+#include <string.h>
+
+#include <new>
+
+#include "cwen_internal.h"
+
+namespace {
+
+struct Layer {
+  int linear;
+  float *attn_norm = nullptr, *post_norm = nullptr;
+  cwen_weight *ffn_gu = nullptr, *ffn_down = nullptr;
+  cwen_weight *qkv = nullptr, *gate_z = nullptr, *alpha = nullptr, *beta = nullptr, *ssm_out = nullptr;
+  float *ssm_a = nullptr, *ssm_dt = nullptr, *ssm_conv = nullptr, *ssm_norm = nullptr;
+  cwen_gdn *gdn = nullptr;
+  cwen_weight *wq = nullptr, *wkv = nullptr, *wo = nullptr;
+  float *q_norm = nullptr, *k_norm = nullptr;
+  float *K = nullptr, *V = nullptr;
+};
+
+template <class T> int dmalloc(T **p, size_t n) {
+  return hipMalloc((void **)p, n * sizeof(T)) == hipSuccess ? CWEN_OK : CWEN_ENOMEM;
+}
+
+}  // namespace
+
+struct cwen_model {
+  cwen_ctx *ctx;
+  cwen_model_cfg cfg;
+  Layer *L;
+  uint8_t *emb_qs = nullptr;
+  uint16_t *emb_sc = nullptr;
+  int emb_type = -1;
+  float *out_norm = nullptr;
+  cwen_weight *head = nullptr;
+  int pos = -1;                  // last filled slot
+  // device scratch
+  int *toks = nullptr, *drafts = nullptr, *res = nullptr;
+  float *X = nullptr;            // residual stream [BMAX][H]
+  _Float16 *Xh = nullptr;        // normed f16 operand [BMAX][H]
+  float *qkv = nullptr, *z = nullptr, *ga = nullptr, *gb = nullptr;
+  _Float16 *gh = nullptr;        // GDN output f16 [BMAX][nvh*dk]
+  float *qfull = nullptr, *kx = nullptr, *vx = nullptr, *qbuf = nullptr, *apart = nullptr;
+  _Float16 *yh = nullptr;        // attention output f16 [BMAX][NH*HD]
+  _Float16 *hh = nullptr;        // FFN hidden f16 [BMAX][I]
+  float *logits = nullptr;       // [BMAX][V]
+  int *hres = nullptr;           // pinned host copy of res
+};
+
+namespace {
+
+bool is_full(const cwen_model_cfg &c, int l) { return l % c.full_interval == c.full_interval - 1; }
+
+int check_cfg(const cwen_model_cfg *c) {
+  if (!c || c->n_layers <= 0 || c->d_model <= 0 || c->d_ffn <= 0 || c->vocab <= 0) return CWEN_EINVAL;
+  if (c->d_model % Q4_K_ALIGN || c->d_ffn % Q4_K_ALIGN) return CWEN_EINVAL;
+  if (c->head_dim != 256 || c->n_head <= 0 || c->n_kv_head <= 0 || c->n_head % c->n_kv_head) return CWEN_EINVAL;
+  if ((c->n_head * c->head_dim) % Q4_K_ALIGN) return CWEN_EINVAL;
+  if (c->gdn_dk != 128 || c->gdn_nkh <= 0 || c->gdn_nvh % c->gdn_nkh || (c->gdn_nvh * 128) % Q4_K_ALIGN)
+    return CWEN_EINVAL;
+  if (c->full_interval <= 0 || c->max_ctx < 2 || c->n_rot_pairs < 0 || 2 * c->n_rot_pairs > c->head_dim)
+    return CWEN_EINVAL;
+  return CWEN_OK;
+}
+
+int upload_f32(const void *data, size_t n, float **out) {
+  if (*out) (void)hipFree(*out);
+  *out = nullptr;
+  if (dmalloc(out, n)) return CWEN_ENOMEM;
+  CWEN_HIP_TRY(hipMemcpy(*out, data, n * sizeof(float), hipMemcpyHostToDevice));
+  return CWEN_OK;
+}
+
+int upload_w(cwen_model *m, int type, const void *data, const void *scales, int ne0, int ne1,
+             int want_ne0, int want_ne1, cwen_weight **out) {
+  if (ne0 != want_ne0 || ne1 != want_ne1) return CWEN_EINVAL;
+  if (*out) cwen_weight_free(*out);
+  *out = nullptr;
+  return cwen_weight_upload(m->ctx, type, data, scales, ne0, ne1, out);
+}
+
+// One verify block over tokens already in m->toks: positions pos+1..pos+B.
+// head: 0 none, 1 head + argmax/walk (drafts in m->drafts, E).
+int block(cwen_model *m, int B, int head, int E, hipStream_t st) {
+  const cwen_model_cfg &c = m->cfg;
+  cwen_ctx *ctx = m->ctx;
+  const int H = c.d_model, I = c.d_ffn;
+  const int pbase = m->pos + 1;
+  int rc;
+  if ((rc = embed_launch(m->emb_qs, m->emb_sc, m->emb_type, m->toks, B, H, m->X, H, st))) return rc;
+  for (int l = 0; l < c.n_layers; ++l) {
+    Layer &y = m->L[l];
+    if ((rc = rmsnorm_launch(m->X, H, y.attn_norm, H, c.rms_eps, nullptr, 0, m->Xh, H, B, st))) return rc;
+    if (y.linear) {
+      const int C = (2 * c.gdn_nkh + c.gdn_nvh) * 128, Zh = c.gdn_nvh * 128;
+      GemvOut o1 = {m->qkv, nullptr, nullptr, C, 0};
+      GemvOut o2 = {m->z, nullptr, nullptr, Zh, 0};
+      GemvOut o3 = {m->ga, nullptr, nullptr, c.gdn_nvh, 0};
+      GemvOut o4 = {m->gb, nullptr, nullptr, c.gdn_nvh, 0};
+      if ((rc = gemv_launch(ctx, y.qkv, 1, 0, GEMV_EPI_STORE, m->Xh, o1, B, st)) ||
+          (rc = gemv_launch(ctx, y.gate_z, 1, 0, GEMV_EPI_STORE, m->Xh, o2, B, st)) ||
+          (rc = gemv_launch(ctx, y.alpha, 1, 0, GEMV_EPI_STORE, m->Xh, o3, B, st)) ||
+          (rc = gemv_launch(ctx, y.beta, 1, 0, GEMV_EPI_STORE, m->Xh, o4, B, st)))
+        return rc;
+      if ((rc = gdn_block_launch(y.gdn, m->qkv, C, m->z, Zh, m->ga, m->gb, c.gdn_nvh, y.ssm_conv, y.ssm_norm,
+                                 nullptr, 0, B, st, m->gh, Zh, y.ssm_a, y.ssm_dt)))
+        return rc;
+      y.gdn->last_B = B;
+      GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
+      if ((rc = gemv_launch(ctx, y.ssm_out, 1, 0, GEMV_EPI_STORE, m->gh, o5, B, st))) return rc;
+    } else {
+      const int Qo = c.n_head * c.head_dim, Ko = c.n_kv_head * c.head_dim;
+      GemvOut o1 = {m->qfull, nullptr, nullptr, 2 * Qo, 0};
+      GemvOut o2 = {m->kx, m->vx, nullptr, Ko, 0};
+      if ((rc = gemv_launch(ctx, y.wq, 1, 0, GEMV_EPI_STORE, m->Xh, o1, B, st)) ||
+          (rc = gemv_launch(ctx, y.wkv, 2, 0, GEMV_EPI_PAIR, m->Xh, o2, B, st)))
+        return rc;
+      if ((rc = attention_launch(m->qfull, m->kx, m->vx, Ko, y.q_norm, y.k_norm, m->qbuf, y.K, y.V, pbase, B,
+                                 c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot, c.rope_theta, c.rms_eps,
+                                 m->apart, c.max_ctx, m->yh, st)))
+        return rc;
+      GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
+      if ((rc = gemv_launch(ctx, y.wo, 1, 0, GEMV_EPI_STORE, m->yh, o5, B, st))) return rc;
+    }
+    if ((rc = rmsnorm_launch(m->X, H, y.post_norm, H, c.rms_eps, nullptr, 0, m->Xh, H, B, st))) return rc;
+    GemvOut f1 = {nullptr, nullptr, m->hh, 0, 0};
+    GemvOut f2 = {m->X, nullptr, nullptr, H, 1};
+    if ((rc = gemv_launch(ctx, y.ffn_gu, 2, 0, GEMV_EPI_SWIGLU, m->Xh, f1, B, st)) ||
+        (rc = gemv_launch(ctx, y.ffn_down, 1, 0, GEMV_EPI_STORE, m->hh, f2, B, st)))
+      return rc;
+    (void)I;
+  }
+  if (head) {
+    if ((rc = rmsnorm_launch(m->X, H, m->out_norm, H, c.rms_eps, nullptr, 0, m->Xh, H, B, st))) return rc;
+    GemvOut o = {m->logits, nullptr, nullptr, c.vocab, 0,
+                 {ctx->amax_keys, ctx->amax_cnt, m->drafts, E, m->res}};
+    if ((rc = gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, m->Xh, o, B, st))) return rc;
+  }
+  return CWEN_OK;
+}
+
+void commit(cwen_model *m, int n) {
+  for (int l = 0; l < m->cfg.n_layers; ++l)
+    if (m->L[l].linear) cwen_gdn_commit(m->L[l].gdn, n);
+  m->pos += n;
+}
+
+int ready(const cwen_model *m) {
+  if (!m->emb_qs || !m->out_norm || !m->head) return 0;
+  for (int l = 0; l < m->cfg.n_layers; ++l) {
+    const Layer &y = m->L[l];
+    if (!y.attn_norm || !y.post_norm || !y.ffn_gu || !y.ffn_down) return 0;
+    if (y.linear && (!y.qkv || !y.gate_z || !y.alpha || !y.beta || !y.ssm_out || !y.ssm_a || !y.ssm_dt ||
+                     !y.ssm_conv || !y.ssm_norm))
+      return 0;
+    if (!y.linear && (!y.wq || !y.wkv || !y.wo || !y.q_norm || !y.k_norm)) return 0;
+  }
+  return 1;
+}
+
+int set_tokens(cwen_model *m, const int *toks, int B, hipStream_t st) {
+  for (int b = 0; b < B; ++b)
+    if (toks[b] < 0 || toks[b] >= m->cfg.vocab) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipMemcpyAsync(m->toks, toks, (size_t)B * sizeof(int), hipMemcpyHostToDevice, st));
+  return CWEN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out) {
+  if (!ctx || !out) return CWEN_EINVAL;
+  *out = nullptr;
+  int rc = check_cfg(cfg);
+  if (rc) return rc;
+  CWEN_HIP_TRY(hipSetDevice(ctx->device));
+  cwen_model *m = new (std::nothrow) cwen_model();
+  if (!m) return CWEN_ENOMEM;
+  m->ctx = ctx;
+  m->cfg = *cfg;
+  const cwen_model_cfg &c = m->cfg;
+  m->L = new (std::nothrow) Layer[c.n_layers];
+  if (!m->L) { delete m; return CWEN_ENOMEM; }
+  const int H = c.d_model, I = c.d_ffn, BM = CWEN_BMAX;
+  const int C = (2 * c.gdn_nkh + c.gdn_nvh) * 128, Zh = c.gdn_nvh * 128;
+  const int Qo = c.n_head * c.head_dim, Ko = c.n_kv_head * c.head_dim;
+  rc = CWEN_OK;
+  for (int l = 0; l < c.n_layers && !rc; ++l) {
+    Layer &y = m->L[l];
+    y.linear = !is_full(c, l);
+    if (y.linear) {
+      rc = cwen_gdn_create(ctx, c.gdn_nkh, c.gdn_nvh, 128, &y.gdn);
+    } else {
+      const size_t kv = (size_t)c.max_ctx * Ko;
+      rc = dmalloc(&y.K, kv) || dmalloc(&y.V, kv) ? CWEN_ENOMEM : CWEN_OK;
+    }
+  }
+  if (!rc)
+    rc = (dmalloc(&m->toks, BM) || dmalloc(&m->drafts, BM) || dmalloc(&m->res, 2 + BM) ||
+          dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->Xh, (size_t)BM * H) ||
+          dmalloc(&m->qkv, (size_t)BM * C) || dmalloc(&m->z, (size_t)BM * Zh) ||
+          dmalloc(&m->ga, (size_t)BM * c.gdn_nvh) || dmalloc(&m->gb, (size_t)BM * c.gdn_nvh) ||
+          dmalloc(&m->gh, (size_t)BM * Zh) || dmalloc(&m->qfull, (size_t)BM * 2 * Qo) ||
+          dmalloc(&m->kx, (size_t)BM * Ko) || dmalloc(&m->vx, (size_t)BM * Ko) ||
+          dmalloc(&m->qbuf, (size_t)BM * Qo) ||
+          dmalloc(&m->apart, attn_partial_floats(c.n_head, c.n_kv_head, c.max_ctx, BM)) ||
+          dmalloc(&m->yh, (size_t)BM * Qo) || dmalloc(&m->hh, (size_t)BM * I) ||
+          dmalloc(&m->logits, (size_t)BM * c.vocab))
+             ? CWEN_ENOMEM
+             : CWEN_OK;
+  if (!rc && hipHostMalloc((void **)&m->hres, (2 + BM) * sizeof(int), hipHostMallocDefault) != hipSuccess)
+    rc = CWEN_ENOMEM;
+  if (rc) {
+    cwen_model_free(m);
+    return rc;
+  }
+  *out = m;
+  return CWEN_OK;
+}
+
+int cwen_model_free(cwen_model *m) {
+  if (!m) return CWEN_EINVAL;
+  (void)hipSetDevice(m->ctx->device);
+  (void)hipDeviceSynchronize();
+  for (int l = 0; m->L && l < m->cfg.n_layers; ++l) {
+    Layer &y = m->L[l];
+    for (float *p : {y.attn_norm, y.post_norm, y.ssm_a, y.ssm_dt, y.ssm_conv, y.ssm_norm, y.q_norm, y.k_norm, y.K,
+                     y.V})
+      if (p) (void)hipFree(p);
+    for (cwen_weight *w : {y.ffn_gu, y.ffn_down, y.qkv, y.gate_z, y.alpha, y.beta, y.ssm_out, y.wq, y.wkv, y.wo})
+      if (w) cwen_weight_free(w);
+    if (y.gdn) cwen_gdn_free(y.gdn);
+  }
+  delete[] m->L;
+  for (void *p : {(void *)m->emb_qs, (void *)m->emb_sc, (void *)m->out_norm, (void *)m->toks, (void *)m->drafts,
+                  (void *)m->res, (void *)m->X, (void *)m->Xh, (void *)m->qkv, (void *)m->z, (void *)m->ga,
+                  (void *)m->gb, (void *)m->gh, (void *)m->qfull, (void *)m->kx, (void *)m->vx, (void *)m->qbuf,
+                  (void *)m->apart, (void *)m->yh, (void *)m->hh, (void *)m->logits})
+    if (p) (void)hipFree(p);
+  if (m->head) cwen_weight_free(m->head);
+  if (m->hres) (void)hipHostFree(m->hres);
+  delete m;
+  return CWEN_OK;
+}
+
+int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data, const void *scales,
+                   int ne0, int ne1) {
+  if (!m || !data) return CWEN_EINVAL;
+  const cwen_model_cfg &c = m->cfg;
+  const int H = c.d_model, I = c.d_ffn;
+  const int C = (2 * c.gdn_nkh + c.gdn_nvh) * 128, Zh = c.gdn_nvh * 128;
+  const int Qo = c.n_head * c.head_dim, Ko = c.n_kv_head * c.head_dim;
+  CWEN_HIP_TRY(hipSetDevice(m->ctx->device));
+  const bool f32 = type == CWEN_T_F32;
+  if (id == CWEN_TOK_EMBD) {  // rows dequantised one token at a time (embed_token_to)
+    if ((type != CWEN_T_Q4_0 && type != CWEN_T_Q4_0RS) || ne0 != H || ne1 != c.vocab) return CWEN_EINVAL;
+    if (type == CWEN_T_Q4_0RS && !scales) return CWEN_EINVAL;
+    const size_t nblk = (size_t)(H / 32) * c.vocab;
+    if (m->emb_qs) (void)hipFree(m->emb_qs);
+    if (m->emb_sc) (void)hipFree(m->emb_sc);
+    m->emb_qs = nullptr; m->emb_sc = nullptr;
+    const size_t qb = type == CWEN_T_Q4_0 ? nblk * 18 : nblk * 16;
+    if (dmalloc(&m->emb_qs, qb)) return CWEN_ENOMEM;
+    CWEN_HIP_TRY(hipMemcpy(m->emb_qs, data, qb, hipMemcpyHostToDevice));
+    if (type == CWEN_T_Q4_0RS) {
+      if (dmalloc(&m->emb_sc, nblk)) return CWEN_ENOMEM;
+      CWEN_HIP_TRY(hipMemcpy(m->emb_sc, scales, nblk * 2, hipMemcpyHostToDevice));
+    }
+    m->emb_type = type;
+    return CWEN_OK;
+  }
+  if (id == CWEN_OUTPUT_NORM) return (f32 && ne0 == H) ? upload_f32(data, H, &m->out_norm) : CWEN_EINVAL;
+  if (id == CWEN_OUTPUT) return f32 ? CWEN_ETYPE : upload_w(m, type, data, scales, ne0, ne1, H, c.vocab, &m->head);
+  if (layer < 0 || layer >= c.n_layers) return CWEN_EINVAL;
+  Layer &y = m->L[layer];
+  switch (id) {
+    case CWEN_ATTN_NORM: return (f32 && ne0 == H) ? upload_f32(data, H, &y.attn_norm) : CWEN_EINVAL;
+    case CWEN_POST_NORM: return (f32 && ne0 == H) ? upload_f32(data, H, &y.post_norm) : CWEN_EINVAL;
+    case CWEN_FFN_GATE_UP:
+      return type == CWEN_T_Q4_0RSI ? upload_w(m, type, data, scales, ne0, ne1, H, I, &y.ffn_gu) : CWEN_ETYPE;
+    case CWEN_FFN_DOWN: return upload_w(m, type, data, scales, ne0, ne1, I, H, &y.ffn_down);
+    default: break;
+  }
+  if (y.linear) {
+    switch (id) {
+      case CWEN_ATTN_QKV: return upload_w(m, type, data, scales, ne0, ne1, H, C, &y.qkv);
+      case CWEN_ATTN_GATE: return upload_w(m, type, data, scales, ne0, ne1, H, Zh, &y.gate_z);
+      case CWEN_SSM_ALPHA: return upload_w(m, type, data, scales, ne0, ne1, H, c.gdn_nvh, &y.alpha);
+      case CWEN_SSM_BETA: return upload_w(m, type, data, scales, ne0, ne1, H, c.gdn_nvh, &y.beta);
+      case CWEN_SSM_OUT: return upload_w(m, type, data, scales, ne0, ne1, Zh, H, &y.ssm_out);
+      case CWEN_SSM_A: return (f32 && ne0 == c.gdn_nvh) ? upload_f32(data, ne0, &y.ssm_a) : CWEN_EINVAL;
+      case CWEN_SSM_DT: return (f32 && ne0 == c.gdn_nvh) ? upload_f32(data, ne0, &y.ssm_dt) : CWEN_EINVAL;
+      case CWEN_SSM_CONV: return (f32 && ne0 == 4 * C) ? upload_f32(data, ne0, &y.ssm_conv) : CWEN_EINVAL;
+      case CWEN_SSM_NORM: return (f32 && ne0 == 128) ? upload_f32(data, ne0, &y.ssm_norm) : CWEN_EINVAL;
+      default: return CWEN_EINVAL;
+    }
+  }
+  switch (id) {
+    case CWEN_ATTN_Q: return upload_w(m, type, data, scales, ne0, ne1, H, 2 * Qo, &y.wq);
+    case CWEN_ATTN_KV:
+      return type == CWEN_T_Q4_0RSI ? upload_w(m, type, data, scales, ne0, ne1, H, Ko, &y.wkv) : CWEN_ETYPE;
+    case CWEN_ATTN_OUTPUT: return upload_w(m, type, data, scales, ne0, ne1, Qo, H, &y.wo);
+    case CWEN_ATTN_Q_NORM: return (f32 && ne0 == c.head_dim) ? upload_f32(data, ne0, &y.q_norm) : CWEN_EINVAL;
+    case CWEN_ATTN_K_NORM: return (f32 && ne0 == c.head_dim) ? upload_f32(data, ne0, &y.k_norm) : CWEN_EINVAL;
+    default: return CWEN_EINVAL;
+  }
+}
+
+int cwen_model_reset(cwen_model *m) {
+  if (!m) return CWEN_EINVAL;
+  for (int l = 0; l < m->cfg.n_layers; ++l)
+    if (m->L[l].linear) {
+      int rc = cwen_gdn_set_state(m->L[l].gdn, nullptr, nullptr);
+      if (rc) return rc;
+    }
+  m->pos = -1;
+  return CWEN_OK;
+}
+
+int cwen_model_pos(const cwen_model *m) { return m ? m->pos : CWEN_EINVAL; }
+
+int cwen_model_capacity(const cwen_model *m) { return m ? m->cfg.max_ctx : CWEN_EINVAL; }
+
+int cwen_model_forward(cwen_model *m, const int *toks, int B, int want_argmax, int *argmax_out, void *stream) {
+  if (!m || !toks || B < 1 || B > CWEN_BMAX || !ready(m)) return CWEN_EINVAL;
+  if (m->pos + B >= m->cfg.max_ctx) return CWEN_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  int rc;
+  if ((rc = set_tokens(m, toks, B, st)) || (rc = block(m, B, want_argmax ? 1 : 0, 0, st))) return rc;
+  if (want_argmax) {
+    CWEN_HIP_TRY(hipMemcpyAsync(m->hres, m->res, (2 + B) * sizeof(int), hipMemcpyDeviceToHost, st));
+    CWEN_HIP_TRY(hipStreamSynchronize(st));
+    if (argmax_out) memcpy(argmax_out, m->hres + 2, (size_t)B * sizeof(int));
+  }
+  commit(m, B);
+  return CWEN_OK;
+}
+
+int cwen_model_verify(cwen_model *m, const int *blk, int B, int *k_out, int *bonus_out, void *stream) {
+  if (!m || !blk || B < 1 || B > CWEN_BMAX || !ready(m)) return CWEN_EINVAL;
+  if (m->pos + B >= m->cfg.max_ctx) return CWEN_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  int rc;
+  if ((rc = set_tokens(m, blk, B, st))) return rc;
+  if (B > 1) CWEN_HIP_TRY(hipMemcpyAsync(m->drafts, m->toks + 1, (size_t)(B - 1) * sizeof(int),
+                                         hipMemcpyDeviceToDevice, st));
+  if ((rc = block(m, B, 1, B - 1, st))) return rc;
+  CWEN_HIP_TRY(hipMemcpyAsync(m->hres, m->res, 2 * sizeof(int), hipMemcpyDeviceToHost, st));
+  CWEN_HIP_TRY(hipStreamSynchronize(st));
+  const int k = m->hres[0];
+  if (k < 0 || k > B - 1) return CWEN_EHIP;
+  commit(m, k + 1);
+  if (k_out) *k_out = k;
+  if (bonus_out) *bonus_out = m->hres[1];
+  return CWEN_OK;
+}
+
+int cwen_model_logits(cwen_model *m, float *host, int rows) {
+  if (!m || !host || rows < 1 || rows > CWEN_BMAX) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipDeviceSynchronize());
+  CWEN_HIP_TRY(hipMemcpy(host, m->logits, (size_t)rows * m->cfg.vocab * sizeof(float), hipMemcpyDeviceToHost));
+  return CWEN_OK;
+}
+
+}  // extern "C"

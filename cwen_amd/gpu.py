@@ -12,6 +12,7 @@ from pathlib import Path
 import numpy as np
 
 LIB_PATH = Path(__file__).resolve().parent / "libcwen_gpu.so"
+HOST_LIB_PATH = Path(__file__).resolve().parent / "libcwen_host.so"
 
 CWEN_OK = 0
 ERRORS = {-1: "EINVAL", -2: "EHIP", -3: "ENOMEM", -4: "ETYPE", -5: "ESCRATCH"}
@@ -44,6 +45,24 @@ SIGNATURES = [
     ("cwen_gdn_get_state", _I, [_VP, _I, _VP, _VP]),
     ("cwen_gdn_block", _I, [_VP, _VP, _VP, _I, _VP, _I, _VP, _VP, _I, _VP, _VP, _VP, _I, _I, _VP]),
     ("cwen_gdn_commit", _I, [_VP, _I]),
+    ("cwen_model_create", _I, [_VP, _VP, C.POINTER(_VP)]),
+    ("cwen_model_free", _I, [_VP]),
+    ("cwen_model_set", _I, [_VP, _I, _I, _I, _VP, _VP, _I, _I]),
+    ("cwen_model_reset", _I, [_VP]),
+    ("cwen_model_pos", _I, [_VP]),
+    ("cwen_model_capacity", _I, [_VP]),
+    ("cwen_model_forward", _I, [_VP, _VP, _I, _I, _VP, _VP]),
+    ("cwen_model_verify", _I, [_VP, _VP, _I, C.POINTER(_I), C.POINTER(_I), _VP]),
+    ("cwen_model_logits", _I, [_VP, _VP, _I]),
+]
+
+# libcwen_host.so (include/.. cwen_amd/host/cwen_host.h)
+HOST_SIGNATURES = [
+    ("cwen_spec_default", None, [_VP]),
+    ("cwen_ngram_draft", _I, [_VP, _I, _VP, _I, _I]),
+    ("cwen_prefill", _I, [_VP, _VP, _I, C.POINTER(_I)]),
+    ("cwen_generate_serial", _I, [_VP, _VP, _I, _I, _VP]),
+    ("cwen_generate_spec", _I, [_VP, _VP, _I, _I, _VP, _VP, _VP]),
 ]
 
 
@@ -68,6 +87,24 @@ def lib() -> C.CDLL:
             f.argtypes = args
         _lib = L
     return _lib
+
+
+_hlib = None
+
+
+def host_lib() -> C.CDLL:
+    global _hlib
+    if _hlib is None:
+        lib()  # the host library resolves libcwen_gpu.so next to it
+        if not HOST_LIB_PATH.exists():
+            raise RuntimeError(f"{HOST_LIB_PATH} is not built; run `python -m cwen_amd.build`")
+        L = C.CDLL(str(HOST_LIB_PATH))
+        for name, res, args in HOST_SIGNATURES:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _hlib = L
+    return _hlib
 
 
 def check(fn: str, rc: int) -> None:
@@ -244,6 +281,102 @@ class GDN:
     def free(self) -> None:
         if self.h:
             lib().cwen_gdn_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- model
+class ModelCfg(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layers", "d_model", "d_ffn", "vocab", "n_head", "n_kv_head",
+                                        "head_dim", "n_rot_pairs", "n_rot", "gdn_nkh", "gdn_nvh", "gdn_dk",
+                                        "full_interval", "max_ctx")] + \
+              [("rope_theta", C.c_float), ("rms_eps", C.c_float)]
+
+
+(TOK_EMBD, OUTPUT_NORM, OUTPUT, ATTN_NORM, POST_NORM, FFN_GATE_UP, FFN_DOWN, ATTN_QKV, ATTN_GATE, SSM_ALPHA,
+ SSM_BETA, SSM_A, SSM_DT, SSM_CONV, SSM_NORM, SSM_OUT, ATTN_Q, ATTN_KV, ATTN_OUTPUT, ATTN_Q_NORM,
+ ATTN_K_NORM) = range(21)
+
+
+class SpecCfg(C.Structure):
+    _fields_ = [("n_key", C.c_int), ("max_draft", C.c_int), ("min_draft", C.c_int), ("cooldown", C.c_int)]
+
+
+class SpecStats(C.Structure):
+    _fields_ = [("cycles", C.c_longlong), ("drafted", C.c_longlong), ("full", C.c_longlong),
+                ("rejected", C.c_longlong), ("kept", C.c_longlong), ("prefill_tokens", C.c_int)]
+
+
+class Model:
+    """The block-verify model on one device (cwen_model_* of the C ABI)."""
+
+    def __init__(self, ctx: Context, **cfg):
+        self.cfg = ModelCfg(**cfg)
+        h = C.c_void_p()
+        check("cwen_model_create", lib().cwen_model_create(ctx.h, C.byref(self.cfg), C.byref(h)))
+        self.h, self.ctx = h, ctx
+
+    def set(self, layer: int, tid: int, wtype: int, data: np.ndarray, scales: np.ndarray | None,
+            ne0: int, ne1: int) -> None:
+        data = np.ascontiguousarray(data)
+        sc = None if scales is None else np.ascontiguousarray(scales)
+        check("cwen_model_set", lib().cwen_model_set(self.h, layer, tid, wtype, data.ctypes.data,
+                                                     None if sc is None else sc.ctypes.data, ne0, ne1))
+
+    def reset(self) -> None:
+        check("cwen_model_reset", lib().cwen_model_reset(self.h))
+
+    @property
+    def pos(self) -> int:
+        return lib().cwen_model_pos(self.h)
+
+    def forward(self, toks, want_argmax: bool = True) -> np.ndarray | None:
+        t = np.ascontiguousarray(toks, dtype=np.int32)
+        am = np.zeros(t.size, dtype=np.int32)
+        check("cwen_model_forward", lib().cwen_model_forward(self.h, t.ctypes.data, t.size, int(want_argmax),
+                                                             am.ctypes.data if want_argmax else None, None))
+        return am if want_argmax else None
+
+    def verify(self, blk) -> tuple[int, int]:
+        t = np.ascontiguousarray(blk, dtype=np.int32)
+        k, bonus = C.c_int(), C.c_int()
+        check("cwen_model_verify", lib().cwen_model_verify(self.h, t.ctypes.data, t.size, C.byref(k),
+                                                           C.byref(bonus), None))
+        return k.value, bonus.value
+
+    def logits(self, rows: int) -> np.ndarray:
+        out = np.empty((rows, self.cfg.vocab), dtype=np.float32)
+        check("cwen_model_logits", lib().cwen_model_logits(self.h, out.ctypes.data, rows))
+        return out
+
+    def generate_serial(self, prompt, n_gen: int) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(n_gen, dtype=np.int32)
+        n = host_lib().cwen_generate_serial(self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data)
+        if n < 0:
+            raise CwenError("cwen_generate_serial", n)
+        return out[:n]
+
+    def generate_spec(self, prompt, n_gen: int, n_key: int = 16, max_draft: int = 8, min_draft: int = 2,
+                      cooldown: int = 8) -> tuple[np.ndarray, SpecStats]:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(n_gen, dtype=np.int32)
+        cfg = SpecCfg(n_key, max_draft, min_draft, cooldown)
+        st = SpecStats()
+        n = host_lib().cwen_generate_spec(self.h, p.ctypes.data, p.size, n_gen, C.byref(cfg), out.ctypes.data,
+                                          C.byref(st))
+        if n < 0:
+            raise CwenError("cwen_generate_spec", n)
+        return out[:n], st
+
+    def free(self) -> None:
+        if self.h:
+            lib().cwen_model_free(self.h)
             self.h = None
 
     def __del__(self):

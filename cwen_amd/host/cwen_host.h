@@ -1,0 +1,57 @@
+/* cwen_host.h -- host-side decode drivers over the cwen_gpu C ABI.
+ *
+ * Plain C: the greedy serial decode loop and the speculative block-verify
+ * loop of the reference engine (maci0/cwen run.c generate_tokens 5027-5045,
+ * generate_tokens_spec 4882-5025), with its history-scan n-gram drafter
+ * (ngram_draft 4533-4549).  Every forward pass runs on the device through
+ * cwen_model_forward / cwen_model_verify; per cycle only token ids go down
+ * and (k, bonus) comes back.
+ */
+#ifndef CWEN_HOST_H
+#define CWEN_HOST_H
+#include "cwen_gpu.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Speculation knobs (run.c:193-198 Scfg_*). */
+typedef struct {
+  int n_key;       /* n-gram lookup key length (16)            */
+  int max_draft;   /* drafts per block, <= CWEN_BMAX - 1 (8)   */
+  int min_draft;   /* a proposal shorter than this is dropped (2) */
+  int cooldown;    /* plain steps after 3 short walks (8)      */
+} cwen_spec_cfg;
+
+typedef struct {
+  long long cycles, drafted, full, rejected, kept;  /* run.c:4891 counters */
+  int prefill_tokens;
+} cwen_spec_stats;
+
+/* Default knobs of the reference. */
+void cwen_spec_default(cwen_spec_cfg *cfg);
+
+/* ngram_draft (run.c:4533-4549): the continuation of the most recent earlier
+ * occurrence of the last n_key history tokens, preferring an older match
+ * with a longer continuation; up to max_d ids into out.  Returns the count. */
+int cwen_ngram_draft(const int *h, int hn, int *out, int n_key, int max_d);
+
+/* prefill_forward (run.c:4823-4857): reset the model, score the prompt in
+ * blocks of up to 16 positions and return the argmax after the last prompt
+ * token in *next. */
+int cwen_prefill(cwen_model *m, const int *prompt, int n_prompt, int *next);
+
+/* generate_tokens (run.c:5027-5045): prefill, then n_gen greedy tokens, one
+ * position per forward pass.  Returns the number of tokens written to out
+ * (fewer than n_gen only when the context fills), or a negative status. */
+int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_gen, int *out);
+
+/* generate_tokens_spec (run.c:4882-5025) with the n-gram drafter: the same
+ * token stream as cwen_generate_serial, produced by block-verify cycles. */
+int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen, const cwen_spec_cfg *cfg,
+                       int *out, cwen_spec_stats *stats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CWEN_HOST_H */

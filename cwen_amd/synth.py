@@ -106,3 +106,68 @@ def rsi_side(qs: np.ndarray, sc: np.ndarray, M: int, K: int, side: int) -> tuple
     q = qs.reshape(M, nb, 2, 16)[:, :, side, :]
     s = sc.reshape(M, nb, 2)[:, :, side]
     return np.ascontiguousarray(q).reshape(-1), np.ascontiguousarray(s).reshape(-1)
+
+
+# ---------------------------------------------------------------- whole model
+def model_tensors(cfg: dict, seed: int = 0):
+    """Seeded random-init tensors of the hybrid decoder, in the reference's
+    layouts: yields (layer, tensor id, type, data, scales, ne0, ne1); layer -1
+    for the global tensors.  Q4_0 matrices are CWENR (RS, or RSI for the
+    gate/up and k/v pairs), the head Q6_K, the embedding Q4_0RS; norms, conv
+    taps and gate parameters F32."""
+    from . import gpu as G
+    H, I, V = cfg["d_model"], cfg["d_ffn"], cfg["vocab"]
+    nkh, nvh = cfg["gdn_nkh"], cfg["gdn_nvh"]
+    C = (2 * nkh + nvh) * 128
+    Zh = nvh * 128
+    Qo, Ko = cfg["n_head"] * cfg["head_dim"], cfg["n_kv_head"] * cfg["head_dim"]
+    f32 = np.float32
+
+    def norm_w(key, n):
+        return (1 + 0.1 * rng(seed, 20, key).standard_normal(n)).astype(f32)
+
+    qs, sc = q4_rs(seed, V, H, key=1000)
+    yield -1, G.TOK_EMBD, G.T_Q4_0RS, qs, sc, H, V
+    yield -1, G.OUTPUT_NORM, G.T_F32, norm_w(1, H), None, H, 1
+    yield -1, G.OUTPUT, G.T_Q6_K, q6_k(seed, V, H, key=1001), None, H, V
+    for l in range(cfg["n_layers"]):
+        k0 = 100 * (l + 1)
+        full = l % cfg["full_interval"] == cfg["full_interval"] - 1
+        yield l, G.ATTN_NORM, G.T_F32, norm_w(k0 + 1, H), None, H, 1
+        yield l, G.POST_NORM, G.T_F32, norm_w(k0 + 2, H), None, H, 1
+        qs, sc = q4_rsi(seed, I, H, key=k0 + 3)
+        yield l, G.FFN_GATE_UP, G.T_Q4_0RSI, qs, sc, H, I
+        qs, sc = q4_rs(seed, H, I, key=k0 + 4)
+        yield l, G.FFN_DOWN, G.T_Q4_0RS, qs, sc, I, H
+        if not full:
+            for tid, M, key in ((G.ATTN_QKV, C, 5), (G.ATTN_GATE, Zh, 6), (G.SSM_ALPHA, nvh, 7),
+                                (G.SSM_BETA, nvh, 8)):
+                qs, sc = q4_rs(seed, M, H, key=k0 + key)
+                yield l, tid, G.T_Q4_0RS, qs, sc, H, M
+            qs, sc = q4_rs(seed, H, Zh, key=k0 + 9)
+            yield l, G.SSM_OUT, G.T_Q4_0RS, qs, sc, Zh, H
+            g = rng(seed, 21, k0)
+            yield l, G.SSM_A, G.T_F32, (-np.exp(g.uniform(-1, 1, nvh))).astype(f32), None, nvh, 1
+            yield l, G.SSM_DT, G.T_F32, (0.5 * g.standard_normal(nvh)).astype(f32), None, nvh, 1
+            yield l, G.SSM_CONV, G.T_F32, (0.3 * g.standard_normal(4 * C)).astype(f32), None, 4 * C, 1
+            yield l, G.SSM_NORM, G.T_F32, norm_w(k0 + 10, 128), None, 128, 1
+        else:
+            qs, sc = q4_rs(seed, 2 * Qo, H, key=k0 + 11)
+            yield l, G.ATTN_Q, G.T_Q4_0RS, qs, sc, H, 2 * Qo
+            qs, sc = q4_rsi(seed, Ko, H, key=k0 + 12)
+            yield l, G.ATTN_KV, G.T_Q4_0RSI, qs, sc, H, Ko
+            qs, sc = q4_rs(seed, H, Qo, key=k0 + 13)
+            yield l, G.ATTN_OUTPUT, G.T_Q4_0RS, qs, sc, Qo, H
+            yield l, G.ATTN_Q_NORM, G.T_F32, norm_w(k0 + 14, cfg["head_dim"]), None, cfg["head_dim"], 1
+            yield l, G.ATTN_K_NORM, G.T_F32, norm_w(k0 + 15, cfg["head_dim"]), None, cfg["head_dim"], 1
+
+
+def prompt_tokens(seed: int, n: int, V: int, period: int = 37, noise: float = 0.1) -> np.ndarray:
+    """A seeded token history with periodic repeats: a random motif repeated,
+    with a fraction `noise` of positions replaced by random ids."""
+    g = rng(seed, 30)
+    motif = g.integers(0, V, period)
+    t = np.resize(motif, n)
+    flip = g.random(n) < noise
+    t[flip] = g.integers(0, V, int(flip.sum()))
+    return t.astype(np.int32)

@@ -168,6 +168,78 @@ int cwen_gdn_block(cwen_ctx *ctx, cwen_gdn *g, const float *qkv, int qs, const f
  * for this layer. */
 int cwen_gdn_commit(cwen_gdn *g, int n);
 
+/* ---- the block-verify model ----
+ * The reference's hybrid decoder (run.c:80-92, 140-160) resident on one
+ * device: layer l is full attention when l % full_interval ==
+ * full_interval - 1 (run.c FULL_INT), otherwise GatedDeltaNet.  One model
+ * replaces the reference's globals W[], tok_embd, output(_norm), Srec,
+ * Cstate, Kcache/Vcache and the block scratch of alloc_state. */
+typedef struct {
+  int n_layers, d_model, d_ffn, vocab;        /* L, H, I, V                      */
+  int n_head, n_kv_head, head_dim;            /* NH, NKV, HD (HD must be 256)    */
+  int n_rot_pairs, n_rot;                     /* RoPE pairs (32) and NROT (64)   */
+  int gdn_nkh, gdn_nvh, gdn_dk;               /* LKH, LVH, LSD (LSD must be 128) */
+  int full_interval;                          /* FULL_INT                        */
+  int max_ctx;                                /* KV / position capacity          */
+  float rope_theta, rms_eps;                  /* ROPE_THETA, RMS_EPS             */
+} cwen_model_cfg;
+typedef struct cwen_model cwen_model;
+
+/* Tensor ids of cwen_model_set, named after the GGUF tensors the reference
+ * binds (run.c:3367-3406). */
+enum {
+  CWEN_TOK_EMBD = 0,     /* token_embd.weight      Q4_0 / Q4_0RS, [V][H]          */
+  CWEN_OUTPUT_NORM,      /* output_norm.weight     F32 [H]                        */
+  CWEN_OUTPUT,           /* output.weight          any GEMV type, [V][H]          */
+  CWEN_ATTN_NORM,        /* blk.l.attn_norm        F32 [H]                        */
+  CWEN_POST_NORM,        /* blk.l.post_attention_norm F32 [H]                     */
+  CWEN_FFN_GATE_UP,      /* ffn_gate + ffn_up      Q4_0RSI pair [I][H]            */
+  CWEN_FFN_DOWN,         /* ffn_down               [H][I]                         */
+  CWEN_ATTN_QKV,         /* attn_qkv (GDN)         [C][H], C = (2 LKH + LVH) LSD  */
+  CWEN_ATTN_GATE,        /* attn_gate (GDN z)      [LVH*LSD][H]                   */
+  CWEN_SSM_ALPHA,        /* ssm_alpha              [LVH][H]                       */
+  CWEN_SSM_BETA,         /* ssm_beta               [LVH][H]                       */
+  CWEN_SSM_A,            /* ssm_a                  F32 [LVH]                      */
+  CWEN_SSM_DT,           /* ssm_dt.bias            F32 [LVH]                      */
+  CWEN_SSM_CONV,         /* ssm_conv1d             F32 [C][4]                     */
+  CWEN_SSM_NORM,         /* ssm_norm               F32 [LSD]                      */
+  CWEN_SSM_OUT,          /* ssm_out                [H][LVH*LSD]                   */
+  CWEN_ATTN_Q,           /* attn_q (q|gate per head) [2*NH*HD][H]                 */
+  CWEN_ATTN_KV,          /* attn_k + attn_v        Q4_0RSI pair [NKV*HD][H]       */
+  CWEN_ATTN_OUTPUT,      /* attn_output            [H][NH*HD]                     */
+  CWEN_ATTN_Q_NORM,      /* attn_q_norm            F32 [HD]                       */
+  CWEN_ATTN_K_NORM       /* attn_k_norm            F32 [HD]                       */
+};
+
+int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out);
+int cwen_model_free(cwen_model *m);
+/* Upload one tensor from HOST memory (layer ignored for the global ones);
+ * quantized types go through cwen_weight_upload's repack. */
+int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data, const void *scales,
+                   int ne0, int ne1);
+/* Empty context: position -1, GDN states and conv histories zero (reset_state). */
+int cwen_model_reset(cwen_model *m);
+/* Last filled position (the reference's pos_n). */
+int cwen_model_pos(const cwen_model *m);
+/* Position capacity (max_ctx; the reference's g_ctx). */
+int cwen_model_capacity(const cwen_model *m);
+/* forward_block (run.c:2752-2779): score HOST token ids toks[0..B-1] at
+ * positions pos+1..pos+B and advance by B.  With want_argmax the head runs
+ * on every row and argmax_out (HOST, B ints, nullable) receives each row's
+ * argmax_of; without it the head is skipped (prefill chunks).  Synchronous
+ * when want_argmax. */
+int cwen_model_forward(cwen_model *m, const int *toks, int B, int want_argmax, int *argmax_out, void *stream);
+/* One speculative verify cycle on the device: score blk[0..B-1] (blk[0] the
+ * pending token, blk[1..B-1] the drafts), take the per-row argmax, walk the
+ * drafts (run.c:4954-4956) and keep the accepted prefix: the state advances
+ * by k+1 positions (GDN snapshots committed, KV slots past the prefix are
+ * rewritten before any read).  Only k and the bonus token return to the
+ * host.  B = 1 is the serial decode step (forward_ex + argmax_of).
+ * Synchronous. */
+int cwen_model_verify(cwen_model *m, const int *blk, int B, int *k, int *bonus, void *stream);
+/* Copy the f32 logits of the last head pass (rows 0..rows-1) to HOST. */
+int cwen_model_logits(cwen_model *m, float *host, int rows);
+
 /* ---- f16 activation operands ----
  * The kernels read activations as IEEE half, row-major [B][K] with row stride
  * exactly K (2-byte elements, 16-byte aligned rows).  These entry points let a

@@ -56,6 +56,9 @@ class Oracle:
         L.orc_walk.argtypes = [_VP, C.c_long, _I, _VP, _I, C.POINTER(_I)]
         L.orc_ngram_draft.restype = _I
         L.orc_ngram_draft.argtypes = [_VP, _I, _VP, _I, _I]
+        L.orc_embed_q4.argtypes = [_VP, _VP, _I, _I, _I, _VP]
+        L.orc_rope_apply.argtypes = [_VP, _I, _I, _I, _I, _I, _F]
+        L.orc_attention.argtypes = [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _I, _VP]
         self.L = L
 
     def gemvb(self, wtype: int, data: np.ndarray, scales, K: int, M: int, X: np.ndarray,
@@ -115,6 +118,29 @@ class Oracle:
         n = self.L.orc_ngram_draft(_i32p(h), h.size, _i32p(out), n_key, max_d)
         return out[:n]
 
+    def embed(self, wtype: int, qs: np.ndarray, sc, token: int, H: int) -> np.ndarray:
+        out = np.empty(H, dtype=np.float32)
+        self.L.orc_embed_q4(qs.ctypes.data, None if sc is None else sc.ctypes.data, wtype, token, H, _f32p(out))
+        return out
+
+    def rope(self, q: np.ndarray, pos: int, npairs: int = 32, nrot: int = 64, theta: float = 1e7) -> np.ndarray:
+        q = np.array(q, dtype=np.float32, copy=True)
+        hd = q.shape[-1]
+        self.L.orc_rope_apply(_f32p(q), q.size // hd, hd, pos, npairs, nrot, theta)
+        return q
+
+    def attention(self, K: np.ndarray, V: np.ndarray, t0: int, pos: int, q: np.ndarray,
+                  gate: np.ndarray) -> np.ndarray:
+        """K, V [t][nkv][hd]; q, gate [nh][hd] -> out [nh][hd]."""
+        K = np.ascontiguousarray(K, np.float32)
+        V = np.ascontiguousarray(V, np.float32)
+        q = np.ascontiguousarray(q, np.float32)
+        gate = np.ascontiguousarray(gate, np.float32)
+        nkv, hd = K.shape[1], K.shape[2]
+        out = np.empty_like(q)
+        self.L.orc_attention(_f32p(K), _f32p(V), nkv, hd, t0, pos, _f32p(q), _f32p(gate), q.shape[0], _f32p(out))
+        return out
+
 
 def cpu_has_avx512() -> bool:
     try:
@@ -157,6 +183,13 @@ class Reference:
         L.ref_ngram_draft.restype = _I
         L.ref_ngram_draft.argtypes = [_VP, _I, _VP, _I, _I]
         L.ref_omp_threads.restype = _I
+        L.ref_rope_apply.restype = _I
+        L.ref_rope_apply.argtypes = [_VP, _I, _I]
+        L.ref_attn_dims.argtypes = [C.POINTER(_I)] * 3
+        L.ref_attention.restype = _I
+        L.ref_attention.argtypes = [_VP, _VP, _I, _I, _VP, _VP, _VP]
+        L.ref_embed.restype = _I
+        L.ref_embed.argtypes = [_I, _VP, _VP, _I, _VP]
         self.L = L
         self.vocab = L.ref_vocab()
 
@@ -224,3 +257,29 @@ class Reference:
         out = np.zeros(max(max_d, 1), dtype=np.int32)
         n = self.L.ref_ngram_draft(_i32p(h), h.size, _i32p(out), n_key, max_d)
         return out[:n]
+
+    def attn_dims(self) -> tuple[int, int, int]:
+        a, b, c = C.c_int(), C.c_int(), C.c_int()
+        self.L.ref_attn_dims(C.byref(a), C.byref(b), C.byref(c))
+        return a.value, b.value, c.value
+
+    def rope(self, q: np.ndarray, pos: int) -> np.ndarray:
+        q = np.array(q, dtype=np.float32, copy=True)
+        if self.L.ref_rope_apply(_f32p(q), q.size // 256, pos):
+            raise RuntimeError("ref_rope_apply")
+        return q
+
+    def attention(self, K, V, t0, pos, q, gate):
+        K = np.ascontiguousarray(K, np.float32)
+        V = np.ascontiguousarray(V, np.float32)
+        q = np.ascontiguousarray(q, np.float32)
+        gate = np.ascontiguousarray(gate, np.float32)
+        out = np.empty_like(q)
+        if self.L.ref_attention(_f32p(K), _f32p(V), t0, pos, _f32p(q), _f32p(gate), _f32p(out)):
+            raise RuntimeError("ref_attention")
+        return out
+
+    def embed(self, wtype, qs, sc, token):
+        out = np.empty(5120, dtype=np.float32)
+        self.L.ref_embed(wtype, qs.ctypes.data, None if sc is None else sc.ctypes.data, token, _f32p(out))
+        return out

@@ -8,6 +8,7 @@
  */
 #include "cwen_oracle.h"
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 static const float ORC_EPS = 1e-6f;              /* RMS_EPS, run.c:89 */
@@ -292,4 +293,75 @@ int orc_ngram_draft(const int *h, int hn, int *out, int n_key, int max_d) {
     }
   }
   return best;
+}
+
+/* run.c:1849-1887 (Q4_0RS and Q4_0 branches) */
+void orc_embed_q4(const uint8_t *qs, const uint16_t *sc, int type, int token, int H, float *dst) {
+  int nb = H / 32;
+  for (int i = 0; i < nb; i++) {
+    const uint8_t *q;
+    float d;
+    if (type == ORC_Q4_0) {
+      const uint8_t *b = qs + ((size_t)token * nb + i) * 18;
+      d = orc_f16_to_f32(ld16(b));
+      q = b + 2;
+    } else {
+      q = qs + ((size_t)token * nb + i) * 16;
+      d = orc_f16_to_f32(sc[(size_t)token * nb + i]);
+    }
+    for (int j = 0; j < 16; j++) {
+      dst[i * 32 + j] = (float)((q[j] & 0xF) - 8) * d;
+      dst[i * 32 + j + 16] = (float)((q[j] >> 4) - 8) * d;
+    }
+  }
+}
+
+/* run.c:1903-1948, mscale = 1 (no YaRN) */
+void orc_rope_apply(float *q, int n_heads, int hd, int pos, int npairs, int nrot, float theta) {
+  for (int h = 0; h < n_heads; h++) {
+    float *v = q + (size_t)h * hd;
+    for (int idx = 0; idx < npairs; idx++) {
+      float freq = 1.f / powf(theta, (float)idx / (float)nrot);
+      float ang = (float)pos * freq;
+      float c = cosf(ang) * 1.f, s = sinf(ang) * 1.f;
+      float a = v[idx * 2], b = v[idx * 2 + 1];
+      v[idx * 2] = a * c - b * s;
+      v[idx * 2 + 1] = a * s + b * c;
+    }
+  }
+}
+
+/* run.c:2362-2409, scalar branches (dot_f32 scalar: run.c:1275-1289) */
+void orc_attention(const float *K, const float *V, int nkv, int hd, int t0, int pos, const float *q,
+                   const float *gate, int nh, float *out) {
+  float scale = 1.f / sqrtf((float)hd);
+  int kv_mul = nh / nkv;
+  float *at = (float *)malloc(sizeof(float) * (size_t)(pos + 1));
+  memset(out, 0, sizeof(float) * (size_t)nh * hd);
+  for (int hkv = 0; hkv < nkv; hkv++) {
+    for (int m = 0; m < kv_mul; m++) {
+      int h = hkv * kv_mul + m;
+      const float *qh = q + (size_t)h * hd;
+      for (int t = t0; t <= pos; t++) {
+        const float *k = K + ((size_t)t * nkv + hkv) * hd;
+        float s = 0;
+        for (int i = 0; i < hd; i++) s += qh[i] * k[i];
+        at[t] = s * scale;
+      }
+      float mx = at[t0];
+      for (int t = t0 + 1; t <= pos; t++) if (at[t] > mx) mx = at[t];
+      float sum = 0;
+      for (int t = t0; t <= pos; t++) { at[t] = expf(at[t] - mx); sum += at[t]; }
+      float inv = 1.f / sum;
+      for (int t = t0; t <= pos; t++) at[t] *= inv;
+      float *o = out + (size_t)h * hd;
+      for (int t = t0; t <= pos; t++) {
+        const float *vv = V + ((size_t)t * nkv + hkv) * hd;
+        float a = at[t];
+        for (int i = 0; i < hd; i++) o[i] += a * vv[i];
+      }
+      for (int i = 0; i < hd; i++) o[i] *= orc_sigmoid(gate[(size_t)h * hd + i]);
+    }
+  }
+  free(at);
 }

@@ -83,6 +83,22 @@ int orc_walk(const float *logits, long ls, int V, const int *drafts, int E, int 
 /* Prompt-lookup drafter (run.c:4533-4549). */
 int orc_ngram_draft(const int *h, int hn, int *out, int n_key, int max_d);
 
+/* run.c:1849-1887 embed_token_to for Q4_0 (18-byte blocks, scales NULL) and
+ * Q4_0RS rows: dst[H] = ((n - 8) * d) of row `token`. */
+void orc_embed_q4(const uint8_t *qs, const uint16_t *sc, int type, int token, int H, float *dst);
+
+/* run.c:1903-1948 rope_tables + rope_apply without YaRN: on each of n_heads
+ * heads of hd floats, pairs (2i, 2i+1), i < npairs, rotate by
+ * pos / theta^(i/nrot). */
+void orc_rope_apply(float *q, int n_heads, int hd, int pos, int npairs, int nrot, float theta);
+
+/* run.c:2362-2409 attention_heads_kv, scalar branch: nh query heads of hd
+ * against nkv key/value heads (GQA group nh/nkv), keys and values
+ * [t][nkv][hd] for t in t0..pos, scale 1/sqrt(hd), softmax, output gated by
+ * sigmoid(gate).  out[nh*hd]. */
+void orc_attention(const float *K, const float *V, int nkv, int hd, int t0, int pos, const float *q,
+                   const float *gate, int nh, float *out);
+
 #ifdef __cplusplus
 }
 #endif

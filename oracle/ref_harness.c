@@ -108,3 +108,29 @@ int ref_omp_threads(void) {
   return 1;
 #endif
 }
+
+/* rope_apply (run.c:1920-1948) on n_heads heads of HD at position pos */
+int ref_rope_apply(float *q, int n_heads, int pos) {
+  if (pos < 0 || pos >= MAX_SEQ) return -1;
+  rope_apply(q, n_heads, pos);
+  return 0;
+}
+int ref_attn_dims(int *nh, int *nkv, int *hd) {
+  *nh = NH; *nkv = NKV; *hd = HD;
+  return 0;
+}
+/* attention_heads_kv (run.c:2362) over caller K/V [t][NKV][HD] */
+int ref_attention(const float *K, const float *Vv, int t0, int pos, const float *q, const float *gate,
+                  float *out) {
+  if (t0 < 0 || t0 > pos || pos >= MAX_SEQ) return -1;
+  attention_heads_kv(K, Vv, t0, pos, q, gate, out);
+  return 0;
+}
+/* embed_token_to (run.c:1849) with a caller token_embd of type Q4_0 / Q4_0RS */
+int ref_embed(int type, const void *qs, const void *sc, int token, float *dst) {
+  Tensor saved = tok_embd;
+  tok_embd = mk(type, qs, sc, H, V, 0);
+  embed_token_to(token, dst);
+  tok_embd = saved;
+  return 0;
+}

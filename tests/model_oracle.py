@@ -1,0 +1,81 @@
+"""Serial forward pass of the hybrid decoder composed from the oracle's C
+restatements (test infrastructure).  Mirrors forward_ex / layer_linear /
+layer_full / mlp of the reference (run.c:2594-2645, 2325-2358, 2412-2458,
+2205-2321) one position at a time."""
+import numpy as np
+
+T_F32, T_Q4_0RS, T_Q4_0RSI, T_Q6_K = 0, 101, 102, 14
+
+
+class OracleModel:
+    def __init__(self, O, cfg: dict, tensors):
+        self.O, self.c = O, cfg
+        self.g = {}
+        self.t = {}
+        for layer, tid, wtype, data, sc, ne0, ne1 in tensors:
+            self.t[(layer, tid)] = (wtype, data, sc, ne0, ne1)
+        c = cfg
+        self.C = (2 * c["gdn_nkh"] + c["gdn_nvh"]) * 128
+        self.reset()
+
+    def reset(self):
+        c = self.c
+        self.S = {}
+        self.hist = {}
+        self.K = {}
+        self.V = {}
+        for l in range(c["n_layers"]):
+            if l % c["full_interval"] == c["full_interval"] - 1:
+                self.K[l] = np.zeros((c["max_ctx"], c["n_kv_head"], c["head_dim"]), np.float32)
+                self.V[l] = np.zeros_like(self.K[l])
+            else:
+                self.S[l] = np.zeros((c["gdn_nvh"], 128, 128), np.float32)
+                self.hist[l] = np.zeros((self.C, 3), np.float32)
+
+    def mv(self, layer, tid, x, side=0):
+        wtype, data, sc, ne0, ne1 = self.t[(layer, tid)]
+        return self.O.gemvb(wtype, data, sc, ne0, ne1, x[None, :], side)[0]
+
+    def f32(self, layer, tid):
+        return self.t[(layer, tid)][1]
+
+    def step(self, tok: int, pos: int) -> np.ndarray:
+        from cwen_amd import gpu as G
+        O, c = self.O, self.c
+        wtype, qs, sc, H, _ = self.t[(-1, G.TOK_EMBD)]
+        x = O.embed(wtype, qs, sc, int(tok), H)
+        for l in range(c["n_layers"]):
+            xb = O.rmsnorm(x, self.f32(l, G.ATTN_NORM))
+            if l in self.S:
+                qkv = self.mv(l, G.ATTN_QKV, xb)
+                z = self.mv(l, G.ATTN_GATE, xb)
+                a = self.mv(l, G.SSM_ALPHA, xb)
+                b = self.mv(l, G.SSM_BETA, xb)
+                A, dt = self.f32(l, G.SSM_A), self.f32(l, G.SSM_DT)
+                xa = (a + dt).astype(np.float32)
+                sp = np.where(xa > 20, xa, np.log(np.float32(1) + np.exp(xa))).astype(np.float32)
+                decay = (A * sp).astype(np.float32)
+                beta = (np.float32(1) / (np.float32(1) + np.exp(-b))).astype(np.float32)
+                xc, self.hist[l] = O.conv1d_update(qkv, self.hist[l], self.f32(l, G.SSM_CONV).reshape(-1, 4))
+                self.S[l], _, o = O.gdn_step(self.S[l], xc, z, decay, beta, self.f32(l, G.SSM_NORM),
+                                             c["gdn_nkh"], c["gdn_nvh"], 128)
+                x = (x + self.mv(l, G.SSM_OUT, o)).astype(np.float32)
+            else:
+                NH, NKV, HD = c["n_head"], c["n_kv_head"], c["head_dim"]
+                qf = self.mv(l, G.ATTN_Q, xb).reshape(NH, 2, HD)
+                q, gate = qf[:, 0].copy(), qf[:, 1].copy()
+                k = self.mv(l, G.ATTN_KV, xb, 0).reshape(NKV, HD)
+                v = self.mv(l, G.ATTN_KV, xb, 1).reshape(NKV, HD)
+                qn, kn = self.f32(l, G.ATTN_Q_NORM), self.f32(l, G.ATTN_K_NORM)
+                q = np.stack([O.rmsnorm(q[h], qn) for h in range(NH)])
+                k = np.stack([O.rmsnorm(k[h], kn) for h in range(NKV)])
+                q = O.rope(q, pos, c["n_rot_pairs"], c["n_rot"], c["rope_theta"])
+                k = O.rope(k, pos, c["n_rot_pairs"], c["n_rot"], c["rope_theta"])
+                self.K[l][pos], self.V[l][pos] = k, v
+                att = O.attention(self.K[l][:pos + 1], self.V[l][:pos + 1], 0, pos, q, gate)
+                x = (x + self.mv(l, G.ATTN_OUTPUT, att.reshape(-1))).astype(np.float32)
+            xb = O.rmsnorm(x, self.f32(l, G.POST_NORM))
+            h = O.silu_mul(self.mv(l, G.FFN_GATE_UP, xb, 0), self.mv(l, G.FFN_GATE_UP, xb, 1))
+            x = (x + self.mv(l, G.FFN_DOWN, h)).astype(np.float32)
+        xb = O.rmsnorm(x, self.f32(-1, G.OUTPUT_NORM))
+        return self.mv(-1, G.OUTPUT, xb)

@@ -1,0 +1,125 @@
+"""The block-verify model on the device (cwen_model_* + the C host drivers)
+on a small config of the same hybrid architecture.
+
+Checked:
+  * forward parity: per-position logits of the device forward pass vs the
+    oracle's serial forward composed from its C restatements
+    (tests/model_oracle.py).  Tolerance (stated): rel_err <= 1e-2 on the
+    logits; every GEMV and state on the path is within 1e-3 of the oracle
+    (their own tests), and the f16 operand rounding compounds over the layers.
+  * block == serial, bit for bit: one block of B positions gives the same
+    logits as B single-position passes (the property spec == serial rests on).
+  * verify with crafted drafts walks and rolls back exactly: accepted drafts
+    and bonus tokens reproduce the serial token stream.
+  * the speculative decode loop (n-gram drafter, host C) emits exactly the
+    serial decode's tokens.
+"""
+import numpy as np
+import pytest
+
+from cwen_amd import synth
+from util import rel_err
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(n_layers=4, d_model=1024, d_ffn=2048, vocab=4096, n_head=4, n_kv_head=2, head_dim=256,
+           n_rot_pairs=32, n_rot=64, gdn_nkh=2, gdn_nvh=4, gdn_dk=128, full_interval=4, max_ctx=512,
+           rope_theta=1e7, rms_eps=1e-6)
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from cwen_amd import gpu
+    ctx = gpu.Context(0)
+    tensors = list(synth.model_tensors(CFG, seed=0))
+    m = gpu.Model(ctx, **CFG)
+    for t in tensors:
+        m.set(*t)
+    yield gpu, ctx, m, tensors
+    m.free()
+    torch.cuda.synchronize()
+
+
+def test_forward_parity_vs_oracle(env, oracle):
+    from model_oracle import OracleModel
+    gpu, ctx, m, tensors = env
+    OM = OracleModel(oracle, CFG, tensors)
+    toks = synth.prompt_tokens(1, 12, CFG["vocab"])
+    m.reset()
+    ref = np.stack([OM.step(t, p) for p, t in enumerate(toks)])
+    got = []
+    for b0, B in ((0, 5), (5, 7)):          # two blocks of different size
+        am = m.forward(toks[b0:b0 + B])
+        lg = m.logits(B)
+        got.append(lg)
+        for b in range(B):
+            assert am[b] == oracle.argmax(lg[b])   # the head's argmax is exact on its own logits
+    got = np.concatenate(got)
+    for p in range(len(toks)):
+        assert rel_err(got[p], ref[p]) <= 1e-2, (p, rel_err(got[p], ref[p]))
+    assert m.pos == len(toks) - 1
+
+
+def test_block_equals_serial_bitwise(env):
+    gpu, ctx, m, _ = env
+    toks = synth.prompt_tokens(2, 20, CFG["vocab"])
+    m.reset()
+    m.forward(toks[:12], want_argmax=False)
+    m.forward(toks[12:20])
+    block = m.logits(8).copy()
+    m.reset()
+    m.forward(toks[:12], want_argmax=False)
+    for b in range(8):
+        m.forward(toks[12 + b:13 + b])
+        assert np.array_equal(m.logits(1)[0], block[b]), b
+
+
+def test_verify_walk_and_rollback(env):
+    """Drafts built from the serial stream with planted mistakes: every
+    accepted draft and bonus must equal the serial stream."""
+    gpu, ctx, m, _ = env
+    V = CFG["vocab"]
+    prompt = synth.prompt_tokens(3, 40, V)
+    n_gen = 60
+    serial = m.generate_serial(prompt, n_gen)
+    assert len(serial) == n_gen
+    g = np.random.default_rng(4)
+    import ctypes as C
+    nxt = C.c_int()
+    gpu.check("cwen_prefill", gpu.host_lib().cwen_prefill(m.h, np.ascontiguousarray(prompt, np.int32).ctypes.data,
+                                                          len(prompt), C.byref(nxt)))
+    out = [nxt.value]
+    seen_partial = seen_full = False
+    while len(out) < n_gen:
+        E = int(g.integers(0, 8))
+        fut = serial[len(out):len(out) + E].astype(np.int32)
+        E = len(fut)
+        drafts = fut.copy()
+        if E and g.random() < 0.5:
+            j = int(g.integers(0, E))
+            drafts[j] = (drafts[j] + 1) % V       # plant a mistake at j
+        k, bonus = m.verify(np.concatenate([[out[-1]], drafts]).astype(np.int32))
+        want_k = next((i for i in range(E) if drafts[i] != fut[i]), E)
+        assert k == want_k, (len(out), E, k, want_k)
+        seen_partial |= k < E
+        seen_full |= E > 0 and k == E
+        out.extend(drafts[:k].tolist())
+        out.append(bonus)
+    assert seen_partial and seen_full
+    assert np.array_equal(np.array(out[:n_gen]), serial)
+
+
+@pytest.mark.parametrize("n_key", [2, 4, 16])
+def test_spec_decode_equals_serial(env, n_key):
+    gpu, ctx, m, _ = env
+    prompt = synth.prompt_tokens(5, 64, CFG["vocab"], period=13, noise=0.05)
+    n_gen = 80
+    serial = m.generate_serial(prompt, n_gen)
+    spec, st = m.generate_spec(prompt, n_gen, n_key=n_key)
+    assert np.array_equal(spec, serial)
+    assert st.cycles <= n_gen
+    if n_key <= 4:
+        assert st.drafted > 0

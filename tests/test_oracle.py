@@ -312,3 +312,68 @@ def test_ngram_draft_vs_reference(oracle, ref):
         for n_key in (2, 4, 16):
             for max_d in (1, 7, 15):
                 assert np.array_equal(oracle.ngram_draft(hist, n_key, max_d), ref.ngram_draft(hist, n_key, max_d))
+
+
+# ---------------------------------------------------------------- model glue
+def test_embed_vs_reference_and_closed_form(oracle, ref_avx2):
+    from cwen_amd import synth
+    V = ref_avx2.vocab
+    H = 5120
+    qs, sc = synth.q4_rs(0, 64, H, key=9)          # 64 token rows are enough to index
+    # the reference indexes a [V][H] table; give it a full-size view of zeros past row 63
+    qfull = np.zeros((V, H // 32, 16), np.uint8)
+    sfull = np.zeros((V, H // 32), np.uint16)
+    qfull[:64] = qs.reshape(64, H // 32, 16)
+    sfull[:64] = sc.reshape(64, H // 32)
+    for tok in (0, 7, 63):
+        a = oracle.embed(101, qfull, sfull, tok, H)
+        b = ref_avx2.embed(101, qfull, sfull, tok)
+        assert np.array_equal(a, b)
+        # closed form: (n - 8) * d, low nibbles first
+        q = qfull[tok].astype(np.int32)
+        d = sfull[tok].view(np.float16).astype(np.float32)
+        want = np.concatenate([(q & 15) - 8, (q >> 4) - 8], axis=1).astype(np.float32) * d[:, None]
+        assert np.array_equal(a, want.reshape(-1))
+    g = synth.q4_gguf(0, 64, H, key=3)
+    gfull = np.zeros((V, H // 32 * 18), np.uint8)
+    gfull[:64] = g.reshape(64, -1)
+    assert np.array_equal(oracle.embed(2, gfull, None, 5, H), ref_avx2.embed(2, gfull, None, 5))
+
+
+@pytest.mark.parametrize("pos", [0, 1, 17, 4095, 8191])
+def test_rope_vs_reference(oracle, ref, pos):
+    g = np.random.default_rng(pos)
+    q = g.standard_normal((24, 256)).astype(np.float32)
+    a = oracle.rope(q, pos)
+    b = ref.rope(q, pos)
+    assert np.array_equal(a, b)
+    assert np.array_equal(a[:, 64:], q[:, 64:])          # only the first 32 pairs rotate
+    # rotation preserves each pair's norm
+    n0 = q[:, :64].reshape(24, 32, 2)
+    n1 = a[:, :64].reshape(24, 32, 2)
+    assert np.allclose((n0 ** 2).sum(-1), (n1 ** 2).sum(-1), rtol=1e-5)
+
+
+def test_attention_vs_reference_and_f64(oracle, ref):
+    nh, nkv, hd = ref.attn_dims()
+    g = np.random.default_rng(21)
+    T = 37
+    K = g.standard_normal((T, nkv, hd)).astype(np.float32)
+    V = g.standard_normal((T, nkv, hd)).astype(np.float32)
+    q = g.standard_normal((nh, hd)).astype(np.float32)
+    gate = g.standard_normal((nh, hd)).astype(np.float32)
+    for t0, pos in ((0, 0), (0, 36), (5, 20)):
+        a = oracle.attention(K, V, t0, pos, q, gate)
+        b = ref.attention(K, V, t0, pos, q, gate)
+        assert rel_err(a, b) < 1e-5
+        # f64 softmax attention
+        kvm = nh // nkv
+        want = np.zeros((nh, hd))
+        for h in range(nh):
+            k = K[t0:pos + 1, h // kvm].astype(np.float64)
+            v = V[t0:pos + 1, h // kvm].astype(np.float64)
+            s = k @ q[h].astype(np.float64) / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            want[h] = (p @ v) / (1 + np.exp(-gate[h].astype(np.float64)))
+        assert rel_err(a, want) < 1e-5
