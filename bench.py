@@ -244,6 +244,49 @@ def extra_leg(steps: int, warmup: int) -> dict:
     return {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in out.items()}
 
 
+C4_CFG = dict(n_layers=64, d_model=5120, d_ffn=17408, vocab=151936, n_head=24, n_kv_head=4, head_dim=256,
+              n_rot_pairs=32, n_rot=64, gdn_nkh=16, gdn_nvh=48, gdn_dk=128, full_interval=4, max_ctx=8192,
+              rope_theta=1e7, rms_eps=1e-6)
+
+
+def c4_step_bytes(ctxlen: float) -> float:
+    """Algorithmic HBM bytes of one verify pass of the 64-layer model at
+    context length ctxlen: Q4_0 trunk + Q6_K head + F32 tensors + GDN state
+    read/write + conv history + KV read/write + embedding rows."""
+    return (13_697_187_840 + 638_131_200 + 10_582_016 + 301_989_888 + 11_796_480
+            + 131_072 * ctxlen + 1_048_576 + 23_040)
+
+
+def c4_leg(n_prompt: int, cycles: int) -> dict:
+    """Full synthetic 27B-shape decoder (device-generated random-init
+    weights): prefill a periodic prompt, run `cycles` speculative cycles at
+    B = 8 (7 n-gram drafts), then the serial decode of as many tokens; the two
+    token streams must be identical."""
+    from cwen_amd import gpu, synth
+    ctx = gpu.Context(0)
+    m = gpu.Model(ctx, **C4_CFG)
+    m.synth(0)
+    prompt = synth.prompt_tokens(0, n_prompt, C4_CFG["vocab"], period=61, noise=0.02)
+    spec, st = m.generate_spec(prompt, cycles * 8 + 8, max_draft=7, max_cycles=cycles)
+    serial, st2 = m.generate_serial(prompt, len(spec), with_stats=True)
+    m.free()
+    mean_ctx = n_prompt + len(spec) / 2
+    gbs = c4_step_bytes(mean_ctx) * st.cycles / st.decode_s / 1e9
+    return {"prompt_tokens": n_prompt, "cycles": int(st.cycles), "tokens": int(len(spec)),
+            "verified_tok_s": round(len(spec) / st.decode_s, 1),
+            "serial_tok_s": round(len(serial) / st2.decode_s, 1),
+            "speedup": round((len(spec) / st.decode_s) / (len(serial) / st2.decode_s), 3),
+            "mean_accepted_drafts": round(st.kept / max(st.drafted, 1), 3),
+            "drafted_cycles": int(st.drafted), "full_accepts": int(st.full),
+            "ms_per_cycle": round(st.decode_s / st.cycles * 1e3, 3),
+            "ms_per_serial_step": round(st2.decode_s / max(st2.cycles, 1) * 1e3, 3),
+            "GB_s_per_cycle": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
+            "prefill_s": round(st.prefill_s, 3),
+            "spec_equals_serial": bool(np.array_equal(spec, serial)),
+            "note": "random-init weights; greedy output of such a model is highly repetitive, "
+                    "so n-gram drafts are accepted far more often than on a trained model"}
+
+
 def cpu_child(B: int, reps: int) -> None:
     """CPU baseline leg: the reference engine's own mlp_blk kernels (gemvb x3 +
     silu_mul, run.c:2677-2681), compiled from its run.c (oracle/_ref); the
@@ -315,6 +358,9 @@ def main() -> int:
     ap.add_argument("--Bs", default="8,1,16",
                     help="comma-separated block sizes; the first is the headline (must include 8)")
     ap.add_argument("--no-extra", action="store_true", help="skip the c0/c2/c3 kernel measurements")
+    ap.add_argument("--no-c4", action="store_true", help="skip the full-model speculative decode")
+    ap.add_argument("--c4-prompt", type=int, default=4096)
+    ap.add_argument("--c4-cycles", type=int, default=256)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a 256 MiB device copy (for FETCH_SIZE/WRITE_SIZE calibration)")
     ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
@@ -334,6 +380,7 @@ def main() -> int:
         calibrate_copy()
     res = gpu_leg(args.steps, args.warmup, Bs)
     extra = None if args.no_extra else extra_leg(args.steps, args.warmup)
+    c4 = None if args.no_c4 else c4_leg(args.c4_prompt, args.c4_cycles)
     traffic = load_traffic()
     h = res[8]
     b1, _ = ffn_bytes(8)
@@ -375,6 +422,7 @@ def main() -> int:
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_leg(8),
         "other_configs": extra,
+        "c4_full_model_spec_b8": c4,
     }
     print(json.dumps(line))
     return 0

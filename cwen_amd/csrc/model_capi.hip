@@ -174,6 +174,100 @@ int set_tokens(cwen_model *m, const int *toks, int B, hipStream_t st) {
   return CWEN_OK;
 }
 
+// ---- seeded synthetic tensors generated on the device (benchmarks: the
+// random-init weights of the architecture without a host round trip).
+// Counter-based: value i of stream `key` is a function of (seed, key, i) only.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t hsh(uint64_t seed, uint64_t key, uint64_t i) {
+  return mix64(seed * 0x9e3779b97f4a7c15ull ^ mix64(key * 0xd1b54a32d192ed03ull + i));
+}
+__device__ __forceinline__ float unif(uint64_t h) { return ((h >> 40) + 0.5f) * (1.f / 16777216.f); }  // (0,1)
+__device__ __forceinline__ float gauss(uint64_t seed, uint64_t key, uint64_t i) {
+  const uint64_t h = hsh(seed, key, i);
+  const float u1 = ((h >> 40) + 0.5f) * (1.f / 16777216.f), u2 = ((h & 0xFFFFFF) + 0.5f) * (1.f / 16777216.f);
+  return sqrtf(-2.f * logf(u1)) * cosf(6.2831853f * u2);
+}
+// bytes uniform 0..255
+__global__ void synth_bytes_kernel(uint8_t *p, size_t n, uint64_t seed, uint64_t key) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = (uint8_t)(hsh(seed, key, i) >> 56);
+}
+// f16 scales |N(0, sigma)|, written at p[i * stride] (bytes) for i < n
+__global__ void synth_scale_kernel(uint8_t *p, size_t n, size_t stride, float sigma, uint64_t seed, uint64_t key) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const _Float16 h = (_Float16)fabsf(gauss(seed, key, i) * sigma);
+    *(uint16_t *)(p + i * stride) = __builtin_bit_cast(uint16_t, h);
+  }
+}
+// f32 values: kind 0: mu + sigma N, kind 1: -exp(U(-1, 1))
+__global__ void synth_f32_kernel(float *p, size_t n, int kind, float mu, float sigma, uint64_t seed, uint64_t key) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = kind == 0 ? mu + sigma * gauss(seed, key, i) : -expf(2.f * unif(hsh(seed, key, i)) - 1.f);
+}
+
+int synth_launch_grid(size_t n) { return (int)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536); }
+
+// A quantized weight of `type` [ne1][ne0] generated in its reference layout on
+// the device, then repacked like an upload.
+int synth_weight(cwen_ctx *ctx, int type, int ne0, int ne1, uint64_t seed, uint64_t key, cwen_weight **out) {
+  const size_t nblk = (size_t)(ne0 / 32) * ne1;
+  size_t qbytes, sbytes = 0;
+  int nside = 1;
+  switch (type) {
+    case CWEN_T_Q4_0RS: qbytes = nblk * 16; sbytes = nblk * 2; break;
+    case CWEN_T_Q4_0RSI: qbytes = nblk * 32; sbytes = nblk * 4; nside = 2; break;
+    case CWEN_T_Q6_K: qbytes = (size_t)(ne0 / 256) * ne1 * 210; break;
+    default: return CWEN_ETYPE;
+  }
+  cwen_weight *w = (cwen_weight *)calloc(1, sizeof(cwen_weight));
+  if (!w) return CWEN_ENOMEM;
+  w->ctx = ctx; w->type = type; w->fmt = gemv_fmt_of(type);
+  w->ne0 = ne0; w->ne1 = ne1; w->nside = nside;
+  w->nrg = (ne1 + Q4_ROWS - 1) / Q4_ROWS;
+  w->nst = ne0 / Q4_ST_K;
+  w->bytes = (size_t)w->nrg * w->nst * nside * gemv_st_bytes(w->fmt);
+  w->src_bytes = qbytes + sbytes;
+  gemv_choose_split(ctx, w);
+  uint8_t *dq = nullptr, *ds = nullptr;
+  int rc = CWEN_ENOMEM;
+  if (w->bytes >= ((size_t)1 << 32) || ne0 % Q4_K_ALIGN) { rc = CWEN_EINVAL; goto fail; }
+  if (dmalloc(&w->dev, w->bytes) || dmalloc(&dq, qbytes) || (sbytes && dmalloc(&ds, sbytes))) goto fail;
+  hipLaunchKernelGGL(synth_bytes_kernel, dim3(synth_launch_grid(qbytes)), dim3(256), 0, nullptr, dq, qbytes, seed,
+                     key * 4);
+  if (type == CWEN_T_Q6_K)  // d = f16(|N(0, 0.002)|) at byte 208 of each 210-byte super-block
+    hipLaunchKernelGGL(synth_scale_kernel, dim3(synth_launch_grid(qbytes / 210)), dim3(256), 0, nullptr, dq + 208,
+                       qbytes / 210, (size_t)210, 0.002f, seed, key * 4 + 1);
+  else  // f16(|N(0, 0.02)| / 8)
+    hipLaunchKernelGGL(synth_scale_kernel, dim3(synth_launch_grid(sbytes / 2)), dim3(256), 0, nullptr, ds,
+                       sbytes / 2, (size_t)2, 0.02f / 8.f, seed, key * 4 + 1);
+  if ((rc = gemv_repack(w, dq, (const uint16_t *)ds, nullptr))) goto fail;
+  if (hipDeviceSynchronize() != hipSuccess) { rc = CWEN_EHIP; goto fail; }
+  (void)hipFree(dq);
+  if (ds) (void)hipFree(ds);
+  *out = w;
+  return CWEN_OK;
+fail:
+  if (dq) (void)hipFree(dq);
+  if (ds) (void)hipFree(ds);
+  if (w->dev) (void)hipFree(w->dev);
+  free(w);
+  return rc;
+}
+
+int synth_f32(float **out, size_t n, int kind, float mu, float sigma, uint64_t seed, uint64_t key) {
+  if (*out) (void)hipFree(*out);
+  *out = nullptr;
+  if (dmalloc(out, n)) return CWEN_ENOMEM;
+  hipLaunchKernelGGL(synth_f32_kernel, dim3(synth_launch_grid(n)), dim3(256), 0, nullptr, *out, n, kind, mu, sigma,
+                     seed, key * 4 + 2);
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -314,6 +408,63 @@ int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data,
     case CWEN_ATTN_K_NORM: return (f32 && ne0 == c.head_dim) ? upload_f32(data, ne0, &y.k_norm) : CWEN_EINVAL;
     default: return CWEN_EINVAL;
   }
+}
+
+int cwen_model_synth(cwen_model *m, unsigned long long seed) {
+  if (!m) return CWEN_EINVAL;
+  const cwen_model_cfg &c = m->cfg;
+  const int H = c.d_model, I = c.d_ffn;
+  const int C = (2 * c.gdn_nkh + c.gdn_nvh) * 128, Zh = c.gdn_nvh * 128;
+  const int Qo = c.n_head * c.head_dim, Ko = c.n_kv_head * c.head_dim;
+  cwen_ctx *ctx = m->ctx;
+  CWEN_HIP_TRY(hipSetDevice(ctx->device));
+  int rc;
+  auto W = [&](cwen_weight **w, int type, int ne0, int ne1, uint64_t key) {
+    if (*w) cwen_weight_free(*w);
+    *w = nullptr;
+    return synth_weight(ctx, type, ne0, ne1, seed, key, w);
+  };
+  {  // embedding Q4_0RS rows
+    const size_t nblk = (size_t)(H / 32) * c.vocab;
+    if (m->emb_qs) (void)hipFree(m->emb_qs);
+    if (m->emb_sc) (void)hipFree(m->emb_sc);
+    m->emb_qs = nullptr; m->emb_sc = nullptr;
+    if (dmalloc(&m->emb_qs, nblk * 16) || dmalloc(&m->emb_sc, nblk)) return CWEN_ENOMEM;
+    hipLaunchKernelGGL(synth_bytes_kernel, dim3(synth_launch_grid(nblk * 16)), dim3(256), 0, nullptr, m->emb_qs,
+                       nblk * 16, (uint64_t)seed, (uint64_t)1);
+    hipLaunchKernelGGL(synth_scale_kernel, dim3(synth_launch_grid(nblk)), dim3(256), 0, nullptr,
+                       (uint8_t *)m->emb_sc, nblk, (size_t)2, 0.02f / 8.f, (uint64_t)seed, (uint64_t)2);
+    m->emb_type = CWEN_T_Q4_0RS;
+  }
+  if ((rc = synth_f32(&m->out_norm, H, 0, 1.f, 0.1f, seed, 3)) || (rc = W(&m->head, CWEN_T_Q6_K, H, c.vocab, 4)))
+    return rc;
+  for (int l = 0; l < c.n_layers; ++l) {
+    Layer &y = m->L[l];
+    const uint64_t k0 = 100 * (uint64_t)(l + 1);
+    if ((rc = synth_f32(&y.attn_norm, H, 0, 1.f, 0.1f, seed, k0 + 1)) ||
+        (rc = synth_f32(&y.post_norm, H, 0, 1.f, 0.1f, seed, k0 + 2)) ||
+        (rc = W(&y.ffn_gu, CWEN_T_Q4_0RSI, H, I, k0 + 3)) || (rc = W(&y.ffn_down, CWEN_T_Q4_0RS, I, H, k0 + 4)))
+      return rc;
+    if (y.linear) {
+      if ((rc = W(&y.qkv, CWEN_T_Q4_0RS, H, C, k0 + 5)) || (rc = W(&y.gate_z, CWEN_T_Q4_0RS, H, Zh, k0 + 6)) ||
+          (rc = W(&y.alpha, CWEN_T_Q4_0RS, H, c.gdn_nvh, k0 + 7)) ||
+          (rc = W(&y.beta, CWEN_T_Q4_0RS, H, c.gdn_nvh, k0 + 8)) ||
+          (rc = W(&y.ssm_out, CWEN_T_Q4_0RS, Zh, H, k0 + 9)) ||
+          (rc = synth_f32(&y.ssm_a, c.gdn_nvh, 1, 0.f, 0.f, seed, k0 + 10)) ||
+          (rc = synth_f32(&y.ssm_dt, c.gdn_nvh, 0, 0.f, 0.5f, seed, k0 + 11)) ||
+          (rc = synth_f32(&y.ssm_conv, (size_t)4 * C, 0, 0.f, 0.3f, seed, k0 + 12)) ||
+          (rc = synth_f32(&y.ssm_norm, 128, 0, 1.f, 0.1f, seed, k0 + 13)))
+        return rc;
+    } else {
+      if ((rc = W(&y.wq, CWEN_T_Q4_0RS, H, 2 * Qo, k0 + 14)) || (rc = W(&y.wkv, CWEN_T_Q4_0RSI, H, Ko, k0 + 15)) ||
+          (rc = W(&y.wo, CWEN_T_Q4_0RS, Qo, H, k0 + 16)) ||
+          (rc = synth_f32(&y.q_norm, c.head_dim, 0, 1.f, 0.1f, seed, k0 + 17)) ||
+          (rc = synth_f32(&y.k_norm, c.head_dim, 0, 1.f, 0.1f, seed, k0 + 18)))
+        return rc;
+    }
+  }
+  CWEN_HIP_TRY(hipDeviceSynchronize());
+  return CWEN_OK;
 }
 
 int cwen_model_reset(cwen_model *m) {

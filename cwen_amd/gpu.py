@@ -49,6 +49,7 @@ SIGNATURES = [
     ("cwen_model_free", _I, [_VP]),
     ("cwen_model_set", _I, [_VP, _I, _I, _I, _VP, _VP, _I, _I]),
     ("cwen_model_reset", _I, [_VP]),
+    ("cwen_model_synth", _I, [_VP, C.c_ulonglong]),
     ("cwen_model_pos", _I, [_VP]),
     ("cwen_model_capacity", _I, [_VP]),
     ("cwen_model_forward", _I, [_VP, _VP, _I, _I, _VP, _VP]),
@@ -61,7 +62,7 @@ HOST_SIGNATURES = [
     ("cwen_spec_default", None, [_VP]),
     ("cwen_ngram_draft", _I, [_VP, _I, _VP, _I, _I]),
     ("cwen_prefill", _I, [_VP, _VP, _I, C.POINTER(_I)]),
-    ("cwen_generate_serial", _I, [_VP, _VP, _I, _I, _VP]),
+    ("cwen_generate_serial", _I, [_VP, _VP, _I, _I, _VP, _VP]),
     ("cwen_generate_spec", _I, [_VP, _VP, _I, _I, _VP, _VP, _VP]),
 ]
 
@@ -304,12 +305,14 @@ class ModelCfg(C.Structure):
 
 
 class SpecCfg(C.Structure):
-    _fields_ = [("n_key", C.c_int), ("max_draft", C.c_int), ("min_draft", C.c_int), ("cooldown", C.c_int)]
+    _fields_ = [("n_key", C.c_int), ("max_draft", C.c_int), ("min_draft", C.c_int), ("cooldown", C.c_int),
+                ("max_cycles", C.c_int)]
 
 
 class SpecStats(C.Structure):
     _fields_ = [("cycles", C.c_longlong), ("drafted", C.c_longlong), ("full", C.c_longlong),
-                ("rejected", C.c_longlong), ("kept", C.c_longlong), ("prefill_tokens", C.c_int)]
+                ("rejected", C.c_longlong), ("kept", C.c_longlong), ("prefill_tokens", C.c_int),
+                ("prefill_s", C.c_double), ("decode_s", C.c_double)]
 
 
 class Model:
@@ -330,6 +333,10 @@ class Model:
 
     def reset(self) -> None:
         check("cwen_model_reset", lib().cwen_model_reset(self.h))
+
+    def synth(self, seed: int = 0) -> None:
+        """Device-generated random-init weights (cwen_model_synth)."""
+        check("cwen_model_synth", lib().cwen_model_synth(self.h, seed))
 
     @property
     def pos(self) -> int:
@@ -354,19 +361,20 @@ class Model:
         check("cwen_model_logits", lib().cwen_model_logits(self.h, out.ctypes.data, rows))
         return out
 
-    def generate_serial(self, prompt, n_gen: int) -> np.ndarray:
+    def generate_serial(self, prompt, n_gen: int, with_stats: bool = False):
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.zeros(n_gen, dtype=np.int32)
-        n = host_lib().cwen_generate_serial(self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data)
+        st = SpecStats()
+        n = host_lib().cwen_generate_serial(self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data, C.byref(st))
         if n < 0:
             raise CwenError("cwen_generate_serial", n)
-        return out[:n]
+        return (out[:n], st) if with_stats else out[:n]
 
     def generate_spec(self, prompt, n_gen: int, n_key: int = 16, max_draft: int = 8, min_draft: int = 2,
-                      cooldown: int = 8) -> tuple[np.ndarray, SpecStats]:
+                      cooldown: int = 8, max_cycles: int = 0) -> tuple[np.ndarray, SpecStats]:
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.zeros(n_gen, dtype=np.int32)
-        cfg = SpecCfg(n_key, max_draft, min_draft, cooldown)
+        cfg = SpecCfg(n_key, max_draft, min_draft, cooldown, max_cycles)
         st = SpecStats()
         n = host_lib().cwen_generate_spec(self.h, p.ctypes.data, p.size, n_gen, C.byref(cfg), out.ctypes.data,
                                           C.byref(st))

@@ -1,16 +1,25 @@
 /* Host decode drivers over the cwen_gpu C ABI (see cwen_host.h). */
-#include "cwen_host.h"
-
+#define _POSIX_C_SOURCE 199309L
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
+
+#include "cwen_host.h"
 
 #define PREFILL_BLOCK 16
+
+static double now_s(void) {
+  struct timespec t;
+  clock_gettime(CLOCK_MONOTONIC, &t);
+  return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
 
 void cwen_spec_default(cwen_spec_cfg *cfg) {
   cfg->n_key = 16;
   cfg->max_draft = 8;
   cfg->min_draft = 2;
   cfg->cooldown = 8;
+  cfg->max_cycles = 0;
 }
 
 /* run.c:4533-4549 */
@@ -48,11 +57,18 @@ int cwen_prefill(cwen_model *m, const int *prompt, int n_prompt, int *next) {
 }
 
 /* run.c:5027-5045: one position per pass, stopping when the context fills. */
-int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_gen, int *out) {
+int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_gen, int *out,
+                         cwen_spec_stats *stats) {
   if (!m || !out || n_gen < 0) return CWEN_EINVAL;
   const int cap = cwen_model_capacity(m);
+  cwen_spec_stats st;
+  memset(&st, 0, sizeof st);
+  st.prefill_tokens = n_prompt;
   int next, rc;
+  double t0 = now_s();
   if ((rc = cwen_prefill(m, prompt, n_prompt, &next))) return rc;
+  double t1 = now_s();
+  st.prefill_s = t1 - t0;
   int n = 0;
   for (int g = 0; g < n_gen; g++) {
     if (cwen_model_pos(m) + 1 >= cap) break;
@@ -60,8 +76,11 @@ int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_g
     if (g + 1 == n_gen) break;
     int k, bonus;
     if ((rc = cwen_model_verify(m, &next, 1, &k, &bonus, NULL))) return rc;
+    st.cycles++;
     next = bonus;
   }
+  st.decode_s = now_s() - t1;
+  if (stats) *stats = st;
   return n;
 }
 
@@ -71,11 +90,16 @@ int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen
   cwen_spec_cfg cfg;
   if (cfg_in) cfg = *cfg_in; else cwen_spec_default(&cfg);
   if (cfg.max_draft > CWEN_BMAX - 1) cfg.max_draft = CWEN_BMAX - 1;
-  cwen_spec_stats st = {0, 0, 0, 0, 0, n_prompt};
+  cwen_spec_stats st;
+  memset(&st, 0, sizeof st);
+  st.prefill_tokens = n_prompt;
   int *hist = (int *)malloc(sizeof(int) * (size_t)(n_prompt + n_gen + CWEN_BMAX));
   if (!hist) return CWEN_ENOMEM;
   int pend, rc;
+  double t0 = now_s();
   if ((rc = cwen_prefill(m, prompt, n_prompt, &pend))) { free(hist); return rc; }
+  double t1 = now_s();
+  st.prefill_s = t1 - t0;
   memcpy(hist, prompt, sizeof(int) * (size_t)n_prompt);
   const int cap = cwen_model_capacity(m);
   int hn = n_prompt, g = 0, streak = 0, cool = 0, fa_streak = 0;
@@ -87,6 +111,7 @@ int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen
   int E_cap = cap_hard;
   int blk[CWEN_BMAX];
   while (g > 0 && g < n_gen) {
+    if (cfg.max_cycles > 0 && st.cycles >= cfg.max_cycles) break;
     const int pos = cwen_model_pos(m);
     if (pos + 1 >= cap) break;                     /* same context cap as the serial loop */
     int E = 0;
@@ -122,6 +147,7 @@ int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen
     if (k == E) streak = 0;
     else if (++streak >= 3) { streak = 0; cool = cfg.cooldown; }
   }
+  st.decode_s = now_s() - t1;
   free(hist);
   if (stats) *stats = st;
   return g;

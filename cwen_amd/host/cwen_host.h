@@ -21,11 +21,13 @@ typedef struct {
   int max_draft;   /* drafts per block, <= CWEN_BMAX - 1 (8)   */
   int min_draft;   /* a proposal shorter than this is dropped (2) */
   int cooldown;    /* plain steps after 3 short walks (8)      */
+  int max_cycles;  /* stop after this many verify cycles (0: no limit) */
 } cwen_spec_cfg;
 
 typedef struct {
-  long long cycles, drafted, full, rejected, kept;  /* run.c:4891 counters */
+  long long cycles, drafted, full, rejected, kept;  /* run.c:4891 counters; cycles = passes */
   int prefill_tokens;
+  double prefill_s, decode_s;                       /* wall time of the two phases */
 } cwen_spec_stats;
 
 /* Default knobs of the reference. */
@@ -44,7 +46,8 @@ int cwen_prefill(cwen_model *m, const int *prompt, int n_prompt, int *next);
 /* generate_tokens (run.c:5027-5045): prefill, then n_gen greedy tokens, one
  * position per forward pass.  Returns the number of tokens written to out
  * (fewer than n_gen only when the context fills), or a negative status. */
-int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_gen, int *out);
+int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_gen, int *out,
+                         cwen_spec_stats *stats);
 
 /* generate_tokens_spec (run.c:4882-5025) with the n-gram drafter: the same
  * token stream as cwen_generate_serial, produced by block-verify cycles. */

@@ -217,6 +217,13 @@ int cwen_model_free(cwen_model *m);
  * quantized types go through cwen_weight_upload's repack. */
 int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data, const void *scales,
                    int ne0, int ne1);
+/* Fill every tensor with seeded random-init values generated on the device
+ * (no host data): Q4_0 matrices CWENR RS / RSI with nibbles uniform and f16
+ * scales |N(0,0.02)|/8, a Q6_K head (bytes uniform, d = |N(0,0.002)|), a
+ * Q4_0RS embedding, F32 norms 1 + 0.1 N(0,1), conv taps 0.3 N(0,1), gate
+ * parameters A = -exp(U(-1,1)), dt = 0.5 N(0,1).  For benchmarks of the
+ * architecture; no reference counterpart (the reference maps a model file). */
+int cwen_model_synth(cwen_model *m, unsigned long long seed);
 /* Empty context: position -1, GDN states and conv histories zero (reset_state). */
 int cwen_model_reset(cwen_model *m);
 /* Last filled position (the reference's pos_n). */
