@@ -14,7 +14,7 @@
 namespace {
 
 constexpr int HD = 128 * 2;          // full-attention head dim
-constexpr int TC = 64;               // keys per attention chunk
+constexpr int TC = 32;               // keys per attention chunk
 
 template <int CTRL> __device__ __forceinline__ float dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
@@ -83,19 +83,38 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uin
 }
 
 // ---- RMSNorm of B rows: y = w * x * (1/sqrt(mean(x^2) + eps)), f32 and/or
-// f16 out.  Grid: B, 256 threads.
+// f16 out.  Grid: B, 256 threads; a thread owns float4 groups tid, tid+256,
+// ... (n <= 8192, n % 4 == 0), all loaded before the first use.
+constexpr int RMS_MAXV = 8;
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *X, int xs, const float *w, int n, float eps,
                                                       float *Y, int ys, _Float16 *Yh, int yhs) {
   __shared__ float red[4];
   const int b = blockIdx.x;
   const float *x = X + (size_t)b * xs;
+  float4 v[RMS_MAXV];
+#pragma unroll
+  for (int j = 0; j < RMS_MAXV; ++j) {
+    const int i = (j * 256 + threadIdx.x) * 4;
+    v[j] = i < n ? *(const float4 *)(x + i) : (float4){0.f, 0.f, 0.f, 0.f};
+  }
   float ss = 0.f;
-  for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(x[i], x[i], ss);
+#pragma unroll
+  for (int j = 0; j < RMS_MAXV; ++j) {
+    ss = fmaf(v[j].x, v[j].x, ss); ss = fmaf(v[j].y, v[j].y, ss);
+    ss = fmaf(v[j].z, v[j].z, ss); ss = fmaf(v[j].w, v[j].w, ss);
+  }
   const float s = 1.f / sqrtf(sum256(ss, red) / (float)n + eps);
-  for (int i = threadIdx.x; i < n; i += 256) {
-    const float v = w[i] * x[i] * s;
-    if (Y) Y[(size_t)b * ys + i] = v;
-    if (Yh) Yh[(size_t)b * yhs + i] = (_Float16)v;
+#pragma unroll
+  for (int j = 0; j < RMS_MAXV; ++j) {
+    const int i = (j * 256 + threadIdx.x) * 4;
+    if (i >= n) break;
+    const float4 wv = *(const float4 *)(w + i);
+    const float4 y = {wv.x * v[j].x * s, wv.y * v[j].y * s, wv.z * v[j].z * s, wv.w * v[j].w * s};
+    if (Y) *(float4 *)(Y + (size_t)b * ys + i) = y;
+    if (Yh) {
+      const half2_t a = {(_Float16)y.x, (_Float16)y.y}, c = {(_Float16)y.z, (_Float16)y.w};
+      *(uint2 *)(Yh + (size_t)b * yhs + i) = make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, c));
+    }
   }
 }
 
@@ -148,51 +167,62 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
 
 // ---- full attention, part 2: one workgroup per (key chunk, kv head) scores
 // the chunk against every query of the group (kvm heads x B positions, each
-// masked to t <= its position), then accumulates exp(s - m_chunk) * V.
-// Lane = key within the chunk for the scores; thread = head dim for P.V.
+// masked to t <= its position), then accumulates exp(s - m_chunk) * V.  The
+// chunk's K rows, then its V rows, are staged in LDS with a padded row
+// stride (KROW floats: the float4 reads of 16 consecutive rows hit distinct
+// banks).  Scores: lane = key, queries strided over 8 groups.  P.V: thread =
+// head dim, 8 queries at a time.
+constexpr int KROW = HD + 4;
 __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
-  extern __shared__ float sm[];      // S / P [nq][TC], then q rows [nq][HD]
+  extern __shared__ __align__(16) float sm[];  // Kt [TC][KROW] | Q [nq][HD] | S [nq][TC]
   const int c = blockIdx.x, hkv = blockIdx.y;
   const int kvm = p.NH / p.NKV;
   const int nq = p.B * kvm;
   const int t0 = c * TC;
   const int tlast = p.pbase + p.B - 1;       // last position of the block
   if (t0 > tlast) return;
-  float *S = sm;                             // [nq][TC]
-  float *Q = sm + nq * TC;                   // [nq][HD]
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tn = min(TC, tlast + 1 - t0);    // keys of this chunk that exist
+  float *Kt = sm;
+  float *Q = sm + TC * KROW;
+  float *S = Q + nq * HD;
+  const int tid = threadIdx.x;
   const float scale = 1.f / sqrtf((float)HD);
-  // queries of this group: (b, m) -> head hkv*kvm + m
-  for (int e = tid; e < nq * HD; e += 256) {
-    const int qi = e / HD, d = e % HD;
+  for (int e = tid; e < nq * (HD / 4); e += 256) {  // queries: (b, m) -> head hkv*kvm + m
+    const int qi = e / (HD / 4), d4 = e % (HD / 4);
     const int b = qi / kvm, m = qi % kvm;
-    Q[e] = p.q[((size_t)b * p.NH + hkv * kvm + m) * HD + d];
+    *(float4 *)(Q + qi * HD + d4 * 4) = *(const float4 *)(p.q + ((size_t)b * p.NH + hkv * kvm + m) * HD + d4 * 4);
+  }
+  for (int e = tid; e < TC * (HD / 4); e += 256) {
+    const int t = e / (HD / 4), d4 = e % (HD / 4);
+    *(float4 *)(Kt + t * KROW + d4 * 4) =
+        t < tn ? *(const float4 *)(p.K + ((size_t)(t0 + t) * p.NKV + hkv) * HD + d4 * 4) : (float4){0.f, 0.f, 0.f, 0.f};
   }
   __syncthreads();
-  // scores: wave w takes queries w, w+4, ...; lane = key t0 + lane
-  {
-    const int t = t0 + lane;
-    const float *kr = p.K + ((size_t)t * p.NKV + hkv) * HD;
-    const bool tv = t <= tlast;
-    for (int qi = wave; qi < nq; qi += 4) {
+  {  // scores and chunk softmax statistics
+    const int key = tid & (TC - 1), qg = tid / TC;   // TC = 32: 8 query groups
+    const int t = t0 + key;
+    const float *kr = Kt + key * KROW;
+    for (int qi = qg; qi < nq; qi += 256 / TC) {
       const int b = qi / kvm;
       const float *q = Q + qi * HD;
-      float s = 0.f;
-      if (tv && t <= p.pbase + b) {
+      float sc = -__builtin_inff();
+      if (t <= p.pbase + b && key < tn) {
+        float a = 0.f;
         for (int d = 0; d < HD; d += 4) {
-          const float4 k4 = *(const float4 *)(kr + d);
-          s = fmaf(q[d], k4.x, s); s = fmaf(q[d + 1], k4.y, s);
-          s = fmaf(q[d + 2], k4.z, s); s = fmaf(q[d + 3], k4.w, s);
+          const float4 k4 = *(const float4 *)(kr + d), q4 = *(const float4 *)(q + d);
+          a = fmaf(q4.x, k4.x, a); a = fmaf(q4.y, k4.y, a); a = fmaf(q4.z, k4.z, a); a = fmaf(q4.w, k4.w, a);
         }
-        s *= scale;
-      } else {
-        s = -__builtin_inff();
+        sc = a * scale;
       }
-      const float m = max64(s);
-      const float e = (s == -__builtin_inff()) ? 0.f : expf(s - m);
-      const float l = sum64(e);
-      S[qi * TC + lane] = e;
-      if (lane == 0) {
+      // max / sum over the 32 keys (lanes 0-31 or 32-63 of the wave)
+      float m = sc;
+      m = fmaxf(m, dpp<0xB1>(m)); m = fmaxf(m, dpp<0x4E>(m)); m = fmaxf(m, dpp<0x141>(m)); m = fmaxf(m, dpp<0x140>(m));
+      m = fmaxf(m, __shfl_xor(m, 16));
+      const float e = (sc == -__builtin_inff()) ? 0.f : expf(sc - m);
+      float l = sum16(e);
+      l += __shfl_xor(l, 16);
+      S[qi * TC + key] = e;
+      if (key == 0) {
         const size_t pi = ((size_t)hkv * p.nchunk + c) * nq + qi;
         p.pm[pi] = m;
         p.pl[pi] = l;
@@ -200,15 +230,33 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-  // P.V: thread = head dim
-  {
+  for (int e = tid; e < TC * (HD / 4); e += 256) {  // V rows replace K
+    const int t = e / (HD / 4), d4 = e % (HD / 4);
+    *(float4 *)(Kt + t * KROW + d4 * 4) =
+        t < tn ? *(const float4 *)(p.V + ((size_t)(t0 + t) * p.NKV + hkv) * HD + d4 * 4) : (float4){0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();
+  {  // P.V: thread = head dim
     const int d = tid;
-    const int tn = min(TC, tlast + 1 - t0);
-    for (int qi = 0; qi < nq; ++qi) {
-      const float *pr = S + qi * TC;
-      float o = 0.f;
-      for (int j = 0; j < tn; ++j) o = fmaf(pr[j], p.V[((size_t)(t0 + j) * p.NKV + hkv) * HD + d], o);
-      p.po[(((size_t)hkv * p.nchunk + c) * nq + qi) * HD + d] = o;
+    for (int q0 = 0; q0 < nq; q0 += 8) {
+      const int nqq = min(8, nq - q0);
+      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < TC; t += 4) {
+        const float v0 = Kt[(t + 0) * KROW + d], v1 = Kt[(t + 1) * KROW + d];
+        const float v2 = Kt[(t + 2) * KROW + d], v3 = Kt[(t + 3) * KROW + d];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (j >= nqq) break;
+          const float4 pr = *(const float4 *)(S + (q0 + j) * TC + t);
+          o[j] = fmaf(pr.x, v0, o[j]); o[j] = fmaf(pr.y, v1, o[j]);
+          o[j] = fmaf(pr.z, v2, o[j]); o[j] = fmaf(pr.w, v3, o[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j >= nqq) break;
+        p.po[(((size_t)hkv * p.nchunk + c) * nq + q0 + j) * HD + d] = o[j];
+      }
     }
   }
 }
@@ -248,6 +296,7 @@ int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *tok
 
 int rmsnorm_launch(const float *X, int xs, const float *w, int n, float eps, float *Y, int ys, _Float16 *Yh,
                    int yhs, int B, hipStream_t st) {
+  if (n % 4 || n > RMS_MAXV * 1024 || xs % 4 || (Y && ys % 4) || (Yh && yhs % 4)) return CWEN_EINVAL;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)B), dim3(256), 0, st, X, xs, w, n, eps, Y, ys, Yh, yhs);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
@@ -276,7 +325,7 @@ int attention_launch(const float *qfull, const float *kx, const float *vx, int k
   p.yh = yh;
   hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
   const int nc = (pbase + B - 1) / TC + 1;
-  const size_t lds = (size_t)nq * (TC + HD) * sizeof(float);
+  const size_t lds = ((size_t)TC * KROW + (size_t)nq * (TC + HD)) * sizeof(float);
   static bool lds_set = false;  // allow the dynamic LDS of B = 16 blocks (above 64 KB)
   if (!lds_set) {
     CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
