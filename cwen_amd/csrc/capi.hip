@@ -22,6 +22,49 @@ constexpr int kCounters = 1 << 16;
 
 }  // namespace
 
+int gemv_alloc_q4(cwen_ctx *ctx, int K, int M, cwen_weight **out) {
+  if (K % Q4_K_ALIGN || K > CWEN_KMAX || M <= 0) return CWEN_EINVAL;
+  cwen_weight *w = (cwen_weight *)calloc(1, sizeof(cwen_weight));
+  if (!w) return CWEN_ENOMEM;
+  w->ctx = ctx; w->type = CWEN_T_Q4_0RS; w->fmt = GEMV_Q4;
+  w->ne0 = K; w->ne1 = M; w->nside = 1;
+  w->nrg = (M + Q4_ROWS - 1) / Q4_ROWS;
+  w->nst = K / Q4_ST_K;
+  w->bytes = (size_t)w->nrg * w->nst * gemv_st_bytes(GEMV_Q4);
+  w->src_bytes = (size_t)(K / 32) * M * 18;
+  if (w->bytes >= ((size_t)1 << 32)) { free(w); return CWEN_EINVAL; }
+  gemv_choose_split(ctx, w);
+  if (hipMalloc((void **)&w->dev, w->bytes) != hipSuccess) { free(w); return CWEN_ENOMEM; }
+  if (hipMemset(w->dev, 0, w->bytes) != hipSuccess) { (void)hipFree(w->dev); free(w); return CWEN_EHIP; }
+  *out = w;
+  return CWEN_OK;
+}
+
+int gemv_upload_part(cwen_weight *w, int type, const void *data, const void *scales, int M, int row_off,
+                     int side_sel) {
+  if (type != CWEN_T_Q4_0 && type != CWEN_T_Q4_0RS && type != CWEN_T_Q4_0RSI) return CWEN_ETYPE;
+  if (type != CWEN_T_Q4_0 && !scales) return CWEN_EINVAL;
+  const size_t nblk = (size_t)(w->ne0 / 32) * M;
+  const size_t qbytes = type == CWEN_T_Q4_0 ? nblk * 18 : type == CWEN_T_Q4_0RS ? nblk * 16 : nblk * 32;
+  const size_t sbytes = type == CWEN_T_Q4_0 ? 0 : type == CWEN_T_Q4_0RS ? nblk * 2 : nblk * 4;
+  uint8_t *dsrc = nullptr;
+  uint16_t *dsc = nullptr;
+  int rc = CWEN_OK;
+  if (hipMalloc((void **)&dsrc, qbytes) != hipSuccess) return CWEN_ENOMEM;
+  if (sbytes && hipMalloc((void **)&dsc, sbytes) != hipSuccess) { rc = CWEN_ENOMEM; goto done; }
+  if (hipMemcpy(dsrc, data, qbytes, hipMemcpyHostToDevice) != hipSuccess ||
+      (sbytes && hipMemcpy(dsc, scales, sbytes, hipMemcpyHostToDevice) != hipSuccess)) {
+    rc = CWEN_EHIP;
+    goto done;
+  }
+  rc = gemv_repack_part(w, dsrc, dsc, type, M, row_off, side_sel, nullptr);
+  if (!rc && hipDeviceSynchronize() != hipSuccess) rc = CWEN_EHIP;
+done:
+  if (dsrc) (void)hipFree(dsrc);
+  if (dsc) (void)hipFree(dsc);
+  return rc;
+}
+
 extern "C" {
 
 const char *cwen_version(void) { return "cwen-gpu 0.1 gfx950"; }

@@ -104,6 +104,15 @@ struct GemvOut {
 int gemv_fmt_of(int type);
 size_t gemv_st_bytes(int fmt);
 int gemv_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStream_t st);
+// Repack a Q4 source of M rows (side side_sel of a Q4_0RSI source, else -1)
+// into rows row_off.. of a single-sided Q4 weight (row-concatenated weights).
+int gemv_repack_part(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, int type, int M, int row_off,
+                     int side_sel, hipStream_t st);
+// A zero-filled single-sided Q4 weight of K x M to receive parts.
+int gemv_alloc_q4(cwen_ctx *ctx, int K, int M, cwen_weight **out);
+// Upload a Q4 source from HOST memory into rows row_off.. of w.
+int gemv_upload_part(cwen_weight *w, int type, const void *data, const void *scales, int M, int row_off,
+                     int side_sel);
 void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w);
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
                 const _Float16 *xh, const GemvOut &out, int B, hipStream_t st);
@@ -122,7 +131,7 @@ int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *tok
 int rmsnorm_launch(const float *X, int xs, const float *w, int n, float eps, float *Y, int ys, _Float16 *Yh,
                    int yhs, int B, hipStream_t st);
 size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B);
-int attention_launch(const float *qfull, const float *kx, const float *vx, int kvs, const float *qn,
+int attention_launch(const float *qfull, int qfs, const float *kx, const float *vx, int kvs, const float *qn,
                      const float *kn, float *qbuf, float *K, float *V, int pbase, int B, int NH, int NKV,
                      int npairs, int nrot, float theta, float eps, float *part, int max_ctx, _Float16 *yh,
                      hipStream_t st);

@@ -574,9 +574,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 
 // Q4_0 family: lane l = 16g + n gets, for each tile u, block g of that tile
 // for row n -- 4 dwords, dword j holding K run j (weights 8j..8j+7 of the
-// block) in kNibPos order -- and the 4 blocks' f16 scales.
+// block) in kNibPos order -- and the 4 blocks' f16 scales.  The source (M rows,
+// nrg row groups) lands at destination row group rg_off onward; side_sel >= 0
+// takes that side of a Q4_0RSI source into a single-sided destination.
 __global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_t *sc, int type,
-                                 int M, int K, int nrg, int nst, int nsw) {
+                                 int M, int K, int nrg, int nst, int nsw, int rg_off, int side_sel) {
   const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   const size_t total = (size_t)nrg * nst * nsw * 64;
   if (id >= total) return;
@@ -588,7 +590,8 @@ __global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_
   const int n = lane & 15, g = lane >> 4;
   const int row = rg * Q4_ROWS + n;
   const int nb = K / 32;
-  uint8_t *stile = dst + (((size_t)rg * nst + st) * nsw + side) * Fmt<GEMV_Q4>::ST_BYTES;
+  const int sside = side_sel >= 0 ? side_sel : side;
+  uint8_t *stile = dst + (((size_t)(rg + rg_off) * nst + st) * nsw + side) * Fmt<GEMV_Q4>::ST_BYTES;
   uint16_t d[TILES];
   for (int u = 0; u < TILES; ++u) {
     const int blk = (st * TILES + u) * 4 + g;
@@ -604,8 +607,8 @@ __global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_
         qs = src + bi * 16;
         d[u] = sc[bi];
       } else {  // Q4_0RSI
-        qs = src + bi * 32 + side * 16;
-        d[u] = sc[bi * 2 + side];
+        qs = src + bi * 32 + sside * 16;
+        d[u] = sc[bi * 2 + sside];
       }
     }
     uint32_t out[4];
@@ -814,13 +817,26 @@ int gemv_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStr
   const size_t grid = (threads + blk - 1) / blk;
   if (w->fmt == GEMV_Q4)
     hipLaunchKernelGGL(repack_q4_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, dsc,
-                       w->type, w->ne1, w->ne0, w->nrg, w->nst, w->nside);
+                       w->type, w->ne1, w->ne0, w->nrg, w->nst, w->nside, 0, -1);
   else if (w->fmt == GEMV_Q6K)
     hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, w->ne1,
                        w->ne0, w->nrg, w->nst);
   else
     hipLaunchKernelGGL(repack_q8_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, w->ne1,
                        w->ne0, w->nrg, w->nst);
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}
+
+int gemv_repack_part(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, int type, int M, int row_off,
+                     int side_sel, hipStream_t st) {
+  if (w->fmt != GEMV_Q4 || w->nside != 1 || row_off % Q4_ROWS || row_off + M > w->ne1) return CWEN_EINVAL;
+  if ((side_sel >= 0) != (type == CWEN_T_Q4_0RSI) || side_sel > 1) return CWEN_EINVAL;
+  const int nrg = (M + Q4_ROWS - 1) / Q4_ROWS;
+  const size_t threads = (size_t)nrg * w->nst * 64;
+  const int blk = 256;
+  hipLaunchKernelGGL(repack_q4_kernel, dim3((unsigned)((threads + blk - 1) / blk)), dim3(blk), 0, st, w->dev, dsrc,
+                     dsc, type, M, w->ne0, nrg, w->nst, 1, row_off / Q4_ROWS, side_sel);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }

@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *X, int xs, co
 // [HD] weight each), partial RoPE on pairs (2i, 2i+1), i < npairs, and the
 // KV-cache write.  Grid: (B, NH + NKV), 256 threads = head dims.
 struct AttnParams {
-  const float *qfull;  // [B][NH*2*HD]: per head q (HD) then gate (HD)
+  const float *qfull; int qfs;  // [B][qfs]: per head q (HD) then gate (HD)
   const float *kx, *vx; int kvs;  // [B][kvs]: NKV*HD each
   const float *qn, *kn;
   float *q;            // [B][NH][HD] normed + roped queries
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
   const int pos = p.pbase + b;
   const bool isq = h < p.NH;
   const int hk = h - p.NH;
-  const float x = isq ? p.qfull[(size_t)b * p.NH * 2 * HD + (size_t)h * 2 * HD + d]
+  const float x = isq ? p.qfull[(size_t)b * p.qfs + (size_t)h * 2 * HD + d]
                       : p.kx[(size_t)b * p.kvs + hk * HD + d];
   const float s = 1.f / sqrtf(sum256(x * x, red) / (float)HD + p.eps);
   float y = (isq ? p.qn[d] : p.kn[d]) * x * s;
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     L = fmaf(w, p.pl[pi], L);
     O = fmaf(w, p.po[pi * HD + d], O);
   }
-  const float g = p.qfull[(size_t)b * p.NH * 2 * HD + (size_t)h * 2 * HD + HD + d];
+  const float g = p.qfull[(size_t)b * p.qfs + (size_t)h * 2 * HD + HD + d];
   const float y = (O / L) * (1.f / (1.f + expf(-g)));
   p.yh[(size_t)b * p.NH * HD + (size_t)h * HD + d] = (_Float16)y;
 }
@@ -307,12 +307,12 @@ size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B) {
   return (size_t)NKV * nchunk * B * (NH / NKV) * (HD + 2);
 }
 
-int attention_launch(const float *qfull, const float *kx, const float *vx, int kvs, const float *qn,
+int attention_launch(const float *qfull, int qfs, const float *kx, const float *vx, int kvs, const float *qn,
                      const float *kn, float *qbuf, float *K, float *V, int pbase, int B, int NH, int NKV,
                      int npairs, int nrot, float theta, float eps, float *part, int max_ctx, _Float16 *yh,
                      hipStream_t st) {
   AttnParams p;
-  p.qfull = qfull; p.kx = kx; p.vx = vx; p.kvs = kvs;
+  p.qfull = qfull; p.qfs = qfs; p.kx = kx; p.vx = vx; p.kvs = kvs;
   p.qn = qn; p.kn = kn;
   p.q = qbuf; p.K = K; p.V = V;
   p.pbase = pbase; p.B = B; p.NH = NH; p.NKV = NKV; p.npairs = npairs; p.nrot = nrot;

@@ -15,16 +15,21 @@
 
 namespace {
 
+// The GEMVs that read the same normalised input are one row-concatenated
+// weight, one launch: GDN layers [qkv | gate | alpha | beta] (lin_in), full
+// layers [wq | wk | wv] (att_in; the k/v pair's two sides become two row
+// blocks).  `parts` records which row blocks have been uploaded.
 struct Layer {
   int linear;
   float *attn_norm = nullptr, *post_norm = nullptr;
   cwen_weight *ffn_gu = nullptr, *ffn_down = nullptr;
-  cwen_weight *qkv = nullptr, *gate_z = nullptr, *alpha = nullptr, *beta = nullptr, *ssm_out = nullptr;
+  cwen_weight *lin_in = nullptr, *ssm_out = nullptr;
   float *ssm_a = nullptr, *ssm_dt = nullptr, *ssm_conv = nullptr, *ssm_norm = nullptr;
   cwen_gdn *gdn = nullptr;
-  cwen_weight *wq = nullptr, *wkv = nullptr, *wo = nullptr;
+  cwen_weight *att_in = nullptr, *wo = nullptr;
   float *q_norm = nullptr, *k_norm = nullptr;
   float *K = nullptr, *V = nullptr;
+  unsigned parts = 0;
 };
 
 template <class T> int dmalloc(T **p, size_t n) {
@@ -47,9 +52,10 @@ struct cwen_model {
   int *toks = nullptr, *drafts = nullptr, *res = nullptr;
   float *X = nullptr;            // residual stream [BMAX][H]
   _Float16 *Xh = nullptr;        // normed f16 operand [BMAX][H]
-  float *qkv = nullptr, *z = nullptr, *ga = nullptr, *gb = nullptr;
+  float *lin = nullptr;           // GDN layer input GEMV out [BMAX][lin_rows]
   _Float16 *gh = nullptr;        // GDN output f16 [BMAX][nvh*dk]
-  float *qfull = nullptr, *kx = nullptr, *vx = nullptr, *qbuf = nullptr, *apart = nullptr;
+  float *att = nullptr;           // attention input GEMV out [BMAX][att_rows]
+  float *qbuf = nullptr, *apart = nullptr;
   _Float16 *yh = nullptr;        // attention output f16 [BMAX][NH*HD]
   _Float16 *hh = nullptr;        // FFN hidden f16 [BMAX][I]
   float *logits = nullptr;       // [BMAX][V]
@@ -59,6 +65,28 @@ struct cwen_model {
 namespace {
 
 bool is_full(const cwen_model_cfg &c, int l) { return l % c.full_interval == c.full_interval - 1; }
+
+// Row layout of the concatenated input weights.
+// Row blocks start on 16-row groups (a block shorter than a multiple of 16
+// is followed by zero rows).
+struct Rows {
+  int C, Zh, nvh, lin;        // lin_in: qkv C | gate Zh | alpha nvh | beta nvh
+  int o_alpha, o_beta;        // row offsets of the alpha and beta blocks
+  int Qo2, Ko, att;           // att_in: wq 2*Qo | wk Ko | wv Ko
+};
+Rows rows_of(const cwen_model_cfg &c) {
+  Rows r;
+  r.C = (2 * c.gdn_nkh + c.gdn_nvh) * 128;
+  r.Zh = c.gdn_nvh * 128;
+  r.nvh = c.gdn_nvh;
+  r.o_alpha = r.C + r.Zh;
+  r.o_beta = r.o_alpha + (r.nvh + Q4_ROWS - 1) / Q4_ROWS * Q4_ROWS;
+  r.lin = r.o_beta + r.nvh;
+  r.Qo2 = 2 * c.n_head * c.head_dim;
+  r.Ko = c.n_kv_head * c.head_dim;
+  r.att = r.Qo2 + 2 * r.Ko;
+  return r;
+}
 
 int check_cfg(const cwen_model_cfg *c) {
   if (!c || c->n_layers <= 0 || c->d_model <= 0 || c->d_ffn <= 0 || c->vocab <= 0) return CWEN_EINVAL;
@@ -101,32 +129,23 @@ int block(cwen_model *m, int B, int head, int E, hipStream_t st) {
     Layer &y = m->L[l];
     if ((rc = rmsnorm_launch(m->X, H, y.attn_norm, H, c.rms_eps, nullptr, 0, m->Xh, H, B, st))) return rc;
     if (y.linear) {
-      const int C = (2 * c.gdn_nkh + c.gdn_nvh) * 128, Zh = c.gdn_nvh * 128;
-      GemvOut o1 = {m->qkv, nullptr, nullptr, C, 0};
-      GemvOut o2 = {m->z, nullptr, nullptr, Zh, 0};
-      GemvOut o3 = {m->ga, nullptr, nullptr, c.gdn_nvh, 0};
-      GemvOut o4 = {m->gb, nullptr, nullptr, c.gdn_nvh, 0};
-      if ((rc = gemv_launch(ctx, y.qkv, 1, 0, GEMV_EPI_STORE, m->Xh, o1, B, st)) ||
-          (rc = gemv_launch(ctx, y.gate_z, 1, 0, GEMV_EPI_STORE, m->Xh, o2, B, st)) ||
-          (rc = gemv_launch(ctx, y.alpha, 1, 0, GEMV_EPI_STORE, m->Xh, o3, B, st)) ||
-          (rc = gemv_launch(ctx, y.beta, 1, 0, GEMV_EPI_STORE, m->Xh, o4, B, st)))
-        return rc;
-      if ((rc = gdn_block_launch(y.gdn, m->qkv, C, m->z, Zh, m->ga, m->gb, c.gdn_nvh, y.ssm_conv, y.ssm_norm,
-                                 nullptr, 0, B, st, m->gh, Zh, y.ssm_a, y.ssm_dt)))
+      const Rows r = rows_of(c);
+      GemvOut o1 = {m->lin, nullptr, nullptr, r.lin, 0};
+      if ((rc = gemv_launch(ctx, y.lin_in, 1, 0, GEMV_EPI_STORE, m->Xh, o1, B, st))) return rc;
+      const float *qkv = m->lin, *z = m->lin + r.C, *ga = m->lin + r.o_alpha, *gb = m->lin + r.o_beta;
+      if ((rc = gdn_block_launch(y.gdn, qkv, r.lin, z, r.lin, ga, gb, r.lin, y.ssm_conv, y.ssm_norm, nullptr, 0, B,
+                                 st, m->gh, r.Zh, y.ssm_a, y.ssm_dt)))
         return rc;
       y.gdn->last_B = B;
       GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
       if ((rc = gemv_launch(ctx, y.ssm_out, 1, 0, GEMV_EPI_STORE, m->gh, o5, B, st))) return rc;
     } else {
-      const int Qo = c.n_head * c.head_dim, Ko = c.n_kv_head * c.head_dim;
-      GemvOut o1 = {m->qfull, nullptr, nullptr, 2 * Qo, 0};
-      GemvOut o2 = {m->kx, m->vx, nullptr, Ko, 0};
-      if ((rc = gemv_launch(ctx, y.wq, 1, 0, GEMV_EPI_STORE, m->Xh, o1, B, st)) ||
-          (rc = gemv_launch(ctx, y.wkv, 2, 0, GEMV_EPI_PAIR, m->Xh, o2, B, st)))
-        return rc;
-      if ((rc = attention_launch(m->qfull, m->kx, m->vx, Ko, y.q_norm, y.k_norm, m->qbuf, y.K, y.V, pbase, B,
-                                 c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot, c.rope_theta, c.rms_eps,
-                                 m->apart, c.max_ctx, m->yh, st)))
+      const Rows r = rows_of(c);
+      GemvOut o1 = {m->att, nullptr, nullptr, r.att, 0};
+      if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, m->Xh, o1, B, st))) return rc;
+      if ((rc = attention_launch(m->att, r.att, m->att + r.Qo2, m->att + r.Qo2 + r.Ko, r.att, y.q_norm, y.k_norm,
+                                 m->qbuf, y.K, y.V, pbase, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
+                                 c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st)))
         return rc;
       GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
       if ((rc = gemv_launch(ctx, y.wo, 1, 0, GEMV_EPI_STORE, m->yh, o5, B, st))) return rc;
@@ -159,10 +178,9 @@ int ready(const cwen_model *m) {
   for (int l = 0; l < m->cfg.n_layers; ++l) {
     const Layer &y = m->L[l];
     if (!y.attn_norm || !y.post_norm || !y.ffn_gu || !y.ffn_down) return 0;
-    if (y.linear && (!y.qkv || !y.gate_z || !y.alpha || !y.beta || !y.ssm_out || !y.ssm_a || !y.ssm_dt ||
-                     !y.ssm_conv || !y.ssm_norm))
+    if (y.linear && (y.parts != 15u || !y.ssm_out || !y.ssm_a || !y.ssm_dt || !y.ssm_conv || !y.ssm_norm))
       return 0;
-    if (!y.linear && (!y.wq || !y.wkv || !y.wo || !y.q_norm || !y.k_norm)) return 0;
+    if (!y.linear && (y.parts != 3u || !y.wo || !y.q_norm || !y.k_norm)) return 0;
   }
   return 1;
 }
@@ -211,51 +229,76 @@ __global__ void synth_f32_kernel(float *p, size_t n, int kind, float mu, float s
 
 int synth_launch_grid(size_t n) { return (int)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536); }
 
-// A quantized weight of `type` [ne1][ne0] generated in its reference layout on
-// the device, then repacked like an upload.
-int synth_weight(cwen_ctx *ctx, int type, int ne0, int ne1, uint64_t seed, uint64_t key, cwen_weight **out) {
+// A quantized matrix of `type` [ne1][ne0] generated in its reference layout on
+// the device (raw bytes and scale channel).
+struct Raw {
+  uint8_t *q = nullptr, *s = nullptr;
+  ~Raw() {
+    if (q) (void)hipFree(q);
+    if (s) (void)hipFree(s);
+  }
+};
+int synth_raw(int type, int ne0, int ne1, uint64_t seed, uint64_t key, Raw &r) {
   const size_t nblk = (size_t)(ne0 / 32) * ne1;
   size_t qbytes, sbytes = 0;
-  int nside = 1;
   switch (type) {
     case CWEN_T_Q4_0RS: qbytes = nblk * 16; sbytes = nblk * 2; break;
-    case CWEN_T_Q4_0RSI: qbytes = nblk * 32; sbytes = nblk * 4; nside = 2; break;
+    case CWEN_T_Q4_0RSI: qbytes = nblk * 32; sbytes = nblk * 4; break;
     case CWEN_T_Q6_K: qbytes = (size_t)(ne0 / 256) * ne1 * 210; break;
     default: return CWEN_ETYPE;
   }
+  if (dmalloc(&r.q, qbytes) || (sbytes && dmalloc(&r.s, sbytes))) return CWEN_ENOMEM;
+  hipLaunchKernelGGL(synth_bytes_kernel, dim3(synth_launch_grid(qbytes)), dim3(256), 0, nullptr, r.q, qbytes, seed,
+                     key * 4);
+  if (type == CWEN_T_Q6_K)  // d = f16(|N(0, 0.002)|) at byte 208 of each 210-byte super-block
+    hipLaunchKernelGGL(synth_scale_kernel, dim3(synth_launch_grid(qbytes / 210)), dim3(256), 0, nullptr, r.q + 208,
+                       qbytes / 210, (size_t)210, 0.002f, seed, key * 4 + 1);
+  else  // f16(|N(0, 0.02)| / 8)
+    hipLaunchKernelGGL(synth_scale_kernel, dim3(synth_launch_grid(sbytes / 2)), dim3(256), 0, nullptr, r.s,
+                       sbytes / 2, (size_t)2, 0.02f / 8.f, seed, key * 4 + 1);
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}
+
+int synth_weight(cwen_ctx *ctx, int type, int ne0, int ne1, uint64_t seed, uint64_t key, cwen_weight **out) {
+  if (ne0 % Q4_K_ALIGN) return CWEN_EINVAL;
+  Raw r;
+  int rc = synth_raw(type, ne0, ne1, seed, key, r);
+  if (rc) return rc;
   cwen_weight *w = (cwen_weight *)calloc(1, sizeof(cwen_weight));
   if (!w) return CWEN_ENOMEM;
   w->ctx = ctx; w->type = type; w->fmt = gemv_fmt_of(type);
-  w->ne0 = ne0; w->ne1 = ne1; w->nside = nside;
+  w->ne0 = ne0; w->ne1 = ne1; w->nside = type == CWEN_T_Q4_0RSI ? 2 : 1;
   w->nrg = (ne1 + Q4_ROWS - 1) / Q4_ROWS;
   w->nst = ne0 / Q4_ST_K;
-  w->bytes = (size_t)w->nrg * w->nst * nside * gemv_st_bytes(w->fmt);
-  w->src_bytes = qbytes + sbytes;
+  w->bytes = (size_t)w->nrg * w->nst * w->nside * gemv_st_bytes(w->fmt);
   gemv_choose_split(ctx, w);
-  uint8_t *dq = nullptr, *ds = nullptr;
-  int rc = CWEN_ENOMEM;
-  if (w->bytes >= ((size_t)1 << 32) || ne0 % Q4_K_ALIGN) { rc = CWEN_EINVAL; goto fail; }
-  if (dmalloc(&w->dev, w->bytes) || dmalloc(&dq, qbytes) || (sbytes && dmalloc(&ds, sbytes))) goto fail;
-  hipLaunchKernelGGL(synth_bytes_kernel, dim3(synth_launch_grid(qbytes)), dim3(256), 0, nullptr, dq, qbytes, seed,
-                     key * 4);
-  if (type == CWEN_T_Q6_K)  // d = f16(|N(0, 0.002)|) at byte 208 of each 210-byte super-block
-    hipLaunchKernelGGL(synth_scale_kernel, dim3(synth_launch_grid(qbytes / 210)), dim3(256), 0, nullptr, dq + 208,
-                       qbytes / 210, (size_t)210, 0.002f, seed, key * 4 + 1);
-  else  // f16(|N(0, 0.02)| / 8)
-    hipLaunchKernelGGL(synth_scale_kernel, dim3(synth_launch_grid(sbytes / 2)), dim3(256), 0, nullptr, ds,
-                       sbytes / 2, (size_t)2, 0.02f / 8.f, seed, key * 4 + 1);
-  if ((rc = gemv_repack(w, dq, (const uint16_t *)ds, nullptr))) goto fail;
-  if (hipDeviceSynchronize() != hipSuccess) { rc = CWEN_EHIP; goto fail; }
-  (void)hipFree(dq);
-  if (ds) (void)hipFree(ds);
+  if (w->bytes >= ((size_t)1 << 32)) { free(w); return CWEN_EINVAL; }
+  if (dmalloc(&w->dev, w->bytes)) { free(w); return CWEN_ENOMEM; }
+  if ((rc = gemv_repack(w, r.q, (const uint16_t *)r.s, nullptr)) || hipDeviceSynchronize() != hipSuccess) {
+    (void)hipFree(w->dev);
+    free(w);
+    return rc ? rc : CWEN_EHIP;
+  }
   *out = w;
   return CWEN_OK;
-fail:
-  if (dq) (void)hipFree(dq);
-  if (ds) (void)hipFree(ds);
-  if (w->dev) (void)hipFree(w->dev);
-  free(w);
-  return rc;
+}
+
+// Rows row_off.. of a concatenated weight from a generated matrix (both
+// sides of a generated Q4_0RSI pair when side_row_off[1] >= 0).
+int synth_part(cwen_weight *w, int type, int M, const int side_row_off[2], uint64_t seed, uint64_t key) {
+  Raw r;
+  int rc = synth_raw(type, w->ne0, M, seed, key, r);
+  if (rc) return rc;
+  if (type == CWEN_T_Q4_0RSI) {
+    if ((rc = gemv_repack_part(w, r.q, (const uint16_t *)r.s, type, M, side_row_off[0], 0, nullptr)) ||
+        (rc = gemv_repack_part(w, r.q, (const uint16_t *)r.s, type, M, side_row_off[1], 1, nullptr)))
+      return rc;
+  } else if ((rc = gemv_repack_part(w, r.q, (const uint16_t *)r.s, type, M, side_row_off[0], -1, nullptr))) {
+    return rc;
+  }
+  CWEN_HIP_TRY(hipDeviceSynchronize());
+  return CWEN_OK;
 }
 
 int synth_f32(float **out, size_t n, int kind, float mu, float sigma, uint64_t seed, uint64_t key) {
@@ -286,27 +329,26 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
   m->L = new (std::nothrow) Layer[c.n_layers];
   if (!m->L) { delete m; return CWEN_ENOMEM; }
   const int H = c.d_model, I = c.d_ffn, BM = CWEN_BMAX;
-  const int C = (2 * c.gdn_nkh + c.gdn_nvh) * 128, Zh = c.gdn_nvh * 128;
-  const int Qo = c.n_head * c.head_dim, Ko = c.n_kv_head * c.head_dim;
+  const Rows R = rows_of(c);
+  const int Zh = R.Zh, Qo = R.Qo2 / 2, Ko = R.Ko;
   rc = CWEN_OK;
   for (int l = 0; l < c.n_layers && !rc; ++l) {
     Layer &y = m->L[l];
     y.linear = !is_full(c, l);
     if (y.linear) {
-      rc = cwen_gdn_create(ctx, c.gdn_nkh, c.gdn_nvh, 128, &y.gdn);
+      if (!(rc = cwen_gdn_create(ctx, c.gdn_nkh, c.gdn_nvh, 128, &y.gdn)))
+        rc = gemv_alloc_q4(ctx, H, R.lin, &y.lin_in);
     } else {
       const size_t kv = (size_t)c.max_ctx * Ko;
       rc = dmalloc(&y.K, kv) || dmalloc(&y.V, kv) ? CWEN_ENOMEM : CWEN_OK;
+      if (!rc) rc = gemv_alloc_q4(ctx, H, R.att, &y.att_in);
     }
   }
   if (!rc)
     rc = (dmalloc(&m->toks, BM) || dmalloc(&m->drafts, BM) || dmalloc(&m->res, 2 + BM) ||
           dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->Xh, (size_t)BM * H) ||
-          dmalloc(&m->qkv, (size_t)BM * C) || dmalloc(&m->z, (size_t)BM * Zh) ||
-          dmalloc(&m->ga, (size_t)BM * c.gdn_nvh) || dmalloc(&m->gb, (size_t)BM * c.gdn_nvh) ||
-          dmalloc(&m->gh, (size_t)BM * Zh) || dmalloc(&m->qfull, (size_t)BM * 2 * Qo) ||
-          dmalloc(&m->kx, (size_t)BM * Ko) || dmalloc(&m->vx, (size_t)BM * Ko) ||
-          dmalloc(&m->qbuf, (size_t)BM * Qo) ||
+          dmalloc(&m->lin, (size_t)BM * R.lin) || dmalloc(&m->gh, (size_t)BM * Zh) ||
+          dmalloc(&m->att, (size_t)BM * R.att) || dmalloc(&m->qbuf, (size_t)BM * Qo) ||
           dmalloc(&m->apart, attn_partial_floats(c.n_head, c.n_kv_head, c.max_ctx, BM)) ||
           dmalloc(&m->yh, (size_t)BM * Qo) || dmalloc(&m->hh, (size_t)BM * I) ||
           dmalloc(&m->logits, (size_t)BM * c.vocab))
@@ -331,14 +373,14 @@ int cwen_model_free(cwen_model *m) {
     for (float *p : {y.attn_norm, y.post_norm, y.ssm_a, y.ssm_dt, y.ssm_conv, y.ssm_norm, y.q_norm, y.k_norm, y.K,
                      y.V})
       if (p) (void)hipFree(p);
-    for (cwen_weight *w : {y.ffn_gu, y.ffn_down, y.qkv, y.gate_z, y.alpha, y.beta, y.ssm_out, y.wq, y.wkv, y.wo})
+    for (cwen_weight *w : {y.ffn_gu, y.ffn_down, y.lin_in, y.ssm_out, y.att_in, y.wo})
       if (w) cwen_weight_free(w);
     if (y.gdn) cwen_gdn_free(y.gdn);
   }
   delete[] m->L;
   for (void *p : {(void *)m->emb_qs, (void *)m->emb_sc, (void *)m->out_norm, (void *)m->toks, (void *)m->drafts,
-                  (void *)m->res, (void *)m->X, (void *)m->Xh, (void *)m->qkv, (void *)m->z, (void *)m->ga,
-                  (void *)m->gb, (void *)m->gh, (void *)m->qfull, (void *)m->kx, (void *)m->vx, (void *)m->qbuf,
+                  (void *)m->res, (void *)m->X, (void *)m->Xh, (void *)m->lin, (void *)m->gh, (void *)m->att,
+                  (void *)m->qbuf,
                   (void *)m->apart, (void *)m->yh, (void *)m->hh, (void *)m->logits})
     if (p) (void)hipFree(p);
   if (m->head) cwen_weight_free(m->head);
@@ -385,12 +427,19 @@ int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data,
     case CWEN_FFN_DOWN: return upload_w(m, type, data, scales, ne0, ne1, I, H, &y.ffn_down);
     default: break;
   }
+  const Rows R = rows_of(c);
+  auto part = [&](cwen_weight *w, int want_ne1, int row_off, int side_sel, unsigned bit) {
+    if (ne0 != H || ne1 != want_ne1) return CWEN_EINVAL;
+    int rc = gemv_upload_part(w, type, data, scales, ne1, row_off, side_sel);
+    if (!rc) y.parts |= bit;
+    return rc;
+  };
   if (y.linear) {
     switch (id) {
-      case CWEN_ATTN_QKV: return upload_w(m, type, data, scales, ne0, ne1, H, C, &y.qkv);
-      case CWEN_ATTN_GATE: return upload_w(m, type, data, scales, ne0, ne1, H, Zh, &y.gate_z);
-      case CWEN_SSM_ALPHA: return upload_w(m, type, data, scales, ne0, ne1, H, c.gdn_nvh, &y.alpha);
-      case CWEN_SSM_BETA: return upload_w(m, type, data, scales, ne0, ne1, H, c.gdn_nvh, &y.beta);
+      case CWEN_ATTN_QKV: return part(y.lin_in, R.C, 0, -1, 1u);
+      case CWEN_ATTN_GATE: return part(y.lin_in, R.Zh, R.C, -1, 2u);
+      case CWEN_SSM_ALPHA: return part(y.lin_in, R.nvh, R.o_alpha, -1, 4u);
+      case CWEN_SSM_BETA: return part(y.lin_in, R.nvh, R.o_beta, -1, 8u);
       case CWEN_SSM_OUT: return upload_w(m, type, data, scales, ne0, ne1, Zh, H, &y.ssm_out);
       case CWEN_SSM_A: return (f32 && ne0 == c.gdn_nvh) ? upload_f32(data, ne0, &y.ssm_a) : CWEN_EINVAL;
       case CWEN_SSM_DT: return (f32 && ne0 == c.gdn_nvh) ? upload_f32(data, ne0, &y.ssm_dt) : CWEN_EINVAL;
@@ -400,9 +449,13 @@ int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data,
     }
   }
   switch (id) {
-    case CWEN_ATTN_Q: return upload_w(m, type, data, scales, ne0, ne1, H, 2 * Qo, &y.wq);
-    case CWEN_ATTN_KV:
-      return type == CWEN_T_Q4_0RSI ? upload_w(m, type, data, scales, ne0, ne1, H, Ko, &y.wkv) : CWEN_ETYPE;
+    case CWEN_ATTN_Q: return part(y.att_in, R.Qo2, 0, -1, 1u);
+    case CWEN_ATTN_KV: {
+      if (type != CWEN_T_Q4_0RSI) return CWEN_ETYPE;
+      int rc = part(y.att_in, R.Ko, R.Qo2, 0, 0u);
+      if (!rc) rc = part(y.att_in, R.Ko, R.Qo2 + R.Ko, 1, 2u);
+      return rc;
+    }
     case CWEN_ATTN_OUTPUT: return upload_w(m, type, data, scales, ne0, ne1, Qo, H, &y.wo);
     case CWEN_ATTN_Q_NORM: return (f32 && ne0 == c.head_dim) ? upload_f32(data, ne0, &y.q_norm) : CWEN_EINVAL;
     case CWEN_ATTN_K_NORM: return (f32 && ne0 == c.head_dim) ? upload_f32(data, ne0, &y.k_norm) : CWEN_EINVAL;
@@ -446,21 +499,29 @@ int cwen_model_synth(cwen_model *m, unsigned long long seed) {
         (rc = W(&y.ffn_gu, CWEN_T_Q4_0RSI, H, I, k0 + 3)) || (rc = W(&y.ffn_down, CWEN_T_Q4_0RS, I, H, k0 + 4)))
       return rc;
     if (y.linear) {
-      if ((rc = W(&y.qkv, CWEN_T_Q4_0RS, H, C, k0 + 5)) || (rc = W(&y.gate_z, CWEN_T_Q4_0RS, H, Zh, k0 + 6)) ||
-          (rc = W(&y.alpha, CWEN_T_Q4_0RS, H, c.gdn_nvh, k0 + 7)) ||
-          (rc = W(&y.beta, CWEN_T_Q4_0RS, H, c.gdn_nvh, k0 + 8)) ||
+      const Rows R = rows_of(c);
+      const int o0[2] = {0, -1}, o1[2] = {R.C, -1}, o2[2] = {R.o_alpha, -1}, o3[2] = {R.o_beta, -1};
+      if ((rc = synth_part(y.lin_in, CWEN_T_Q4_0RS, C, o0, seed, k0 + 5)) ||
+          (rc = synth_part(y.lin_in, CWEN_T_Q4_0RS, Zh, o1, seed, k0 + 6)) ||
+          (rc = synth_part(y.lin_in, CWEN_T_Q4_0RS, c.gdn_nvh, o2, seed, k0 + 7)) ||
+          (rc = synth_part(y.lin_in, CWEN_T_Q4_0RS, c.gdn_nvh, o3, seed, k0 + 8)) ||
           (rc = W(&y.ssm_out, CWEN_T_Q4_0RS, Zh, H, k0 + 9)) ||
           (rc = synth_f32(&y.ssm_a, c.gdn_nvh, 1, 0.f, 0.f, seed, k0 + 10)) ||
           (rc = synth_f32(&y.ssm_dt, c.gdn_nvh, 0, 0.f, 0.5f, seed, k0 + 11)) ||
           (rc = synth_f32(&y.ssm_conv, (size_t)4 * C, 0, 0.f, 0.3f, seed, k0 + 12)) ||
           (rc = synth_f32(&y.ssm_norm, 128, 0, 1.f, 0.1f, seed, k0 + 13)))
         return rc;
+      y.parts = 15u;
     } else {
-      if ((rc = W(&y.wq, CWEN_T_Q4_0RS, H, 2 * Qo, k0 + 14)) || (rc = W(&y.wkv, CWEN_T_Q4_0RSI, H, Ko, k0 + 15)) ||
+      const Rows R = rows_of(c);
+      const int oq[2] = {0, -1}, okv[2] = {R.Qo2, R.Qo2 + R.Ko};
+      if ((rc = synth_part(y.att_in, CWEN_T_Q4_0RS, 2 * Qo, oq, seed, k0 + 14)) ||
+          (rc = synth_part(y.att_in, CWEN_T_Q4_0RSI, Ko, okv, seed, k0 + 15)) ||
           (rc = W(&y.wo, CWEN_T_Q4_0RS, Qo, H, k0 + 16)) ||
           (rc = synth_f32(&y.q_norm, c.head_dim, 0, 1.f, 0.1f, seed, k0 + 17)) ||
           (rc = synth_f32(&y.k_norm, c.head_dim, 0, 1.f, 0.1f, seed, k0 + 18)))
         return rc;
+      y.parts = 3u;
     }
   }
   CWEN_HIP_TRY(hipDeviceSynchronize());
