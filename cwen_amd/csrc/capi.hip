@@ -341,11 +341,13 @@ int cwen_gdn_create(cwen_ctx *ctx, int nkh, int nvh, int dk, cwen_gdn **out) {
   if (hipMalloc((void **)&g->S, sf * g->nslot * sizeof(float)) != hipSuccess ||
       hipMalloc((void **)&g->H, hf * g->nslot * sizeof(float)) != hipSuccess ||
       hipMalloc((void **)&g->xc, (size_t)CWEN_BMAX * g->C * sizeof(float)) != hipSuccess ||
-      hipMalloc((void **)&g->ob, (size_t)CWEN_BMAX * nvh * dk * sizeof(float)) != hipSuccess) {
+      hipMalloc((void **)&g->ob, (size_t)CWEN_BMAX * nvh * dk * sizeof(float)) != hipSuccess ||
+      hipMalloc((void **)&g->dcur, sizeof(int)) != hipSuccess) {
     cwen_gdn_free(g);
     return CWEN_ENOMEM;
   }
-  if (hipMemset(g->S, 0, sf * sizeof(float)) != hipSuccess ||
+  g->own_dcur = 1;
+  if (hipMemset(g->dcur, 0, sizeof(int)) != hipSuccess || hipMemset(g->S, 0, sf * sizeof(float)) != hipSuccess ||
       hipMemset(g->H, 0, hf * sizeof(float)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
     cwen_gdn_free(g);
     return CWEN_EHIP;
@@ -362,6 +364,7 @@ int cwen_gdn_free(cwen_gdn *g) {
   if (g->H) (void)hipFree(g->H);
   if (g->xc) (void)hipFree(g->xc);
   if (g->ob) (void)hipFree(g->ob);
+  if (g->dcur && g->own_dcur) (void)hipFree(g->dcur);
   free(g);
   return CWEN_OK;
 }
@@ -406,8 +409,12 @@ int cwen_gdn_block(cwen_ctx *ctx, cwen_gdn *g, const float *qkv, int qs, const f
 }
 
 int cwen_gdn_commit(cwen_gdn *g, int n) {
-  if (!g || n < 0 || n > g->last_B) return CWEN_EINVAL;
-  g->cur = (g->cur + n) % g->nslot;
+  if (!g || n < 0 || n > g->last_B || !g->own_dcur) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipSetDevice(g->ctx->device));
+  CWEN_HIP_TRY(hipDeviceSynchronize());  // blocks already queued read the old slot
+  const int cur = (g->cur + n) % g->nslot;
+  CWEN_HIP_TRY(hipMemcpy(g->dcur, &cur, sizeof(int), hipMemcpyHostToDevice));
+  g->cur = cur;
   g->last_B = 0;
   return CWEN_OK;
 }

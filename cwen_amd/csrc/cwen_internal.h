@@ -54,7 +54,9 @@ struct cwen_weight {
 struct cwen_gdn {
   cwen_ctx *ctx;
   int nkh, nvh, dk, C;
-  int nslot, cur;
+  int nslot, cur;           // host copy of the current slot
+  int *dcur;                // device copy of the current slot (what the kernels read)
+  int own_dcur;             // dcur allocated by this object (else borrowed from a model)
   int last_B;               // positions of the last block (commit bound)
   float *S, *H;             // device slot rings
   float *xc, *ob;           // scratch: post-conv values [BMAX][C], pre-norm outputs [BMAX][nvh*dk]
@@ -131,7 +133,11 @@ int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *tok
 int rmsnorm_launch(const float *X, int xs, const float *w, int n, float eps, float *Y, int ys, _Float16 *Yh,
                    int yhs, int B, hipStream_t st);
 size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B);
+int attention_init();
+// `last` is a device int: the last filled cache slot before the block (the
+// block's positions are last+1 .. last+B).  The launch shape depends on
+// (B, NH, NKV, max_ctx) only, so a captured graph replays at any position.
 int attention_launch(const float *qfull, int qfs, const float *kx, const float *vx, int kvs, const float *qn,
-                     const float *kn, float *qbuf, float *K, float *V, int pbase, int B, int NH, int NKV,
+                     const float *kn, float *qbuf, float *K, float *V, const int *last, int B, int NH, int NKV,
                      int npairs, int nrot, float theta, float eps, float *part, int max_ctx, _Float16 *yh,
                      hipStream_t st);

@@ -63,13 +63,15 @@ __device__ __forceinline__ float sum64(float v) {
          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
 }
 
+// Slot ring: the state before the block is slot *cur; the state after
+// position b is written to slot (*cur + 1 + b) % nslot.  The slot is read on
+// the device, so a captured launch replays at any ring position.
 struct GdnParams {
-  const float *S_in;          // state slot read [nvh][DK][DK]
-  float *S_slots;             // slot ring base
-  const float *H_in;          // conv history slot read [C][3]
-  float *H_slots;
+  float *S_slots;             // state ring [nslot][nvh][DK][DK]
+  float *H_slots;             // conv history ring [nslot][C][3]
   size_t s_floats, h_floats;  // floats per slot
-  int cur, nslot;
+  const int *cur;             // device: current slot
+  int nslot;
   const float *qkv; int qs;   // raw (pre-conv) qkv [B][qs]
   const float *z; int zs;     // [B][zs]
   const float *decay, *beta; int gs;  // [B][gs]
@@ -88,21 +90,23 @@ struct GdnParams {
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
   const int c = blockIdx.x * 256 + threadIdx.x;
   if (c >= p.C) return;
+  const int cur = *p.cur;
+  const float *H_in = p.H_slots + (size_t)cur * p.h_floats;
   const float4 w = *(const float4 *)(p.kw + (size_t)c * 4);
-  float h0 = p.H_in[(size_t)c * 3 + 0], h1 = p.H_in[(size_t)c * 3 + 1], h2 = p.H_in[(size_t)c * 3 + 2];
+  float h0 = H_in[(size_t)c * 3 + 0], h1 = H_in[(size_t)c * 3 + 1], h2 = H_in[(size_t)c * 3 + 2];
   float raw[MAXB];
 #pragma unroll
   for (int b = 0; b < MAXB; ++b) raw[b] = b < p.B ? p.qkv[(size_t)b * p.qs + c] : 0.f;
 #pragma unroll
   for (int b = 0; b < MAXB; ++b) {
     if (b >= p.B) break;
-    const float cur = raw[b];
-    // ((st0*w0 + st1*w1) + st2*w2) + cur*w3, each product and sum rounded
+    const float xin = raw[b];
+    // ((st0*w0 + st1*w1) + st2*w2) + xin*w3, each product and sum rounded
     const float x = __fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(h0, w.x), __fmul_rn(h1, w.y)), __fmul_rn(h2, w.z)),
-                              __fmul_rn(cur, w.w));
-    h0 = h1; h1 = h2; h2 = cur;
+                              __fmul_rn(xin, w.w));
+    h0 = h1; h1 = h2; h2 = xin;
     p.xc[(size_t)b * p.C + c] = silu_ref(x);
-    float *hs = p.H_slots + (size_t)((p.cur + 1 + b) % p.nslot) * p.h_floats + (size_t)c * 3;
+    float *hs = p.H_slots + (size_t)((cur + 1 + b) % p.nslot) * p.h_floats + (size_t)c * 3;
     hs[0] = h0; hs[1] = h1; hs[2] = h2;
   }
 }
@@ -119,12 +123,13 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
   const int slice = blockIdx.x % (DK / COLS);
   const int hk = hv % p.nkh;
   const int B = p.B;
+  const int cur = *p.cur;
   const int rg = lane & 15, cg = lane >> 4;
   const int i0 = rg * 8, j0 = slice * COLS + cg * 4;
 
   float4 s[8];
   {
-    const float *Sh = p.S_in + (size_t)hv * DK * DK;
+    const float *Sh = p.S_slots + (size_t)cur * p.s_floats + (size_t)hv * DK * DK;
 #pragma unroll
     for (int r = 0; r < 8; ++r) s[r] = *(const float4 *)(Sh + (size_t)(i0 + r) * DK + j0);
   }
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
       o.z = fmaf(s[r].z, qr[r], o.z); o.w = fmaf(s[r].w, qr[r], o.w);
     }
     o = (float4){sum16(o.x) * scale, sum16(o.y) * scale, sum16(o.z) * scale, sum16(o.w) * scale};
-    float *So = p.S_slots + (size_t)((p.cur + 1 + b) % p.nslot) * p.s_floats + (size_t)hv * DK * DK;
+    float *So = p.S_slots + (size_t)((cur + 1 + b) % p.nslot) * p.s_floats + (size_t)hv * DK * DK;
 #pragma unroll
     for (int r = 0; r < 8; ++r) *(float4 *)(So + (size_t)(i0 + r) * DK + j0) = s[r];
     if (rg == 0) *(float4 *)(p.ob + (size_t)b * p.nvh * DK + hv * DK + j0) = o;
@@ -215,9 +220,7 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
   p.h_floats = (size_t)g->C * 3;
   p.S_slots = g->S;
   p.H_slots = g->H;
-  p.S_in = g->S + (size_t)g->cur * p.s_floats;
-  p.H_in = g->H + (size_t)g->cur * p.h_floats;
-  p.cur = g->cur;
+  p.cur = g->dcur;
   p.nslot = g->nslot;
   p.qkv = qkv; p.qs = qs;
   p.z = z; p.zs = zs;

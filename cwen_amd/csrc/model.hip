@@ -127,7 +127,9 @@ struct AttnParams {
   const float *qn, *kn;
   float *q;            // [B][NH][HD] normed + roped queries
   float *K, *V;        // this layer's cache [ctx][NKV][HD]
-  int pbase, B, NH, NKV, npairs, nrot;
+  const int *last;     // device: last filled cache slot before the block
+  int max_ctx;         // cache slots; positions at or past it are not touched
+  int B, NH, NKV, npairs, nrot;
   float theta, eps;
   // attention
   float *po;           // partial outputs [NKV][nchunk][B*kvm][HD]
@@ -140,7 +142,8 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
   __shared__ float red[4];
   __shared__ float v[HD];
   const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-  const int pos = p.pbase + b;
+  const int pos = *p.last + 1 + b;
+  if (pos < 0 || pos >= p.max_ctx) return;   // workgroup-uniform
   const bool isq = h < p.NH;
   const int hk = h - p.NH;
   const float x = isq ? p.qfull[(size_t)b * p.qfs + (size_t)h * 2 * HD + d]
@@ -165,9 +168,12 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
   }
 }
 
-// ---- full attention, part 2: one workgroup per (key chunk, kv head) scores
-// the chunk against every query of the group (kvm heads x B positions, each
-// masked to t <= its position), then accumulates exp(s - m_chunk) * V.  The
+// ---- full attention, part 2: per (key chunk, kv head) score the chunk
+// against every query of the group (kvm heads x B positions, each masked to
+// t <= its position), then accumulate exp(s - m_chunk) * V.  A fixed grid of
+// workgroups per kv head takes chunks blockIdx.x, + gridDim.x, ... up to the
+// block's last position (the partials are per chunk, so the mapping does not
+// change the arithmetic).  The
 // chunk's K rows, then its V rows, are staged in LDS with a padded row
 // stride (KROW floats: the float4 reads of 16 consecutive rows hit distinct
 // banks).  Scores: lane = key, queries strided over 8 groups.  P.V: thread =
@@ -175,13 +181,12 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
 constexpr int KROW = HD + 4;
 __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
   extern __shared__ __align__(16) float sm[];  // Kt [TC][KROW] | Q [nq][HD] | S [nq][TC]
-  const int c = blockIdx.x, hkv = blockIdx.y;
+  const int hkv = blockIdx.y;
   const int kvm = p.NH / p.NKV;
   const int nq = p.B * kvm;
-  const int t0 = c * TC;
-  const int tlast = p.pbase + p.B - 1;       // last position of the block
-  if (t0 > tlast) return;
-  const int tn = min(TC, tlast + 1 - t0);    // keys of this chunk that exist
+  const int pbase = *p.last + 1;
+  const int tlast = min(pbase + p.B - 1, p.max_ctx - 1);  // last position of the block
+  if ((int)blockIdx.x * TC > tlast) return;
   float *Kt = sm;
   float *Q = sm + TC * KROW;
   float *S = Q + nq * HD;
@@ -192,70 +197,75 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
     const int b = qi / kvm, m = qi % kvm;
     *(float4 *)(Q + qi * HD + d4 * 4) = *(const float4 *)(p.q + ((size_t)b * p.NH + hkv * kvm + m) * HD + d4 * 4);
   }
-  for (int e = tid; e < TC * (HD / 4); e += 256) {
-    const int t = e / (HD / 4), d4 = e % (HD / 4);
-    *(float4 *)(Kt + t * KROW + d4 * 4) =
-        t < tn ? *(const float4 *)(p.K + ((size_t)(t0 + t) * p.NKV + hkv) * HD + d4 * 4) : (float4){0.f, 0.f, 0.f, 0.f};
-  }
-  __syncthreads();
-  {  // scores and chunk softmax statistics
-    const int key = tid & (TC - 1), qg = tid / TC;   // TC = 32: 8 query groups
-    const int t = t0 + key;
-    const float *kr = Kt + key * KROW;
-    for (int qi = qg; qi < nq; qi += 256 / TC) {
-      const int b = qi / kvm;
-      const float *q = Q + qi * HD;
-      float sc = -__builtin_inff();
-      if (t <= p.pbase + b && key < tn) {
-        float a = 0.f;
-        for (int d = 0; d < HD; d += 4) {
-          const float4 k4 = *(const float4 *)(kr + d), q4 = *(const float4 *)(q + d);
-          a = fmaf(q4.x, k4.x, a); a = fmaf(q4.y, k4.y, a); a = fmaf(q4.z, k4.z, a); a = fmaf(q4.w, k4.w, a);
+  for (int c = blockIdx.x; c * TC <= tlast; c += gridDim.x) {
+    const int t0 = c * TC;
+    const int tn = min(TC, tlast + 1 - t0);     // keys of this chunk that exist
+    __syncthreads();                            // previous chunk's P.V reads done
+    for (int e = tid; e < TC * (HD / 4); e += 256) {
+      const int t = e / (HD / 4), d4 = e % (HD / 4);
+      *(float4 *)(Kt + t * KROW + d4 * 4) =
+          t < tn ? *(const float4 *)(p.K + ((size_t)(t0 + t) * p.NKV + hkv) * HD + d4 * 4) : (float4){0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads();
+    {  // scores and chunk softmax statistics
+      const int key = tid & (TC - 1), qg = tid / TC;   // TC = 32: 8 query groups
+      const int t = t0 + key;
+      const float *kr = Kt + key * KROW;
+      for (int qi = qg; qi < nq; qi += 256 / TC) {
+        const int b = qi / kvm;
+        const float *q = Q + qi * HD;
+        float sc = -__builtin_inff();
+        if (t <= pbase + b && key < tn) {
+          float a = 0.f;
+          for (int d = 0; d < HD; d += 4) {
+            const float4 k4 = *(const float4 *)(kr + d), q4 = *(const float4 *)(q + d);
+            a = fmaf(q4.x, k4.x, a); a = fmaf(q4.y, k4.y, a); a = fmaf(q4.z, k4.z, a); a = fmaf(q4.w, k4.w, a);
+          }
+          sc = a * scale;
         }
-        sc = a * scale;
-      }
-      // max / sum over the 32 keys (lanes 0-31 or 32-63 of the wave)
-      float m = sc;
-      m = fmaxf(m, dpp<0xB1>(m)); m = fmaxf(m, dpp<0x4E>(m)); m = fmaxf(m, dpp<0x141>(m)); m = fmaxf(m, dpp<0x140>(m));
-      m = fmaxf(m, __shfl_xor(m, 16));
-      const float e = (sc == -__builtin_inff()) ? 0.f : expf(sc - m);
-      float l = sum16(e);
-      l += __shfl_xor(l, 16);
-      S[qi * TC + key] = e;
-      if (key == 0) {
-        const size_t pi = ((size_t)hkv * p.nchunk + c) * nq + qi;
-        p.pm[pi] = m;
-        p.pl[pi] = l;
+        // max / sum over the 32 keys (lanes 0-31 or 32-63 of the wave)
+        float m = sc;
+        m = fmaxf(m, dpp<0xB1>(m)); m = fmaxf(m, dpp<0x4E>(m)); m = fmaxf(m, dpp<0x141>(m)); m = fmaxf(m, dpp<0x140>(m));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        const float e = (sc == -__builtin_inff()) ? 0.f : expf(sc - m);
+        float l = sum16(e);
+        l += __shfl_xor(l, 16);
+        S[qi * TC + key] = e;
+        if (key == 0) {
+          const size_t pi = ((size_t)hkv * p.nchunk + c) * nq + qi;
+          p.pm[pi] = m;
+          p.pl[pi] = l;
+        }
       }
     }
-  }
-  __syncthreads();
-  for (int e = tid; e < TC * (HD / 4); e += 256) {  // V rows replace K
-    const int t = e / (HD / 4), d4 = e % (HD / 4);
-    *(float4 *)(Kt + t * KROW + d4 * 4) =
-        t < tn ? *(const float4 *)(p.V + ((size_t)(t0 + t) * p.NKV + hkv) * HD + d4 * 4) : (float4){0.f, 0.f, 0.f, 0.f};
-  }
-  __syncthreads();
-  {  // P.V: thread = head dim
-    const int d = tid;
-    for (int q0 = 0; q0 < nq; q0 += 8) {
-      const int nqq = min(8, nq - q0);
-      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int t = 0; t < TC; t += 4) {
-        const float v0 = Kt[(t + 0) * KROW + d], v1 = Kt[(t + 1) * KROW + d];
-        const float v2 = Kt[(t + 2) * KROW + d], v3 = Kt[(t + 3) * KROW + d];
+    __syncthreads();
+    for (int e = tid; e < TC * (HD / 4); e += 256) {  // V rows replace K
+      const int t = e / (HD / 4), d4 = e % (HD / 4);
+      *(float4 *)(Kt + t * KROW + d4 * 4) =
+          t < tn ? *(const float4 *)(p.V + ((size_t)(t0 + t) * p.NKV + hkv) * HD + d4 * 4) : (float4){0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads();
+    {  // P.V: thread = head dim
+      const int d = tid;
+      for (int q0 = 0; q0 < nq; q0 += 8) {
+        const int nqq = min(8, nq - q0);
+        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < TC; t += 4) {
+          const float v0 = Kt[(t + 0) * KROW + d], v1 = Kt[(t + 1) * KROW + d];
+          const float v2 = Kt[(t + 2) * KROW + d], v3 = Kt[(t + 3) * KROW + d];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            if (j >= nqq) break;
+            const float4 pr = *(const float4 *)(S + (q0 + j) * TC + t);
+            o[j] = fmaf(pr.x, v0, o[j]); o[j] = fmaf(pr.y, v1, o[j]);
+            o[j] = fmaf(pr.z, v2, o[j]); o[j] = fmaf(pr.w, v3, o[j]);
+          }
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           if (j >= nqq) break;
-          const float4 pr = *(const float4 *)(S + (q0 + j) * TC + t);
-          o[j] = fmaf(pr.x, v0, o[j]); o[j] = fmaf(pr.y, v1, o[j]);
-          o[j] = fmaf(pr.z, v2, o[j]); o[j] = fmaf(pr.w, v3, o[j]);
+          p.po[(((size_t)hkv * p.nchunk + c) * nq + q0 + j) * HD + d] = o[j];
         }
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (j >= nqq) break;
-        p.po[(((size_t)hkv * p.nchunk + c) * nq + q0 + j) * HD + d] = o[j];
       }
     }
   }
@@ -269,7 +279,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
   const int hkv = h / kvm, m = h % kvm;
   const int nq = p.B * kvm;
   const int qi = b * kvm + m;
-  const int pos = p.pbase + b;
+  const int pos = *p.last + 1 + b;
+  if (pos < 0 || pos >= p.max_ctx) return;
   const int nc = pos / TC + 1;
   float M = -__builtin_inff();
   for (int c = 0; c < nc; ++c) M = fmaxf(M, p.pm[((size_t)hkv * p.nchunk + c) * nq + qi]);
@@ -307,15 +318,31 @@ size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B) {
   return (size_t)NKV * nchunk * B * (NH / NKV) * (HD + 2);
 }
 
+// Dynamic LDS above 64 KB (B = 16 blocks) needs the attribute; set once per
+// process before any launch (not inside a graph capture).
+int attention_init() {
+  static bool done = false;
+  if (!done) {
+    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     160 * 1024));
+    done = true;
+  }
+  return CWEN_OK;
+}
+
+// Chunk workgroups per kv head: enough to cover the chip at long contexts;
+// more chunks than this are looped over.
+constexpr int ATTN_CHUNK_WGS = 128;
+
 int attention_launch(const float *qfull, int qfs, const float *kx, const float *vx, int kvs, const float *qn,
-                     const float *kn, float *qbuf, float *K, float *V, int pbase, int B, int NH, int NKV,
+                     const float *kn, float *qbuf, float *K, float *V, const int *last, int B, int NH, int NKV,
                      int npairs, int nrot, float theta, float eps, float *part, int max_ctx, _Float16 *yh,
                      hipStream_t st) {
   AttnParams p;
   p.qfull = qfull; p.qfs = qfs; p.kx = kx; p.vx = vx; p.kvs = kvs;
   p.qn = qn; p.kn = kn;
   p.q = qbuf; p.K = K; p.V = V;
-  p.pbase = pbase; p.B = B; p.NH = NH; p.NKV = NKV; p.npairs = npairs; p.nrot = nrot;
+  p.last = last; p.max_ctx = max_ctx; p.B = B; p.NH = NH; p.NKV = NKV; p.npairs = npairs; p.nrot = nrot;
   p.theta = theta; p.eps = eps;
   p.nchunk = (max_ctx + TC - 1) / TC;
   const int nq = B * (NH / NKV);
@@ -324,15 +351,11 @@ int attention_launch(const float *qfull, int qfs, const float *kx, const float *
   p.pl = p.pm + (size_t)NKV * p.nchunk * nq;
   p.yh = yh;
   hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
-  const int nc = (pbase + B - 1) / TC + 1;
+  const int nwg = p.nchunk < ATTN_CHUNK_WGS ? p.nchunk : ATTN_CHUNK_WGS;
   const size_t lds = ((size_t)TC * KROW + (size_t)nq * (TC + HD)) * sizeof(float);
-  static bool lds_set = false;  // allow the dynamic LDS of B = 16 blocks (above 64 KB)
-  if (!lds_set) {
-    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     160 * 1024));
-    lds_set = true;
-  }
-  hipLaunchKernelGGL(attn_chunk_kernel, dim3((unsigned)nc, (unsigned)NKV), dim3(256), lds, st, p);
+  int rc;
+  if ((rc = attention_init())) return rc;
+  hipLaunchKernelGGL(attn_chunk_kernel, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);
   hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)B, (unsigned)NH), dim3(HD), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;

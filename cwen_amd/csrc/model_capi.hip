@@ -47,9 +47,20 @@ struct cwen_model {
   int emb_type = -1;
   float *out_norm = nullptr;
   cwen_weight *head = nullptr;
-  int pos = -1;                  // last filled slot
+  int pos = -1;                  // last filled slot (host copy)
+  int *ctl = nullptr;            // device: [0] last filled slot, [1] GDN ring slot
+  // With CWEN_GRAPHS=1 each (mode, B) block is captured once into a graph
+  // and replayed: the launch shapes depend on (mode, B) and the weight
+  // shapes only, the position and ring slot are read from ctl on the device.
+  // Off by default: replay measured no faster than eager launches (the
+  // per-kernel cost is on the device side).
+  int use_graphs = 0;
+  hipStream_t cap = nullptr;     // capture stream
+  hipGraphExec_t gexec[3][CWEN_BMAX] = {};
+  int *htok = nullptr;           // pinned token staging [BMAX]
+  hipEvent_t tok_ev = nullptr;   // the last staging copy has been issued past this
   // device scratch
-  int *toks = nullptr, *drafts = nullptr, *res = nullptr;
+  int *toks = nullptr, *res = nullptr;
   float *X = nullptr;            // residual stream [BMAX][H]
   _Float16 *Xh = nullptr;        // normed f16 operand [BMAX][H]
   float *lin = nullptr;           // GDN layer input GEMV out [BMAX][lin_rows]
@@ -116,13 +127,24 @@ int upload_w(cwen_model *m, int type, const void *data, const void *scales, int 
   return cwen_weight_upload(m->ctx, type, data, scales, ne0, ne1, out);
 }
 
-// One verify block over tokens already in m->toks: positions pos+1..pos+B.
-// head: 0 none, 1 head + argmax/walk (drafts in m->drafts, E).
-int block(cwen_model *m, int B, int head, int E, hipStream_t st) {
+// Advance the device position and ring slot by the positions kept: n, or
+// res[0] + 1 (accepted drafts + bonus) when res is given, clamped to [1, nmax].
+__global__ void advance_kernel(int *ctl, const int *res, int n, int nmax, int nslot) {
+  if (res) n = res[0] + 1;
+  n = n < 1 ? 1 : (n > nmax ? nmax : n);
+  ctl[0] += n;
+  ctl[1] = (ctl[1] + n) % nslot;
+}
+
+enum { MODE_FWD = 0, MODE_FWD_HEAD = 1, MODE_VERIFY = 2 };
+
+// One block over the tokens in m->toks: positions ctl[0]+1 .. ctl[0]+B, then
+// the device commit.  MODE_FWD_HEAD adds the head and per-position argmax,
+// MODE_VERIFY the head and the walk over drafts toks[1..B-1] (kept = k + 1).
+int block(cwen_model *m, int B, int mode, hipStream_t st) {
   const cwen_model_cfg &c = m->cfg;
   cwen_ctx *ctx = m->ctx;
   const int H = c.d_model, I = c.d_ffn;
-  const int pbase = m->pos + 1;
   int rc;
   if ((rc = embed_launch(m->emb_qs, m->emb_sc, m->emb_type, m->toks, B, H, m->X, H, st))) return rc;
   for (int l = 0; l < c.n_layers; ++l) {
@@ -136,7 +158,6 @@ int block(cwen_model *m, int B, int head, int E, hipStream_t st) {
       if ((rc = gdn_block_launch(y.gdn, qkv, r.lin, z, r.lin, ga, gb, r.lin, y.ssm_conv, y.ssm_norm, nullptr, 0, B,
                                  st, m->gh, r.Zh, y.ssm_a, y.ssm_dt)))
         return rc;
-      y.gdn->last_B = B;
       GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
       if ((rc = gemv_launch(ctx, y.ssm_out, 1, 0, GEMV_EPI_STORE, m->gh, o5, B, st))) return rc;
     } else {
@@ -144,7 +165,7 @@ int block(cwen_model *m, int B, int head, int E, hipStream_t st) {
       GemvOut o1 = {m->att, nullptr, nullptr, r.att, 0};
       if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, m->Xh, o1, B, st))) return rc;
       if ((rc = attention_launch(m->att, r.att, m->att + r.Qo2, m->att + r.Qo2 + r.Ko, r.att, y.q_norm, y.k_norm,
-                                 m->qbuf, y.K, y.V, pbase, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
+                                 m->qbuf, y.K, y.V, m->ctl, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
                                  c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st)))
         return rc;
       GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
@@ -158,18 +179,67 @@ int block(cwen_model *m, int B, int head, int E, hipStream_t st) {
       return rc;
     (void)I;
   }
-  if (head) {
+  if (mode != MODE_FWD) {
+    const int E = mode == MODE_VERIFY ? B - 1 : 0;
     if ((rc = rmsnorm_launch(m->X, H, m->out_norm, H, c.rms_eps, nullptr, 0, m->Xh, H, B, st))) return rc;
     GemvOut o = {m->logits, nullptr, nullptr, c.vocab, 0,
-                 {ctx->amax_keys, ctx->amax_cnt, m->drafts, E, m->res}};
+                 {ctx->amax_keys, ctx->amax_cnt, m->toks + 1, E, m->res}};
     if ((rc = gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, m->Xh, o, B, st))) return rc;
   }
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->ctl, mode == MODE_VERIFY ? m->res : nullptr, B, B,
+                     CWEN_BMAX + 1);
+  CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }
 
+void drop_graphs(cwen_model *m) {
+  for (auto &row : m->gexec)
+    for (hipGraphExec_t &g : row)
+      if (g) {
+        (void)hipGraphExecDestroy(g);
+        g = nullptr;
+      }
+}
+
+// Stage the tokens, then run the block: replay its graph (captured on first
+// use) or launch eagerly.
+int run_block(cwen_model *m, const int *toks, int B, int mode, hipStream_t st) {
+  for (int b = 0; b < B; ++b)
+    if (toks[b] < 0 || toks[b] >= m->cfg.vocab) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipEventSynchronize(m->tok_ev));  // the previous staging copy has been read
+  memcpy(m->htok, toks, (size_t)B * sizeof(int));
+  CWEN_HIP_TRY(hipMemcpyAsync(m->toks, m->htok, (size_t)B * sizeof(int), hipMemcpyHostToDevice, st));
+  CWEN_HIP_TRY(hipEventRecord(m->tok_ev, st));
+  if (!m->use_graphs) return block(m, B, mode, st);
+  hipGraphExec_t &ge = m->gexec[mode][B - 1];
+  if (!ge) {
+    hipGraph_t g = nullptr;
+    CWEN_HIP_TRY(hipStreamBeginCapture(m->cap, hipStreamCaptureModeThreadLocal));
+    const int rc = block(m, B, mode, m->cap);
+    const hipError_t e = hipStreamEndCapture(m->cap, &g);
+    if (rc || e != hipSuccess) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc ? rc : CWEN_EHIP;
+    }
+    const hipError_t ei = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ei != hipSuccess) {
+      ge = nullptr;
+      return CWEN_EHIP;
+    }
+  }
+  CWEN_HIP_TRY(hipGraphLaunch(ge, st));
+  return CWEN_OK;
+}
+
+// Host copy of the commit the block made on the device.
 void commit(cwen_model *m, int n) {
   for (int l = 0; l < m->cfg.n_layers; ++l)
-    if (m->L[l].linear) cwen_gdn_commit(m->L[l].gdn, n);
+    if (m->L[l].linear) {
+      cwen_gdn *g = m->L[l].gdn;
+      g->cur = (g->cur + n) % g->nslot;
+      g->last_B = 0;
+    }
   m->pos += n;
 }
 
@@ -185,12 +255,6 @@ int ready(const cwen_model *m) {
   return 1;
 }
 
-int set_tokens(cwen_model *m, const int *toks, int B, hipStream_t st) {
-  for (int b = 0; b < B; ++b)
-    if (toks[b] < 0 || toks[b] >= m->cfg.vocab) return CWEN_EINVAL;
-  CWEN_HIP_TRY(hipMemcpyAsync(m->toks, toks, (size_t)B * sizeof(int), hipMemcpyHostToDevice, st));
-  return CWEN_OK;
-}
 
 // ---- seeded synthetic tensors generated on the device (benchmarks: the
 // random-init weights of the architecture without a host round trip).
@@ -331,13 +395,25 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
   const int H = c.d_model, I = c.d_ffn, BM = CWEN_BMAX;
   const Rows R = rows_of(c);
   const int Zh = R.Zh, Qo = R.Qo2 / 2, Ko = R.Ko;
-  rc = CWEN_OK;
+  const char *ge = getenv("CWEN_GRAPHS");
+  m->use_graphs = ge && ge[0] == '1';
+  const int ctl0[2] = {-1, 0};
+  rc = dmalloc(&m->ctl, 2) ? CWEN_ENOMEM : CWEN_OK;
+  if (!rc && (hipMemcpy(m->ctl, ctl0, sizeof(ctl0), hipMemcpyHostToDevice) != hipSuccess ||
+              hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking) != hipSuccess ||
+              hipEventCreateWithFlags(&m->tok_ev, hipEventDisableTiming) != hipSuccess))
+    rc = CWEN_EHIP;
+  if (!rc) rc = attention_init();
   for (int l = 0; l < c.n_layers && !rc; ++l) {
     Layer &y = m->L[l];
     y.linear = !is_full(c, l);
     if (y.linear) {
-      if (!(rc = cwen_gdn_create(ctx, c.gdn_nkh, c.gdn_nvh, 128, &y.gdn)))
+      if (!(rc = cwen_gdn_create(ctx, c.gdn_nkh, c.gdn_nvh, 128, &y.gdn))) {
+        (void)hipFree(y.gdn->dcur);  // every layer's ring moves with the model's slot
+        y.gdn->dcur = m->ctl + 1;
+        y.gdn->own_dcur = 0;
         rc = gemv_alloc_q4(ctx, H, R.lin, &y.lin_in);
+      }
     } else {
       const size_t kv = (size_t)c.max_ctx * Ko;
       rc = dmalloc(&y.K, kv) || dmalloc(&y.V, kv) ? CWEN_ENOMEM : CWEN_OK;
@@ -345,7 +421,7 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
     }
   }
   if (!rc)
-    rc = (dmalloc(&m->toks, BM) || dmalloc(&m->drafts, BM) || dmalloc(&m->res, 2 + BM) ||
+    rc = (dmalloc(&m->toks, BM) || dmalloc(&m->res, 2 + BM) ||
           dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->Xh, (size_t)BM * H) ||
           dmalloc(&m->lin, (size_t)BM * R.lin) || dmalloc(&m->gh, (size_t)BM * Zh) ||
           dmalloc(&m->att, (size_t)BM * R.att) || dmalloc(&m->qbuf, (size_t)BM * Qo) ||
@@ -354,7 +430,8 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
           dmalloc(&m->logits, (size_t)BM * c.vocab))
              ? CWEN_ENOMEM
              : CWEN_OK;
-  if (!rc && hipHostMalloc((void **)&m->hres, (2 + BM) * sizeof(int), hipHostMallocDefault) != hipSuccess)
+  if (!rc && (hipHostMalloc((void **)&m->hres, (2 + BM) * sizeof(int), hipHostMallocDefault) != hipSuccess ||
+              hipHostMalloc((void **)&m->htok, BM * sizeof(int), hipHostMallocDefault) != hipSuccess))
     rc = CWEN_ENOMEM;
   if (rc) {
     cwen_model_free(m);
@@ -368,6 +445,9 @@ int cwen_model_free(cwen_model *m) {
   if (!m) return CWEN_EINVAL;
   (void)hipSetDevice(m->ctx->device);
   (void)hipDeviceSynchronize();
+  drop_graphs(m);
+  if (m->cap) (void)hipStreamDestroy(m->cap);
+  if (m->tok_ev) (void)hipEventDestroy(m->tok_ev);
   for (int l = 0; m->L && l < m->cfg.n_layers; ++l) {
     Layer &y = m->L[l];
     for (float *p : {y.attn_norm, y.post_norm, y.ssm_a, y.ssm_dt, y.ssm_conv, y.ssm_norm, y.q_norm, y.k_norm, y.K,
@@ -378,13 +458,14 @@ int cwen_model_free(cwen_model *m) {
     if (y.gdn) cwen_gdn_free(y.gdn);
   }
   delete[] m->L;
-  for (void *p : {(void *)m->emb_qs, (void *)m->emb_sc, (void *)m->out_norm, (void *)m->toks, (void *)m->drafts,
+  for (void *p : {(void *)m->emb_qs, (void *)m->emb_sc, (void *)m->out_norm, (void *)m->toks, (void *)m->ctl,
                   (void *)m->res, (void *)m->X, (void *)m->Xh, (void *)m->lin, (void *)m->gh, (void *)m->att,
                   (void *)m->qbuf,
                   (void *)m->apart, (void *)m->yh, (void *)m->hh, (void *)m->logits})
     if (p) (void)hipFree(p);
   if (m->head) cwen_weight_free(m->head);
   if (m->hres) (void)hipHostFree(m->hres);
+  if (m->htok) (void)hipHostFree(m->htok);
   delete m;
   return CWEN_OK;
 }
@@ -392,6 +473,7 @@ int cwen_model_free(cwen_model *m) {
 int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data, const void *scales,
                    int ne0, int ne1) {
   if (!m || !data) return CWEN_EINVAL;
+  drop_graphs(m);  // captured launches hold the weight pointers
   const cwen_model_cfg &c = m->cfg;
   const int H = c.d_model, I = c.d_ffn;
   const int C = (2 * c.gdn_nkh + c.gdn_nvh) * 128, Zh = c.gdn_nvh * 128;
@@ -465,6 +547,7 @@ int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data,
 
 int cwen_model_synth(cwen_model *m, unsigned long long seed) {
   if (!m) return CWEN_EINVAL;
+  drop_graphs(m);
   const cwen_model_cfg &c = m->cfg;
   const int H = c.d_model, I = c.d_ffn;
   const int C = (2 * c.gdn_nkh + c.gdn_nvh) * 128, Zh = c.gdn_nvh * 128;
@@ -530,11 +613,16 @@ int cwen_model_synth(cwen_model *m, unsigned long long seed) {
 
 int cwen_model_reset(cwen_model *m) {
   if (!m) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipSetDevice(m->ctx->device));
+  CWEN_HIP_TRY(hipDeviceSynchronize());
   for (int l = 0; l < m->cfg.n_layers; ++l)
     if (m->L[l].linear) {
+      m->L[l].gdn->cur = 0;
       int rc = cwen_gdn_set_state(m->L[l].gdn, nullptr, nullptr);
       if (rc) return rc;
     }
+  const int ctl0[2] = {-1, 0};
+  CWEN_HIP_TRY(hipMemcpy(m->ctl, ctl0, sizeof(ctl0), hipMemcpyHostToDevice));
   m->pos = -1;
   return CWEN_OK;
 }
@@ -548,7 +636,7 @@ int cwen_model_forward(cwen_model *m, const int *toks, int B, int want_argmax, i
   if (m->pos + B >= m->cfg.max_ctx) return CWEN_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   int rc;
-  if ((rc = set_tokens(m, toks, B, st)) || (rc = block(m, B, want_argmax ? 1 : 0, 0, st))) return rc;
+  if ((rc = run_block(m, toks, B, want_argmax ? MODE_FWD_HEAD : MODE_FWD, st))) return rc;
   if (want_argmax) {
     CWEN_HIP_TRY(hipMemcpyAsync(m->hres, m->res, (2 + B) * sizeof(int), hipMemcpyDeviceToHost, st));
     CWEN_HIP_TRY(hipStreamSynchronize(st));
@@ -563,10 +651,7 @@ int cwen_model_verify(cwen_model *m, const int *blk, int B, int *k_out, int *bon
   if (m->pos + B >= m->cfg.max_ctx) return CWEN_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   int rc;
-  if ((rc = set_tokens(m, blk, B, st))) return rc;
-  if (B > 1) CWEN_HIP_TRY(hipMemcpyAsync(m->drafts, m->toks + 1, (size_t)(B - 1) * sizeof(int),
-                                         hipMemcpyDeviceToDevice, st));
-  if ((rc = block(m, B, 1, B - 1, st))) return rc;
+  if ((rc = run_block(m, blk, B, MODE_VERIFY, st))) return rc;
   CWEN_HIP_TRY(hipMemcpyAsync(m->hres, m->res, 2 * sizeof(int), hipMemcpyDeviceToHost, st));
   CWEN_HIP_TRY(hipStreamSynchronize(st));
   const int k = m->hres[0];

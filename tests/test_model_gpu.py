@@ -123,3 +123,30 @@ def test_spec_decode_equals_serial(env, n_key):
     assert st.cycles <= n_gen
     if n_key <= 4:
         assert st.drafted > 0
+
+
+def test_graph_replay_equals_eager(env, monkeypatch):
+    """CWEN_GRAPHS=1: each (mode, B) block is captured once and replayed at
+    later positions (position and ring slot read on the device).  Replays
+    give the eager model's logits and token stream bit for bit."""
+    gpu, ctx, m, tensors = env
+    monkeypatch.setenv("CWEN_GRAPHS", "1")
+    mg = gpu.Model(ctx, **CFG)
+    monkeypatch.delenv("CWEN_GRAPHS")
+    for t in tensors:
+        mg.set(*t)
+    toks = synth.prompt_tokens(6, 30, CFG["vocab"])
+    for model in (m, mg):
+        model.reset()
+    for b0, B in ((0, 5), (5, 5), (10, 5), (15, 1), (16, 1), (17, 8)):   # replays of B = 5 and B = 1
+        a = m.forward(toks[b0:b0 + B])
+        la = m.logits(B)
+        b = mg.forward(toks[b0:b0 + B])
+        assert np.array_equal(a, b), b0
+        assert np.array_equal(la, mg.logits(B)), b0
+    prompt = synth.prompt_tokens(5, 64, CFG["vocab"], period=13, noise=0.05)
+    serial = m.generate_serial(prompt, 60)
+    spec, st = mg.generate_spec(prompt, 60, n_key=2)
+    assert np.array_equal(spec, serial)
+    assert st.drafted > 0
+    mg.free()
