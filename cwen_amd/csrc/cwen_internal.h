@@ -83,6 +83,28 @@ __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t voff,
   return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
 
+// Cross-lane sums on DPP row permutes (no LDS round trip).  The reduction
+// tree is fixed, so a sum is bit-reproducible.
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over each aligned row of 16 lanes: quad xor 1, quad xor 2, half-row
+// mirror, row mirror.
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  return v + dpp<0x140>(v);
+}
+// Sum over the wave (wave-uniform result).
+__device__ __forceinline__ float sum64(float v) {
+  const int b = __builtin_bit_cast(int, sum16(v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+}
+
 // run.c:378-384 silu_one: x * (1 / (1 + exp(-x)))
 __device__ __forceinline__ float silu_f(float x) { return x * (1.f / (1.f + expf(-x))); }
 
@@ -102,6 +124,17 @@ struct GemvOut {
   int ys;
   int accumulate;    // y += result
   ArgmaxOut am;      // ARGMAX only
+  float *ssq;        // STORE: per row tile, the sum of squares of the final y per column [row tile][CWEN_BMAX]
+};
+// Normalised f32 input: the GEMV's activations are RMSNorm(x) with weight w,
+// applied while staging; the sum of squares per column comes from the
+// producer's ssq partials (npart of them).
+struct GemvNorm {
+  const float *x;    // [B][K]
+  const float *w;    // [K]
+  const float *ssq;  // [npart][CWEN_BMAX]
+  int npart;
+  float eps;
 };
 int gemv_fmt_of(int type);
 size_t gemv_st_bytes(int fmt);
@@ -116,8 +149,10 @@ int gemv_alloc_q4(cwen_ctx *ctx, int K, int M, cwen_weight **out);
 int gemv_upload_part(cwen_weight *w, int type, const void *data, const void *scales, int M, int row_off,
                      int side_sel);
 void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w);
+// Row tiles of a launch over w: the number of ssq partials it writes.
+int gemv_row_tiles(const cwen_weight *w);
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
-                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st);
+                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvNorm *nrm = nullptr);
 int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st);
 int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &a, hipStream_t st);
 
@@ -128,10 +163,9 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
                      const float *A = nullptr, const float *dt = nullptr);
 
 // ------------------------------------------------------------ model.hip
+// Also writes each row's sum of squares to ssq[b] (one partial per column).
 int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *toks, int B, int H, float *X,
-                 int xs, hipStream_t st);
-int rmsnorm_launch(const float *X, int xs, const float *w, int n, float eps, float *Y, int ys, _Float16 *Yh,
-                   int yhs, int B, hipStream_t st);
+                 int xs, float *ssq, hipStream_t st);
 size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B);
 int attention_init();
 // `last` is a device int: the last filled cache slot before the block (the

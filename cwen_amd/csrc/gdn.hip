@@ -42,27 +42,6 @@ constexpr int COLS = 16;            // columns of a head per recurrence workgrou
 
 __device__ __forceinline__ float silu_ref(float x) { return x * (1.f / (1.f + expf(-x))); }
 
-// Cross-lane sums on DPP row permutes (no LDS round trip).
-template <int CTRL> __device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-// Sum over each aligned row of 16 lanes: quad xor 1, quad xor 2, half-row
-// mirror, row mirror.
-__device__ __forceinline__ float sum16(float v) {
-  v += dpp<0xB1>(v);
-  v += dpp<0x4E>(v);
-  v += dpp<0x141>(v);
-  return v + dpp<0x140>(v);
-}
-// Sum over the wave (wave-uniform result).
-__device__ __forceinline__ float sum64(float v) {
-  const int b = __builtin_bit_cast(int, sum16(v));
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
-         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16)) +
-         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
-         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
-}
-
 // Slot ring: the state before the block is slot *cur; the state after
 // position b is written to slot (*cur + 1 + b) % nslot.  The slot is read on
 // the device, so a captured launch replays at any ring position.

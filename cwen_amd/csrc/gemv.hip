@@ -233,17 +233,38 @@ struct GemvParams {
   int M, nrg, nst;
   int S, rps;          // K split across workgroups, super-tiles (rounds) per split
   const _Float16 *xh;  // activations f16 [B][K]
-  uint32_t xbytes;     // B*K*2 (buffer range: columns >= B read as zero)
+  uint32_t xbytes;     // B*K*2, or B*K*4 for XN (buffer range: columns >= B read as zero)
+  // XN: the activations are RMSNorm(xf) applied while staging,
+  // f16((nw[k] * x[k]) * s_c), s_c = 1 / sqrt(sum_p ssq[p][c] / K + eps).
+  const float *xf;     // f32 rows [B][K]
+  const float *nw;     // norm weight [K]
+  const float *ssq;    // per-row-tile partial sums of squares [npart][CWEN_BMAX]
+  int npart;           // 1..64
+  float eps;
   int K, B;
   float *part;         // split-K partials
   int *cnt;            // per row-tile arrival counters (zero between launches)
   GemvOut out;
 };
 
+// 8 f32 activations x and norm weights w -> 8 f16 (w * x) * s (the RMSNorm
+// of run.c:346-368 rmsnorm, rounded to the f16 operand).
+__device__ __forceinline__ uint4 norm8(const uint4 (&x)[2], const float4 *w, float s) {
+  const float4 x0 = __builtin_bit_cast(float4, x[0]), x1 = __builtin_bit_cast(float4, x[1]);
+  const float4 w0 = w[0], w1 = w[1];
+  const half2_t h0 = {(_Float16)(w0.x * x0.x * s), (_Float16)(w0.y * x0.y * s)};
+  const half2_t h1 = {(_Float16)(w0.z * x0.z * s), (_Float16)(w0.w * x0.w * s)};
+  const half2_t h2 = {(_Float16)(w1.x * x1.x * s), (_Float16)(w1.y * x1.y * s)};
+  const half2_t h3 = {(_Float16)(w1.z * x1.z * s), (_Float16)(w1.w * x1.w * s)};
+  return make_uint4(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
+                    __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3));
+}
+
 // FMT: weight format.  NS: sides per row group (2 = both halves of an
 // interleaved pair).  R: row groups per wave; each wave carries R*NS weight
 // streams.  EPI: epilogue.  CB: activation columns staged (4, 8 or 16; >= B).
-template <int FMT, int NS, int R, int EPI, int CB>
+// XN: f32 activations normalised while staging (GemvParams::xf).
+template <int FMT, int NS, int R, int EPI, int CB, bool XN>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   using F = Fmt<FMT>;
   constexpr int NSET = NS * R;
@@ -264,7 +285,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   const int nround = min(p.nst - st0, p.rps);
 
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.wbytes);
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.xh, p.xbytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(XN ? (const void *)p.xf : (const void *)p.xh, p.xbytes);
+  const __amdgpu_buffer_rsrc_t nwr = make_rsrc(p.nw, XN ? (uint32_t)p.K * 4u : 0u);
 
   // Weight streams of this wave: set q = r*NS + s is row group rgs[r], side s.
   const uint32_t sstride = (uint32_t)p.nsw * F::ST_BYTES;
@@ -281,23 +303,31 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   const uint32_t lq = lane * 16, ls = F::SC_OFS + lane * 8;
 
   // Activation staging: this wave copies columns c = wave + WAVES*i; lane
-  // copies 16-byte unit `lane` of the column's 512-K chunk.
-  const uint32_t xround = Q4_ST_K * 2;
+  // copies f16 unit `lane` (K elements 8*lane .. 8*lane+7) of the column's
+  // 512-K chunk.
+  constexpr uint32_t XE = XN ? 4 : 2;        // bytes per activation in memory
+  const uint32_t xround = Q4_ST_K * XE;
   uint32_t xofs[XL];
   int xslot[XL];
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
     const int c = wave + WAVES * i;
-    xofs[i] = (uint32_t)c * (uint32_t)p.K * 2 + (uint32_t)st0 * xround + lane * 16;  // per lane: range-checked
+    xofs[i] = (uint32_t)c * (uint32_t)p.K * XE + (uint32_t)st0 * xround + lane * 8 * XE;  // range-checked
     xslot[i] = c * 64 + (lane ^ c);
   }
+  // XN: the norm weights of a round (512 floats) pass through LDS, two
+  // rounds ahead: thread t loads floats 2t, 2t+1 of round r + 2 during round
+  // r and stores them into nwl[r % 2] at its end.
+  __shared__ float2 nwl[XN ? 2 : 1][XN ? 64 * WAVES : 1];
+  const uint32_t nofs = (uint32_t)st0 * xround + tid * 8;
 
   // Loads of one round's weight data.  Tile u, vector v of a stream.
   auto tile_ofs = [&](int u, int v) -> uint32_t {
     return FMT == GEMV_Q8 ? lq + u * 2048 + v * 1024 : lq + u * 1024;
   };
 
-  uint4 xs[XL];
+  uint4 xs[XL][XN ? 2 : 1];
+  uint2 nv = {0u, 0u};        // XN: this thread's norm weights of the round two ahead
   uint4 wq[TILES][NSET][TV];
   uint2 sc[NSET];
   uint32_t dq[NSET];          // Q6_K: f16 d of the round's two super-blocks
@@ -307,8 +337,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     sc[q] = bload8(wr, ls, wofs[q]);
     if constexpr (FMT == GEMV_Q6K) dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q], 0);
   }
+  auto stage_load = [&](uint32_t soff) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < XL; ++i) xs[i] = bload16(xr, xofs[i]);
+    for (int i = 0; i < XL; ++i) {
+      xs[i][0] = bload16(xr, xofs[i], soff);
+      if constexpr (XN) xs[i][1] = bload16(xr, xofs[i] + 16, soff);
+    }
+  };
+  stage_load(0);
+  if constexpr (XN) {
+    nwl[0][tid] = __builtin_bit_cast(float2, bload8(nwr, nofs, 0));
+    nwl[1][tid] = __builtin_bit_cast(float2, bload8(nwr, nofs, nround > 1 ? xround : 0u));
+  }
 #pragma unroll
   for (int j = 0; j < TILES; ++j) {
 #pragma unroll
@@ -323,8 +363,30 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);  // issue the ring in slot order
   }
+  // XN: column scales from the producer's partial sums of squares, summed
+  // in a fixed order (lane p holds partial p), so every workgroup and every
+  // block size gets the same scale for a column.
+  float scl[XL];
 #pragma unroll
-  for (int i = 0; i < XL; ++i) act[0][xslot[i]] = xs[i];
+  for (int i = 0; i < XL; ++i) {
+    scl[i] = 0.f;
+    if constexpr (XN) {
+      const int c = wave + WAVES * i;
+      const float v = (lane < p.npart && c < p.B) ? p.ssq[lane * CWEN_BMAX + c] : 0.f;
+      const float ss = sum64(v);
+      const float sc1 = c < p.B ? 1.f / sqrtf(ss / (float)p.K + p.eps) : 0.f;
+      scl[i] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc1)));  // uniform
+    }
+  }
+  auto stage_store = [&](uint4 *buf, int nb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      if constexpr (XN) buf[xslot[i]] = norm8(xs[i], (const float4 *)&nwl[nb][0] + 2 * lane, scl[i]);
+      else buf[xslot[i]] = xs[i][0];
+    }
+  };
+  if constexpr (XN) lds_barrier();  // nwl[0], nwl[1] written
+  stage_store(act[0], 0);
   lds_barrier();
 
   const Unpack uc = unpack_consts();
@@ -372,8 +434,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       if constexpr (FMT == GEMV_Q6K)
         dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q] + nr * sstride, 0);
     }
-#pragma unroll
-    for (int i = 0; i < XL; ++i) xs[i] = bload16(xr, xofs[i], nr * xround);
+    stage_load(nr * xround);
+    if constexpr (XN) nv = bload8(nwr, nofs, (uint32_t)(rd + 2 < nround ? rd + 2 : nround - 1) * xround);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < TILES; ++j) {
@@ -423,8 +485,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
           acc[q][m & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b[q][m], acc[q][m & 1], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);  // keep slots in issue order
     }
-#pragma unroll
-    for (int i = 0; i < XL; ++i) act[cur ^ 1][xslot[i]] = xs[i];
+    stage_store(act[cur ^ 1], cur ^ 1);
+    if constexpr (XN) nwl[cur][tid] = __builtin_bit_cast(float2, nv);
     lds_barrier();
   };
   int rd = 0;
@@ -537,6 +599,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     return;
   }
 
+  float sq[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of the row tile's sum of squares
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = rgs[r] * Q4_ROWS + n;
@@ -564,6 +627,26 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       if (o.y) o.y[(size_t)c * o.ys + row] = v[e];
       if (o.yh) o.yh[(size_t)c * p.M + row] = (_Float16)v[e];
       if (EPI == GEMV_EPI_PAIR) o.y1[(size_t)c * o.ys + row] = res[r * NS + NS - 1][e];
+      sq[e] = fmaf(v[e], v[e], sq[e]);
+    }
+  }
+  if (o.ssq) {
+    // Sum of squares of this row tile's outputs per column, in a fixed order
+    // (rows of a wave by the DPP tree, then waves in order): ssq[rt][c], the
+    // partials a normalising consumer sums.
+    __shared__ float s_sq[WAVES][16];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sq[e] = sum16(sq[e]);
+    if (n == 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s_sq[wave][g * 4 + e] = sq[e];
+    }
+    __syncthreads();
+    if (tid < 16 && tid < p.B) {
+      float t = s_sq[0][tid];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) t += s_sq[w][tid];
+      o.ssq[rt * CWEN_BMAX + tid] = t;
     }
   }
 }
@@ -768,17 +851,23 @@ __global__ __launch_bounds__(256) void argmax_walk_kernel(const float *lg, long 
   argmax_finish(s_col, B, a, tid, &s_flag);
 }
 
-template <int FMT, int NS, int R, int EPI, int CB>
+template <int FMT, int NS, int R, int EPI, int CB, bool XN>
 void launch_one(const GemvParams &p, int nrt, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_kernel<FMT, NS, R, EPI, CB>), dim3((unsigned)(nrt * p.S)), dim3(64 * WAVES), 0,
+  hipLaunchKernelGGL((gemv_kernel<FMT, NS, R, EPI, CB, XN>), dim3((unsigned)(nrt * p.S)), dim3(64 * WAVES), 0,
                      st, p);
+}
+
+template <int FMT, int NS, int R, int EPI, bool XN>
+void launch_xn(const GemvParams &p, int nrt, hipStream_t st) {
+  if (p.B <= 4) launch_one<FMT, NS, R, EPI, 4, XN>(p, nrt, st);
+  else if (p.B <= 8) launch_one<FMT, NS, R, EPI, 8, XN>(p, nrt, st);
+  else launch_one<FMT, NS, R, EPI, 16, XN>(p, nrt, st);
 }
 
 template <int FMT, int NS, int R, int EPI>
 void launch_cb(const GemvParams &p, int nrt, hipStream_t st) {
-  if (p.B <= 4) launch_one<FMT, NS, R, EPI, 4>(p, nrt, st);
-  else if (p.B <= 8) launch_one<FMT, NS, R, EPI, 8>(p, nrt, st);
-  else launch_one<FMT, NS, R, EPI, 16>(p, nrt, st);
+  if (p.xf) launch_xn<FMT, NS, R, EPI, true>(p, nrt, st);
+  else launch_xn<FMT, NS, R, EPI, false>(p, nrt, st);
 }
 
 template <int FMT>
@@ -859,8 +948,12 @@ void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
   w->split = (nrd + rps - 1) / rps;
 }
 
+int gemv_row_tiles(const cwen_weight *w) { return (w->nrg + WAVES * w->rows - 1) / (WAVES * w->rows); }
+
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
-                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st) {
+                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvNorm *nrm) {
+  if (nrm && (xh || !nrm->x || !nrm->w || !nrm->ssq || nrm->npart < 1 || nrm->npart > 64)) return CWEN_EINVAL;
+  if (out.ssq && (epi != GEMV_EPI_STORE || gemv_row_tiles(w) > 64)) return CWEN_EINVAL;
   GemvParams p;
   p.w = w->dev;
   p.wbytes = (uint32_t)w->bytes;
@@ -872,7 +965,12 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   p.S = w->split;
   p.rps = w->rps;
   p.xh = xh;
-  p.xbytes = (uint32_t)((size_t)B * w->ne0 * 2);
+  p.xbytes = (uint32_t)((size_t)B * w->ne0 * (nrm ? 4 : 2));
+  p.xf = nrm ? nrm->x : nullptr;
+  p.nw = nrm ? nrm->w : nullptr;
+  p.ssq = nrm ? nrm->ssq : nullptr;
+  p.npart = nrm ? nrm->npart : 0;
+  p.eps = nrm ? nrm->eps : 0.f;
   p.K = w->ne0;
   p.B = B;
   p.part = ctx->partials;

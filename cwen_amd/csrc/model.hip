@@ -16,22 +16,6 @@ namespace {
 constexpr int HD = 128 * 2;          // full-attention head dim
 constexpr int TC = 32;               // keys per attention chunk
 
-template <int CTRL> __device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float sum16(float v) {
-  v += dpp<0xB1>(v);
-  v += dpp<0x4E>(v);
-  v += dpp<0x141>(v);
-  return v + dpp<0x140>(v);
-}
-__device__ __forceinline__ float sum64(float v) {
-  const int b = __builtin_bit_cast(int, sum16(v));
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
-         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16)) +
-         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
-         __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
-}
 __device__ __forceinline__ float max64(float v) {
   auto mx = [](float a, float b) { return a > b ? a : b; };
   v = mx(v, dpp<0xB1>(v));
@@ -59,10 +43,12 @@ __device__ __forceinline__ float f16f(uint16_t h) { return (float)__builtin_bit_
 // ---- embedding: Q4_0 (GGUF blocks) or Q4_0RS (split scales) rows, exact
 // f32 dequant w = (n - 8) * d.  Grid: B, 256 threads, thread = block.
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uint16_t *sc, int type,
-                                                    const int *toks, int H, float *X, int xs) {
+                                                    const int *toks, int H, float *X, int xs, float *ssq) {
+  __shared__ float red[4];
   const int b = blockIdx.x;
   const size_t tok = (size_t)toks[b];
   const int nb = H / 32;
+  float sq = 0.f;
   for (int i = threadIdx.x; i < nb; i += 256) {
     const uint8_t *q;
     float d;
@@ -76,46 +62,16 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uin
     }
     float *dst = X + (size_t)b * xs + i * 32;
     for (int j = 0; j < 16; ++j) {
-      dst[j] = (float)((int)(q[j] & 0xF) - 8) * d;
-      dst[j + 16] = (float)((int)(q[j] >> 4) - 8) * d;
+      const float lo = (float)((int)(q[j] & 0xF) - 8) * d, hi = (float)((int)(q[j] >> 4) - 8) * d;
+      dst[j] = lo;
+      dst[j + 16] = hi;
+      sq = fmaf(lo, lo, sq);
+      sq = fmaf(hi, hi, sq);
     }
   }
-}
-
-// ---- RMSNorm of B rows: y = w * x * (1/sqrt(mean(x^2) + eps)), f32 and/or
-// f16 out.  Grid: B, 256 threads; a thread owns float4 groups tid, tid+256,
-// ... (n <= 8192, n % 4 == 0), all loaded before the first use.
-constexpr int RMS_MAXV = 8;
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *X, int xs, const float *w, int n, float eps,
-                                                      float *Y, int ys, _Float16 *Yh, int yhs) {
-  __shared__ float red[4];
-  const int b = blockIdx.x;
-  const float *x = X + (size_t)b * xs;
-  float4 v[RMS_MAXV];
-#pragma unroll
-  for (int j = 0; j < RMS_MAXV; ++j) {
-    const int i = (j * 256 + threadIdx.x) * 4;
-    v[j] = i < n ? *(const float4 *)(x + i) : (float4){0.f, 0.f, 0.f, 0.f};
-  }
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < RMS_MAXV; ++j) {
-    ss = fmaf(v[j].x, v[j].x, ss); ss = fmaf(v[j].y, v[j].y, ss);
-    ss = fmaf(v[j].z, v[j].z, ss); ss = fmaf(v[j].w, v[j].w, ss);
-  }
-  const float s = 1.f / sqrtf(sum256(ss, red) / (float)n + eps);
-#pragma unroll
-  for (int j = 0; j < RMS_MAXV; ++j) {
-    const int i = (j * 256 + threadIdx.x) * 4;
-    if (i >= n) break;
-    const float4 wv = *(const float4 *)(w + i);
-    const float4 y = {wv.x * v[j].x * s, wv.y * v[j].y * s, wv.z * v[j].z * s, wv.w * v[j].w * s};
-    if (Y) *(float4 *)(Y + (size_t)b * ys + i) = y;
-    if (Yh) {
-      const half2_t a = {(_Float16)y.x, (_Float16)y.y}, c = {(_Float16)y.z, (_Float16)y.w};
-      *(uint2 *)(Yh + (size_t)b * yhs + i) = make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, c));
-    }
-  }
+  // The row's sum of squares: the one partial a normalising GEMV reads.
+  const float t = sum256(sq, red);
+  if (threadIdx.x == 0) ssq[b] = t;
 }
 
 // ---- full attention, part 1: per (position, head) q/k RMSNorm (one shared
@@ -299,16 +255,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
 }  // namespace
 
 int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *toks, int B, int H, float *X,
-                 int xs, hipStream_t st) {
-  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)B), dim3(256), 0, st, qs, sc, type, toks, H, X, xs);
-  CWEN_HIP_TRY(hipGetLastError());
-  return CWEN_OK;
-}
-
-int rmsnorm_launch(const float *X, int xs, const float *w, int n, float eps, float *Y, int ys, _Float16 *Yh,
-                   int yhs, int B, hipStream_t st) {
-  if (n % 4 || n > RMS_MAXV * 1024 || xs % 4 || (Y && ys % 4) || (Yh && yhs % 4)) return CWEN_EINVAL;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)B), dim3(256), 0, st, X, xs, w, n, eps, Y, ys, Yh, yhs);
+                 int xs, float *ssq, hipStream_t st) {
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)B), dim3(256), 0, st, qs, sc, type, toks, H, X, xs, ssq);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }

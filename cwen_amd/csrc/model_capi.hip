@@ -62,7 +62,7 @@ struct cwen_model {
   // device scratch
   int *toks = nullptr, *res = nullptr;
   float *X = nullptr;            // residual stream [BMAX][H]
-  _Float16 *Xh = nullptr;        // normed f16 operand [BMAX][H]
+  float *ssq = nullptr;          // partial sums of squares of X [64][BMAX]
   float *lin = nullptr;           // GDN layer input GEMV out [BMAX][lin_rows]
   _Float16 *gh = nullptr;        // GDN output f16 [BMAX][nvh*dk]
   float *att = nullptr;           // attention input GEMV out [BMAX][att_rows]
@@ -102,6 +102,7 @@ Rows rows_of(const cwen_model_cfg &c) {
 int check_cfg(const cwen_model_cfg *c) {
   if (!c || c->n_layers <= 0 || c->d_model <= 0 || c->d_ffn <= 0 || c->vocab <= 0) return CWEN_EINVAL;
   if (c->d_model % Q4_K_ALIGN || c->d_ffn % Q4_K_ALIGN) return CWEN_EINVAL;
+  if (c->d_model > 8192) return CWEN_EINVAL;  // <= 64 row-tile partials of the residual's sum of squares
   if (c->head_dim != 256 || c->n_head <= 0 || c->n_kv_head <= 0 || c->n_head % c->n_kv_head) return CWEN_EINVAL;
   if ((c->n_head * c->head_dim) % Q4_K_ALIGN) return CWEN_EINVAL;
   if (c->gdn_dk != 128 || c->gdn_nkh <= 0 || c->gdn_nvh % c->gdn_nkh || (c->gdn_nvh * 128) % Q4_K_ALIGN)
@@ -146,45 +147,56 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
   cwen_ctx *ctx = m->ctx;
   const int H = c.d_model, I = c.d_ffn;
   int rc;
-  if ((rc = embed_launch(m->emb_qs, m->emb_sc, m->emb_type, m->toks, B, H, m->X, H, st))) return rc;
+  // The residual stream X is normalised inside the GEMVs that read it: each
+  // producer of X (embed, the accumulating GEMVs) leaves per-row-tile sums
+  // of squares in m->ssq, `npart` of them, for the next consumer.
+  if ((rc = embed_launch(m->emb_qs, m->emb_sc, m->emb_type, m->toks, B, H, m->X, H, m->ssq, st))) return rc;
+  int npart = 1;
   for (int l = 0; l < c.n_layers; ++l) {
     Layer &y = m->L[l];
-    if ((rc = rmsnorm_launch(m->X, H, y.attn_norm, H, c.rms_eps, nullptr, 0, m->Xh, H, B, st))) return rc;
+    const GemvNorm n1 = {m->X, y.attn_norm, m->ssq, npart, c.rms_eps};
+    const cwen_weight *wout;
     if (y.linear) {
       const Rows r = rows_of(c);
       GemvOut o1 = {m->lin, nullptr, nullptr, r.lin, 0};
-      if ((rc = gemv_launch(ctx, y.lin_in, 1, 0, GEMV_EPI_STORE, m->Xh, o1, B, st))) return rc;
+      if ((rc = gemv_launch(ctx, y.lin_in, 1, 0, GEMV_EPI_STORE, nullptr, o1, B, st, &n1))) return rc;
       const float *qkv = m->lin, *z = m->lin + r.C, *ga = m->lin + r.o_alpha, *gb = m->lin + r.o_beta;
       if ((rc = gdn_block_launch(y.gdn, qkv, r.lin, z, r.lin, ga, gb, r.lin, y.ssm_conv, y.ssm_norm, nullptr, 0, B,
                                  st, m->gh, r.Zh, y.ssm_a, y.ssm_dt)))
         return rc;
       GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
+      o5.ssq = m->ssq;
       if ((rc = gemv_launch(ctx, y.ssm_out, 1, 0, GEMV_EPI_STORE, m->gh, o5, B, st))) return rc;
+      wout = y.ssm_out;
     } else {
       const Rows r = rows_of(c);
       GemvOut o1 = {m->att, nullptr, nullptr, r.att, 0};
-      if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, m->Xh, o1, B, st))) return rc;
+      if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, nullptr, o1, B, st, &n1))) return rc;
       if ((rc = attention_launch(m->att, r.att, m->att + r.Qo2, m->att + r.Qo2 + r.Ko, r.att, y.q_norm, y.k_norm,
                                  m->qbuf, y.K, y.V, m->ctl, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
                                  c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st)))
         return rc;
       GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
+      o5.ssq = m->ssq;
       if ((rc = gemv_launch(ctx, y.wo, 1, 0, GEMV_EPI_STORE, m->yh, o5, B, st))) return rc;
+      wout = y.wo;
     }
-    if ((rc = rmsnorm_launch(m->X, H, y.post_norm, H, c.rms_eps, nullptr, 0, m->Xh, H, B, st))) return rc;
+    const GemvNorm n2 = {m->X, y.post_norm, m->ssq, gemv_row_tiles(wout), c.rms_eps};
     GemvOut f1 = {nullptr, nullptr, m->hh, 0, 0};
     GemvOut f2 = {m->X, nullptr, nullptr, H, 1};
-    if ((rc = gemv_launch(ctx, y.ffn_gu, 2, 0, GEMV_EPI_SWIGLU, m->Xh, f1, B, st)) ||
+    f2.ssq = m->ssq;
+    if ((rc = gemv_launch(ctx, y.ffn_gu, 2, 0, GEMV_EPI_SWIGLU, nullptr, f1, B, st, &n2)) ||
         (rc = gemv_launch(ctx, y.ffn_down, 1, 0, GEMV_EPI_STORE, m->hh, f2, B, st)))
       return rc;
+    npart = gemv_row_tiles(y.ffn_down);
     (void)I;
   }
   if (mode != MODE_FWD) {
     const int E = mode == MODE_VERIFY ? B - 1 : 0;
-    if ((rc = rmsnorm_launch(m->X, H, m->out_norm, H, c.rms_eps, nullptr, 0, m->Xh, H, B, st))) return rc;
+    const GemvNorm nh = {m->X, m->out_norm, m->ssq, npart, c.rms_eps};
     GemvOut o = {m->logits, nullptr, nullptr, c.vocab, 0,
                  {ctx->amax_keys, ctx->amax_cnt, m->toks + 1, E, m->res}};
-    if ((rc = gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, m->Xh, o, B, st))) return rc;
+    if ((rc = gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, nullptr, o, B, st, &nh))) return rc;
   }
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->ctl, mode == MODE_VERIFY ? m->res : nullptr, B, B,
                      CWEN_BMAX + 1);
@@ -422,7 +434,7 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
   }
   if (!rc)
     rc = (dmalloc(&m->toks, BM) || dmalloc(&m->res, 2 + BM) ||
-          dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->Xh, (size_t)BM * H) ||
+          dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->ssq, (size_t)64 * BM) ||
           dmalloc(&m->lin, (size_t)BM * R.lin) || dmalloc(&m->gh, (size_t)BM * Zh) ||
           dmalloc(&m->att, (size_t)BM * R.att) || dmalloc(&m->qbuf, (size_t)BM * Qo) ||
           dmalloc(&m->apart, attn_partial_floats(c.n_head, c.n_kv_head, c.max_ctx, BM)) ||
@@ -459,7 +471,7 @@ int cwen_model_free(cwen_model *m) {
   }
   delete[] m->L;
   for (void *p : {(void *)m->emb_qs, (void *)m->emb_sc, (void *)m->out_norm, (void *)m->toks, (void *)m->ctl,
-                  (void *)m->res, (void *)m->X, (void *)m->Xh, (void *)m->lin, (void *)m->gh, (void *)m->att,
+                  (void *)m->res, (void *)m->X, (void *)m->ssq, (void *)m->lin, (void *)m->gh, (void *)m->att,
                   (void *)m->qbuf,
                   (void *)m->apart, (void *)m->yh, (void *)m->hh, (void *)m->logits})
     if (p) (void)hipFree(p);
