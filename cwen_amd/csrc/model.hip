@@ -124,103 +124,147 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
   }
 }
 
-// ---- full attention, part 2: per (key chunk, kv head) score the chunk
-// against every query of the group (kvm heads x B positions, each masked to
-// t <= its position), then accumulate exp(s - m_chunk) * V.  A fixed grid of
-// workgroups per kv head takes chunks blockIdx.x, + gridDim.x, ... up to the
-// block's last position (the partials are per chunk, so the mapping does not
-// change the arithmetic).  The
-// chunk's K rows, then its V rows, are staged in LDS with a padded row
-// stride (KROW floats: the float4 reads of 16 consecutive rows hit distinct
-// banks).  Scores: lane = key, queries strided over 8 groups.  P.V: thread =
-// head dim, 8 queries at a time.
-constexpr int KROW = HD + 4;
+// ---- full attention, part 2: per (key chunk, kv head), the kvm x B queries
+// of the group (each masked to keys t <= its position) against the chunk's
+// TC keys on f32 matrix cores (v_mfma_f32_16x16x4f32):
+//   S[q][t] = (Q[q] . K[t]) / sqrt(HD);  P[q][t] = exp(S - m_q), m_q = max_t S,
+//   l_q = sum_t P;  O[q] = sum_t P[q][t] V[t]   -> partials po, pm, pl.
+// In a product's k-th step lane group g (lanes 16g..16g+15) supplies
+// element g*run + k of the reduction dimension, so a lane reads 4 steps with
+// one 16-byte LDS read; the summation order is fixed and the same for every
+// query row, whatever B is.  Scores: one wave per 16-query tile (both 16-key
+// halves, so the chunk softmax stays in the wave).  P.V: V is staged
+// transposed; wave w takes head-dim tiles 4w..4w+3 of every query tile.  A
+// fixed grid of workgroups per kv head takes chunks blockIdx.x, + gridDim.x,
+// ... up to the block's last position (the partials are per chunk, so the
+// mapping does not change the arithmetic).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int QROW = HD + 4, KROW = HD + 4, VROW = TC + 4, PROW = TC + 4;
+constexpr int KV_FLOATS = TC * KROW > HD * VROW ? TC * KROW : HD * VROW;
+
+__device__ __forceinline__ float max16(float m) {
+  m = fmaxf(m, dpp<0xB1>(m)); m = fmaxf(m, dpp<0x4E>(m));
+  m = fmaxf(m, dpp<0x141>(m)); return fmaxf(m, dpp<0x140>(m));
+}
+
 __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
-  extern __shared__ __align__(16) float sm[];  // Kt [TC][KROW] | Q [nq][HD] | S [nq][TC]
+  extern __shared__ __align__(16) float sm[];
   const int hkv = blockIdx.y;
   const int kvm = p.NH / p.NKV;
   const int nq = p.B * kvm;
+  const int MT = (nq + 15) / 16;               // 16-query tiles
   const int pbase = *p.last + 1;
   const int tlast = min(pbase + p.B - 1, p.max_ctx - 1);  // last position of the block
   if ((int)blockIdx.x * TC > tlast) return;
-  float *Kt = sm;
-  float *Q = sm + TC * KROW;
-  float *S = Q + nq * HD;
-  const int tid = threadIdx.x;
+  float *Qs = sm;                              // [MT*16][QROW], rows >= nq zero
+  float *KV = Qs + MT * 16 * QROW;             // K [TC][KROW], then V^T [HD][VROW]
+  float *Ps = KV + KV_FLOATS;                  // [MT*16][PROW]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
   const float scale = 1.f / sqrtf((float)HD);
-  for (int e = tid; e < nq * (HD / 4); e += 256) {  // queries: (b, m) -> head hkv*kvm + m
-    const int qi = e / (HD / 4), d4 = e % (HD / 4);
-    const int b = qi / kvm, m = qi % kvm;
-    *(float4 *)(Q + qi * HD + d4 * 4) = *(const float4 *)(p.q + ((size_t)b * p.NH + hkv * kvm + m) * HD + d4 * 4);
+  // Global -> LDS copies keep QB (queries) or KV_L (key/value rows) loads
+  // per thread in flight before the first store.
+  constexpr int QB = 8;
+  for (int e0 = 0; e0 < MT * 16 * (HD / 4); e0 += 256 * QB) {  // query (b, m) -> head hkv*kvm + m
+    float4 t[QB];
+#pragma unroll
+    for (int u = 0; u < QB; ++u) {
+      const int e = e0 + tid + 256 * u, qi = e / (HD / 4), d4 = e % (HD / 4);
+      t[u] = (float4){0.f, 0.f, 0.f, 0.f};
+      if (qi < nq) t[u] = *(const float4 *)(p.q + ((size_t)(qi / kvm) * p.NH + hkv * kvm + qi % kvm) * HD + d4 * 4);
+    }
+#pragma unroll
+    for (int u = 0; u < QB; ++u) {
+      const int e = e0 + tid + 256 * u;
+      if (e < MT * 16 * (HD / 4)) *(float4 *)(Qs + (e / (HD / 4)) * QROW + (e % (HD / 4)) * 4) = t[u];
+    }
   }
+  constexpr int KV_L = TC * (HD / 4) / 256;    // float4 of a chunk's K (or V) rows per thread
   for (int c = blockIdx.x; c * TC <= tlast; c += gridDim.x) {
     const int t0 = c * TC;
     const int tn = min(TC, tlast + 1 - t0);     // keys of this chunk that exist
-    __syncthreads();                            // previous chunk's P.V reads done
-    for (int e = tid; e < TC * (HD / 4); e += 256) {
-      const int t = e / (HD / 4), d4 = e % (HD / 4);
-      *(float4 *)(Kt + t * KROW + d4 * 4) =
-          t < tn ? *(const float4 *)(p.K + ((size_t)(t0 + t) * p.NKV + hkv) * HD + d4 * 4) : (float4){0.f, 0.f, 0.f, 0.f};
+    float4 kv[KV_L], vr[KV_L];                  // row t = wave + 4u, float4 d4 = lane
+#pragma unroll
+    for (int u = 0; u < KV_L; ++u) {
+      const int t = wave + 4 * u;
+      const size_t at = ((size_t)(t0 + t) * p.NKV + hkv) * HD + lane * 4;
+      kv[u] = t < tn ? *(const float4 *)(p.K + at) : (float4){0.f, 0.f, 0.f, 0.f};
+      vr[u] = t < tn ? *(const float4 *)(p.V + at) : (float4){0.f, 0.f, 0.f, 0.f};  // held until P is done
     }
+    __syncthreads();                            // previous chunk's reads of KV and Ps done
+#pragma unroll
+    for (int u = 0; u < KV_L; ++u) *(float4 *)(KV + (wave + 4 * u) * KROW + lane * 4) = kv[u];
     __syncthreads();
-    {  // scores and chunk softmax statistics
-      const int key = tid & (TC - 1), qg = tid / TC;   // TC = 32: 8 query groups
-      const int t = t0 + key;
-      const float *kr = Kt + key * KROW;
-      for (int qi = qg; qi < nq; qi += 256 / TC) {
-        const int b = qi / kvm;
-        const float *q = Q + qi * HD;
-        float sc = -__builtin_inff();
-        if (t <= pbase + b && key < tn) {
-          float a = 0.f;
-          for (int d = 0; d < HD; d += 4) {
-            const float4 k4 = *(const float4 *)(kr + d), q4 = *(const float4 *)(q + d);
-            a = fmaf(q4.x, k4.x, a); a = fmaf(q4.y, k4.y, a); a = fmaf(q4.z, k4.z, a); a = fmaf(q4.w, k4.w, a);
-          }
-          sc = a * scale;
-        }
-        // max / sum over the 32 keys (lanes 0-31 or 32-63 of the wave)
-        float m = sc;
-        m = fmaxf(m, dpp<0xB1>(m)); m = fmaxf(m, dpp<0x4E>(m)); m = fmaxf(m, dpp<0x141>(m)); m = fmaxf(m, dpp<0x140>(m));
-        m = fmaxf(m, __shfl_xor(m, 16));
-        const float e = (sc == -__builtin_inff()) ? 0.f : expf(sc - m);
-        float l = sum16(e);
-        l += __shfl_xor(l, 16);
-        S[qi * TC + key] = e;
-        if (key == 0) {
+    // scores and the chunk softmax, one 16-query tile per wave
+    for (int mt = wave; mt < MT; mt += 4) {
+      f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      const float *qa = Qs + (mt * 16 + lr) * QROW + lg * (HD / 4);
+      const float *k0 = KV + lr * KROW + lg * (HD / 4), *k1 = k0 + 16 * KROW;
+#pragma unroll 4
+      for (int k = 0; k < HD / 4; k += 4) {
+        const float4 a = *(const float4 *)(qa + k), b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b0.x, s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b1.x, s1, 0, 0, 0);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b0.y, s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b1.y, s1, 0, 0, 0);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b0.z, s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b1.z, s1, 0, 0, 0);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b0.w, s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b1.w, s1, 0, 0, 0);
+      }
+      // s0[r], s1[r]: query row mt*16 + 4*lg + r, keys lr and 16 + lr
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qi = mt * 16 + 4 * lg + r;
+        const int tq = pbase + qi / kvm;       // the query's position
+        const bool v0 = qi < nq && lr < tn && t0 + lr <= tq;
+        const bool v1 = qi < nq && 16 + lr < tn && t0 + 16 + lr <= tq;
+        const float a0 = v0 ? s0[r] * scale : -__builtin_inff(), a1 = v1 ? s1[r] * scale : -__builtin_inff();
+        const float m = max16(fmaxf(a0, a1));
+        const float e0 = v0 ? expf(a0 - m) : 0.f, e1 = v1 ? expf(a1 - m) : 0.f;
+        const float l = sum16(e0 + e1);
+        Ps[(mt * 16 + 4 * lg + r) * PROW + lr] = e0;
+        Ps[(mt * 16 + 4 * lg + r) * PROW + 16 + lr] = e1;
+        if (lr == 0 && qi < nq) {
           const size_t pi = ((size_t)hkv * p.nchunk + c) * nq + qi;
           p.pm[pi] = m;
           p.pl[pi] = l;
         }
       }
     }
-    __syncthreads();
-    for (int e = tid; e < TC * (HD / 4); e += 256) {  // V rows replace K
-      const int t = e / (HD / 4), d4 = e % (HD / 4);
-      *(float4 *)(Kt + t * KROW + d4 * 4) =
-          t < tn ? *(const float4 *)(p.V + ((size_t)(t0 + t) * p.NKV + hkv) * HD + d4 * 4) : (float4){0.f, 0.f, 0.f, 0.f};
+    __syncthreads();                            // K reads and P writes done
+#pragma unroll
+    for (int u = 0; u < KV_L; ++u) {            // V^T[d][t]
+      const int t = wave + 4 * u;
+      KV[(lane * 4 + 0) * VROW + t] = vr[u].x;
+      KV[(lane * 4 + 1) * VROW + t] = vr[u].y;
+      KV[(lane * 4 + 2) * VROW + t] = vr[u].z;
+      KV[(lane * 4 + 3) * VROW + t] = vr[u].w;
     }
     __syncthreads();
-    {  // P.V: thread = head dim
-      const int d = tid;
-      for (int q0 = 0; q0 < nq; q0 += 8) {
-        const int nqq = min(8, nq - q0);
-        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int t = 0; t < TC; t += 4) {
-          const float v0 = Kt[(t + 0) * KROW + d], v1 = Kt[(t + 1) * KROW + d];
-          const float v2 = Kt[(t + 2) * KROW + d], v3 = Kt[(t + 3) * KROW + d];
+    // P.V: head-dim tiles 4*wave .. 4*wave+3 of every query tile
+    for (int mt = 0; mt < MT; ++mt) {
+      const float *pa = Ps + (mt * 16 + lr) * PROW + lg * (TC / 4);
+      const float4 pa0 = *(const float4 *)pa, pa1 = *(const float4 *)(pa + 4);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            if (j >= nqq) break;
-            const float4 pr = *(const float4 *)(S + (q0 + j) * TC + t);
-            o[j] = fmaf(pr.x, v0, o[j]); o[j] = fmaf(pr.y, v1, o[j]);
-            o[j] = fmaf(pr.z, v2, o[j]); o[j] = fmaf(pr.w, v3, o[j]);
-          }
-        }
+      for (int q = 0; q < 4; ++q) {
+        const int nd = wave * 4 + q;
+        const float *vb = KV + (nd * 16 + lr) * VROW + lg * (TC / 4);
+        const float4 vb0 = *(const float4 *)vb, vb1 = *(const float4 *)(vb + 4);
+        f32x4_t o = {0.f, 0.f, 0.f, 0.f};
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.x, vb0.x, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.y, vb0.y, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.z, vb0.z, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.w, vb0.w, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.x, vb1.x, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.y, vb1.y, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.z, vb1.z, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.w, vb1.w, o, 0, 0, 0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (j >= nqq) break;
-          p.po[(((size_t)hkv * p.nchunk + c) * nq + q0 + j) * HD + d] = o[j];
+        for (int r = 0; r < 4; ++r) {
+          const int qi = mt * 16 + 4 * lg + r;
+          if (qi < nq) p.po[(((size_t)hkv * p.nchunk + c) * nq + qi) * HD + nd * 16 + lr] = o[r];
         }
       }
     }
@@ -238,14 +282,39 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
   const int pos = *p.last + 1 + b;
   if (pos < 0 || pos >= p.max_ctx) return;
   const int nc = pos / TC + 1;
-  float M = -__builtin_inff();
-  for (int c = 0; c < nc; ++c) M = fmaxf(M, p.pm[((size_t)hkv * p.nchunk + c) * nq + qi]);
+  __shared__ float red[4], s_w[256], s_l[256];
+  const size_t base = (size_t)hkv * p.nchunk * nq + qi;  // statistics of chunk c at base + c * nq
+  float mx = -__builtin_inff();
+  for (int c = d; c < nc; c += 256) mx = fmaxf(mx, p.pm[base + (size_t)c * nq]);
+  mx = max64(mx);
+  if ((d & 63) == 0) red[d >> 6] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // Chunks in order, 256 at a time: thread j weighs chunk c0 + j into LDS,
+  // then every thread (head dim d) accumulates them with its partial
+  // outputs loaded 8 at a time.
   float L = 0.f, O = 0.f;
-  for (int c = 0; c < nc; ++c) {
-    const size_t pi = ((size_t)hkv * p.nchunk + c) * nq + qi;
-    const float w = expf(p.pm[pi] - M);
-    L = fmaf(w, p.pl[pi], L);
-    O = fmaf(w, p.po[pi * HD + d], O);
+  for (int c0 = 0; c0 < nc; c0 += 256) {
+    __syncthreads();  // previous tile's weights read
+    if (c0 + d < nc) {
+      const size_t pi = base + (size_t)(c0 + d) * nq;
+      s_w[d] = expf(p.pm[pi] - M);
+      s_l[d] = p.pl[pi];
+    }
+    __syncthreads();
+    const int n = min(256, nc - c0);
+    for (int j0 = 0; j0 < n; j0 += 8) {
+      float pv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        pv[u] = j0 + u < n ? p.po[(base + (size_t)(c0 + j0 + u) * nq) * HD + d] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (j0 + u >= n) break;
+        L = fmaf(s_w[j0 + u], s_l[j0 + u], L);
+        O = fmaf(s_w[j0 + u], pv[u], O);
+      }
+    }
   }
   const float g = p.qfull[(size_t)b * p.qfs + (size_t)h * 2 * HD + HD + d];
   const float y = (O / L) * (1.f / (1.f + expf(-g)));
@@ -300,7 +369,9 @@ int attention_launch(const float *qfull, int qfs, const float *kx, const float *
   p.yh = yh;
   hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
   const int nwg = p.nchunk < ATTN_CHUNK_WGS ? p.nchunk : ATTN_CHUNK_WGS;
-  const size_t lds = ((size_t)TC * KROW + (size_t)nq * (TC + HD)) * sizeof(float);
+  const int MT = (nq + 15) / 16;
+  const size_t lds = ((size_t)MT * 16 * (QROW + PROW) + KV_FLOATS) * sizeof(float);
+  if (lds > 160 * 1024) return CWEN_EINVAL;
   int rc;
   if ((rc = attention_init())) return rc;
   hipLaunchKernelGGL(attn_chunk_kernel, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);

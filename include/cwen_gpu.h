@@ -163,9 +163,9 @@ int cwen_gdn_block(cwen_ctx *ctx, cwen_gdn *g, const float *qkv, int qs, const f
                    float *out, int os, int B, void *stream);
 /* Accept the first n positions (0..B) of the last block: the current state
  * becomes the snapshot after position n-1 (n = 0 keeps the state from
- * before the block).  Host-side index move, no device work.  Replaces
- * snap_load + the replaying forward_block of a short walk (run.c:4975-4988)
- * for this layer. */
+ * before the block).  Moves the ring index only (no state is copied);
+ * waits for queued work first.  Replaces snap_load + the replaying
+ * forward_block of a short walk (run.c:4975-4988) for this layer. */
 int cwen_gdn_commit(cwen_gdn *g, int n);
 
 /* ---- the block-verify model ----

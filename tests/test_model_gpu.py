@@ -63,6 +63,28 @@ def test_forward_parity_vs_oracle(env, oracle):
     assert m.pos == len(toks) - 1
 
 
+def test_forward_parity_across_key_chunks(env, oracle):
+    """70 positions in ragged blocks (16, 16, 3, 13, 16, 6): blocks cross the
+    32-key chunk boundaries of the attention, so the chunk partials, their
+    merge and the per-query masks inside a chunk are all exercised.  Same
+    tolerance as the single-chunk parity test."""
+    from model_oracle import OracleModel
+    gpu, ctx, m, tensors = env
+    OM = OracleModel(oracle, CFG, tensors)
+    toks = synth.prompt_tokens(7, 70, CFG["vocab"])
+    m.reset()
+    ref = np.stack([OM.step(t, p) for p, t in enumerate(toks)])
+    got, b0 = [], 0
+    for B in (16, 16, 3, 13, 16, 6):
+        am = m.forward(toks[b0:b0 + B])       # with the head: logits are written
+        got.append(m.logits(B))
+        assert all(am[i] == oracle.argmax(got[-1][i]) for i in range(B))
+        b0 += B
+    got = np.concatenate(got)
+    for p in range(len(toks)):
+        assert rel_err(got[p], ref[p]) <= 1e-2, (p, rel_err(got[p], ref[p]))
+
+
 def test_block_equals_serial_bitwise(env):
     gpu, ctx, m, _ = env
     toks = synth.prompt_tokens(2, 20, CFG["vocab"])
