@@ -410,7 +410,7 @@ def main() -> int:
                       for B, r in sorted(res.items())},
         },
         "roofline": {
-            "kernel": "q4_gemv_kernel<2,1,2,8> (Q4_0 RSI gate/up pair + SwiGLU, 8 staged columns), B=8",
+            "kernel": "gemv_kernel<0,2,1,2,8,false> (Q4_0 RSI gate/up pair + SwiGLU, 8 staged f16 columns), B=8",
             "bound": "hbm",
             "achieved": round(h["swiglu_gbs"], 1),
             "peak": PEAK_GBS,

@@ -220,6 +220,21 @@ static int check_w(const cwen_ctx *ctx, const cwen_weight *W) {
   return (!ctx || !W || W->ctx != ctx) ? CWEN_EINVAL : CWEN_OK;
 }
 
+// f32 activations of the f32 entry points: for B <= 4 the GEMV stages and
+// converts them itself (one launch); for larger blocks a separate conversion
+// into ctx->xh is faster (the f32 staging adds registers and L2 traffic to
+// every workgroup of the GEMV), measured on the FFN shapes.
+static int f32_operand(cwen_ctx *ctx, const float *X, int xs, int K, int B, hipStream_t st, GemvNorm *n,
+                       const _Float16 **xh) {
+  if (B <= 4) {
+    *n = {X, nullptr, nullptr, 0, 0.f, xs};
+    *xh = nullptr;
+    return CWEN_OK;
+  }
+  *xh = ctx->xh;
+  return act_to_f16(X, xs, ctx->xh, K, B, st);
+}
+
 int cwen_act_to_f16(cwen_ctx *ctx, const float *X, int xs, void *Xh, int K, int B, void *stream) {
   if (!ctx || !Xh || !aligned16(Xh) || K <= 0 || (K & 7)) return CWEN_EINVAL;
   int rc = check_act(X, xs, K, B);
@@ -234,9 +249,11 @@ int cwen_gemvb(cwen_ctx *ctx, const cwen_weight *W, int side, const float *X, in
   if (side < 0 || side >= W->nside) return CWEN_EINVAL;
   if ((rc = check_act(X, xs, W->ne0, B)) || (rc = check_out(Y, ys, W->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
-  if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
+  GemvNorm x;
+  const _Float16 *xh;
+  if ((rc = f32_operand(ctx, X, xs, W->ne0, B, st, &x, &xh))) return rc;
   GemvOut o = {Y, nullptr, nullptr, ys, 0};
-  return gemv_launch(ctx, W, 1, side, GEMV_EPI_STORE, ctx->xh, o, B, st);
+  return gemv_launch(ctx, W, 1, side, GEMV_EPI_STORE, xh, o, B, st, xh ? nullptr : &x);
 }
 
 int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *YA,
@@ -248,9 +265,11 @@ int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs,
       (rc = check_out(YB, ys, W->ne1, B)))
     return rc;
   hipStream_t st = (hipStream_t)stream;
-  if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
+  GemvNorm x;
+  const _Float16 *xh;
+  if ((rc = f32_operand(ctx, X, xs, W->ne0, B, st, &x, &xh))) return rc;
   GemvOut o = {YA, YB, nullptr, ys, 0};
-  return gemv_launch(ctx, W, 2, 0, GEMV_EPI_PAIR, ctx->xh, o, B, st);
+  return gemv_launch(ctx, W, 2, 0, GEMV_EPI_PAIR, xh, o, B, st, xh ? nullptr : &x);
 }
 
 int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, float *H,
@@ -260,9 +279,11 @@ int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int x
   if (W->nside != 2) return CWEN_EINVAL;
   if ((rc = check_act(X, xs, W->ne0, B)) || (rc = check_out(H, hs, W->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
-  if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
+  GemvNorm x;
+  const _Float16 *xh;
+  if ((rc = f32_operand(ctx, X, xs, W->ne0, B, st, &x, &xh))) return rc;
   GemvOut o = {H, nullptr, nullptr, hs, 0};
-  return gemv_launch(ctx, W, 2, 0, GEMV_EPI_SWIGLU, ctx->xh, o, B, st);
+  return gemv_launch(ctx, W, 2, 0, GEMV_EPI_SWIGLU, xh, o, B, st, xh ? nullptr : &x);
 }
 
 int cwen_gemvb_f16(cwen_ctx *ctx, const cwen_weight *W, int side, const void *Xh, float *Y,
@@ -297,9 +318,11 @@ int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd,
     return CWEN_EINVAL;
   if ((rc = check_act(X, xs, Wgu->ne0, B)) || (rc = check_out(Y, ys, Wd->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
-  if ((rc = act_to_f16(X, xs, ctx->xh, Wgu->ne0, B, st))) return rc;
+  GemvNorm x;
+  const _Float16 *xh;
+  if ((rc = f32_operand(ctx, X, xs, Wgu->ne0, B, st, &x, &xh))) return rc;
   GemvOut o1 = {nullptr, nullptr, ctx->hh, 0, 0};
-  if ((rc = gemv_launch(ctx, Wgu, 2, 0, GEMV_EPI_SWIGLU, ctx->xh, o1, B, st))) return rc;
+  if ((rc = gemv_launch(ctx, Wgu, 2, 0, GEMV_EPI_SWIGLU, xh, o1, B, st, xh ? nullptr : &x))) return rc;
   GemvOut o2 = {Y, nullptr, nullptr, ys, 1};
   return gemv_launch(ctx, Wd, 1, 0, GEMV_EPI_STORE, ctx->hh, o2, B, st);
 }
@@ -313,9 +336,11 @@ int cwen_head_verify(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs
   if (E < 0 || E > B - 1 || (E > 0 && !drafts)) return CWEN_EINVAL;
   if (logits && (rc = check_out(logits, ls, W->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
-  if ((rc = act_to_f16(X, xs, ctx->xh, W->ne0, B, st))) return rc;
+  GemvNorm x;
+  const _Float16 *xh;
+  if ((rc = f32_operand(ctx, X, xs, W->ne0, B, st, &x, &xh))) return rc;
   GemvOut o = {logits, nullptr, nullptr, ls, 0, {ctx->amax_keys, ctx->amax_cnt, drafts, E, res}};
-  return gemv_launch(ctx, W, 1, 0, GEMV_EPI_ARGMAX, ctx->xh, o, B, st);
+  return gemv_launch(ctx, W, 1, 0, GEMV_EPI_ARGMAX, xh, o, B, st, xh ? nullptr : &x);
 }
 
 int cwen_argmax_walk(cwen_ctx *ctx, const float *logits, int ls, int V, int B, const int *drafts,

@@ -126,15 +126,17 @@ struct GemvOut {
   ArgmaxOut am;      // ARGMAX only
   float *ssq;        // STORE: per row tile, the sum of squares of the final y per column [row tile][CWEN_BMAX]
 };
-// Normalised f32 input: the GEMV's activations are RMSNorm(x) with weight w,
-// applied while staging; the sum of squares per column comes from the
-// producer's ssq partials (npart of them).
+// f32 input staged by the GEMV itself: the activations are RMSNorm(x) with
+// weight w, applied while staging; the sum of squares per column comes from
+// the producer's ssq partials (npart of them).  Plain conversion to the f16
+// operand when w and ssq are null and npart is 0.
 struct GemvNorm {
-  const float *x;    // [B][K]
+  const float *x;    // [c*xs + k], 16-byte aligned, xs % 4 == 0
   const float *w;    // [K]
   const float *ssq;  // [npart][CWEN_BMAX]
   int npart;
   float eps;
+  int xs;            // row stride of x in floats (>= K when B > 1)
 };
 int gemv_fmt_of(int type);
 size_t gemv_st_bytes(int fmt);
@@ -166,6 +168,9 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
 // Also writes each row's sum of squares to ssq[b] (one partial per column).
 int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *toks, int B, int H, float *X,
                  int xs, float *ssq, hipStream_t st);
+// The normalised f16 operand of a GemvNorm (non-plain) into Y [b*ys + k],
+// bit-identical to what the normalising GEMV stages.
+int norm_f16_launch(const GemvNorm &n, int K, int B, _Float16 *Y, int ys, hipStream_t st);
 size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B);
 int attention_init();
 // `last` is a device int: the last filled cache slot before the block (the

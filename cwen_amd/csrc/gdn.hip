@@ -122,36 +122,17 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
     s_g[lane] = expf(dec);
     s_beta[lane] = bt;
   }
-  // v of this slice and q, k of key head hk for every position: all loads
-  // issued before the first use (a load-use loop would pay one memory round
-  // trip per position).
-  constexpr int VL = (MAXB * COLS + 63) / 64;
-  float vv[VL], q0[MAXB], q1[MAXB], k0[MAXB], k1[MAXB];
-#pragma unroll
-  for (int u = 0; u < VL; ++u) {
-    const int e = lane + 64 * u;
-    vv[u] = e < B * COLS ? p.xc[(size_t)(e / COLS) * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS] : 0.f;
-  }
-#pragma unroll
-  for (int b = 0; b < MAXB; ++b) {
-    if (b >= B) break;
+  for (int e = lane; e < B * COLS; e += 64)
+    vs[e / COLS][e % COLS] = p.xc[(size_t)(e / COLS) * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
+  // q and k of key head hk, l2-normalised per position
+  for (int b = 0; b < B; ++b) {
     const float *xq = p.xc + (size_t)b * p.C + hk * DK;
     const float *xk = p.xc + (size_t)b * p.C + (p.nkh + hk) * DK;
-    q0[b] = xq[lane]; q1[b] = xq[lane + 64]; k0[b] = xk[lane]; k1[b] = xk[lane + 64];
-  }
-#pragma unroll
-  for (int u = 0; u < VL; ++u) {
-    const int e = lane + 64 * u;
-    if (e < B * COLS) vs[e / COLS][e % COLS] = vv[u];
-  }
-  // q and k l2-normalised per position
-#pragma unroll
-  for (int b = 0; b < MAXB; ++b) {
-    if (b >= B) break;
-    const float sq = 1.f / sqrtf(sum64(q0[b] * q0[b] + q1[b] * q1[b]) + 1e-6f);
-    const float sk = 1.f / sqrtf(sum64(k0[b] * k0[b] + k1[b] * k1[b]) + 1e-6f);
-    qk[b][lane] = q0[b] * sq; qk[b][lane + 64] = q1[b] * sq;
-    qk[b][DK + lane] = k0[b] * sk; qk[b][DK + lane + 64] = k1[b] * sk;
+    const float q0 = xq[lane], q1 = xq[lane + 64], k0 = xk[lane], k1 = xk[lane + 64];
+    const float sq = 1.f / sqrtf(sum64(q0 * q0 + q1 * q1) + 1e-6f);
+    const float sk = 1.f / sqrtf(sum64(k0 * k0 + k1 * k1) + 1e-6f);
+    qk[b][lane] = q0 * sq; qk[b][lane + 64] = q1 * sq;
+    qk[b][DK + lane] = k0 * sk; qk[b][DK + lane + 64] = k1 * sk;
   }
   __syncthreads();
 

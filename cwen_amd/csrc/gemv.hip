@@ -235,9 +235,11 @@ struct GemvParams {
   const _Float16 *xh;  // activations f16 [B][K]
   uint32_t xbytes;     // B*K*2, or B*K*4 for XN (buffer range: columns >= B read as zero)
   // XN: the activations are RMSNorm(xf) applied while staging,
-  // f16((nw[k] * x[k]) * s_c), s_c = 1 / sqrt(sum_p ssq[p][c] / K + eps).
-  const float *xf;     // f32 rows [B][K]
-  const float *nw;     // norm weight [K]
+  // f16((nw[k] * x[k]) * s_c), s_c = 1 / sqrt(sum_p ssq[p][c] / K + eps);
+  // plain f16(x[k]) when nw is null.
+  const float *xf;     // f32 rows [c*xfs + k]
+  int xfs;
+  const float *nw;     // norm weight [K], or null
   const float *ssq;    // per-row-tile partial sums of squares [npart][CWEN_BMAX]
   int npart;           // 1..64
   float eps;
@@ -286,7 +288,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.wbytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(XN ? (const void *)p.xf : (const void *)p.xh, p.xbytes);
-  const __amdgpu_buffer_rsrc_t nwr = make_rsrc(p.nw, XN ? (uint32_t)p.K * 4u : 0u);
+  const bool plain = p.nw == nullptr;        // XN without a norm: conversion only
+  const __amdgpu_buffer_rsrc_t nwr = make_rsrc(p.nw, (XN && !plain) ? (uint32_t)p.K * 4u : 0u);
+  const uint2 ones = {0x3f800000u, 0x3f800000u};
 
   // Weight streams of this wave: set q = r*NS + s is row group rgs[r], side s.
   const uint32_t sstride = (uint32_t)p.nsw * F::ST_BYTES;
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
     const int c = wave + WAVES * i;
-    xofs[i] = (uint32_t)c * (uint32_t)p.K * XE + (uint32_t)st0 * xround + lane * 8 * XE;  // range-checked
+    xofs[i] = (uint32_t)c * (uint32_t)(XN ? p.xfs : p.K) * XE + (uint32_t)st0 * xround + lane * 8 * XE;  // range-checked
     xslot[i] = c * 64 + (lane ^ c);
   }
   // XN: the norm weights of a round (512 floats) pass through LDS, two
@@ -346,8 +350,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   };
   stage_load(0);
   if constexpr (XN) {
-    nwl[0][tid] = __builtin_bit_cast(float2, bload8(nwr, nofs, 0));
-    nwl[1][tid] = __builtin_bit_cast(float2, bload8(nwr, nofs, nround > 1 ? xround : 0u));
+    nwl[0][tid] = __builtin_bit_cast(float2, plain ? ones : bload8(nwr, nofs, 0));
+    nwl[1][tid] = __builtin_bit_cast(float2, plain ? ones : bload8(nwr, nofs, nround > 1 ? xround : 0u));
   }
 #pragma unroll
   for (int j = 0; j < TILES; ++j) {
@@ -374,7 +378,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       const int c = wave + WAVES * i;
       const float v = (lane < p.npart && c < p.B) ? p.ssq[lane * CWEN_BMAX + c] : 0.f;
       const float ss = sum64(v);
-      const float sc1 = c < p.B ? 1.f / sqrtf(ss / (float)p.K + p.eps) : 0.f;
+      const float sc1 = c >= p.B ? 0.f : plain ? 1.f : 1.f / sqrtf(ss / (float)p.K + p.eps);
       scl[i] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc1)));  // uniform
     }
   }
@@ -435,7 +439,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
         dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q] + nr * sstride, 0);
     }
     stage_load(nr * xround);
-    if constexpr (XN) nv = bload8(nwr, nofs, (uint32_t)(rd + 2 < nround ? rd + 2 : nround - 1) * xround);
+    if constexpr (XN) {
+      nv = bload8(nwr, nofs, (uint32_t)(rd + 2 < nround ? rd + 2 : nround - 1) * xround);
+      if (plain) nv = ones;
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < TILES; ++j) {
@@ -952,7 +959,11 @@ int gemv_row_tiles(const cwen_weight *w) { return (w->nrg + WAVES * w->rows - 1)
 
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
                 const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvNorm *nrm) {
-  if (nrm && (xh || !nrm->x || !nrm->w || !nrm->ssq || nrm->npart < 1 || nrm->npart > 64)) return CWEN_EINVAL;
+  if (nrm) {
+    const bool plain = !nrm->w && !nrm->ssq && nrm->npart == 0;
+    if (xh || !nrm->x || ((uintptr_t)nrm->x & 15) || (nrm->xs & 3) || (B > 1 && nrm->xs < w->ne0)) return CWEN_EINVAL;
+    if (!plain && (!nrm->w || !nrm->ssq || nrm->npart < 1 || nrm->npart > 64)) return CWEN_EINVAL;
+  }
   if (out.ssq && (epi != GEMV_EPI_STORE || gemv_row_tiles(w) > 64)) return CWEN_EINVAL;
   GemvParams p;
   p.w = w->dev;
@@ -965,8 +976,10 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   p.S = w->split;
   p.rps = w->rps;
   p.xh = xh;
-  p.xbytes = (uint32_t)((size_t)B * w->ne0 * (nrm ? 4 : 2));
+  const int xfs = nrm ? (B > 1 ? nrm->xs : w->ne0) : 0;
+  p.xbytes = nrm ? (uint32_t)(((size_t)(B - 1) * xfs + w->ne0) * 4) : (uint32_t)((size_t)B * w->ne0 * 2);
   p.xf = nrm ? nrm->x : nullptr;
+  p.xfs = xfs;
   p.nw = nrm ? nrm->w : nullptr;
   p.ssq = nrm ? nrm->ssq : nullptr;
   p.npart = nrm ? nrm->npart : 0;

@@ -63,6 +63,7 @@ struct cwen_model {
   int *toks = nullptr, *res = nullptr;
   float *X = nullptr;            // residual stream [BMAX][H]
   float *ssq = nullptr;          // partial sums of squares of X [64][BMAX]
+  _Float16 *xh = nullptr;        // normalised f16 operand for blocks of more than 8 [BMAX][H]
   float *lin = nullptr;           // GDN layer input GEMV out [BMAX][lin_rows]
   _Float16 *gh = nullptr;        // GDN output f16 [BMAX][nvh*dk]
   float *att = nullptr;           // attention input GEMV out [BMAX][att_rows]
@@ -128,6 +129,18 @@ int upload_w(cwen_model *m, int type, const void *data, const void *scales, int 
   return cwen_weight_upload(m->ctx, type, data, scales, ne0, ne1, out);
 }
 
+// A GEMV over the normalised residual stream: for blocks of up to 8
+// columns the GEMV stages and normalises the f32 rows itself; for larger
+// blocks the f16 operand is written first (the 16-column normalising GEMV
+// needs more registers than 3 waves per SIMD allow).  Both give the same
+// operand bits.
+int gemv_normed(cwen_model *m, const cwen_weight *w, int nsides, int epi, const GemvNorm &n, const GemvOut &o,
+                int B, hipStream_t st) {
+  if (B <= 8) return gemv_launch(m->ctx, w, nsides, 0, epi, nullptr, o, B, st, &n);
+  const int rc = norm_f16_launch(n, w->ne0, B, m->xh, w->ne0, st);
+  return rc ? rc : gemv_launch(m->ctx, w, nsides, 0, epi, m->xh, o, B, st);
+}
+
 // Advance the device position and ring slot by the positions kept: n, or
 // res[0] + 1 (accepted drafts + bonus) when res is given, clamped to [1, nmax].
 __global__ void advance_kernel(int *ctl, const int *res, int n, int nmax, int nslot) {
@@ -154,12 +167,12 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
   int npart = 1;
   for (int l = 0; l < c.n_layers; ++l) {
     Layer &y = m->L[l];
-    const GemvNorm n1 = {m->X, y.attn_norm, m->ssq, npart, c.rms_eps};
+    const GemvNorm n1 = {m->X, y.attn_norm, m->ssq, npart, c.rms_eps, H};
     const cwen_weight *wout;
     if (y.linear) {
       const Rows r = rows_of(c);
       GemvOut o1 = {m->lin, nullptr, nullptr, r.lin, 0};
-      if ((rc = gemv_launch(ctx, y.lin_in, 1, 0, GEMV_EPI_STORE, nullptr, o1, B, st, &n1))) return rc;
+      if ((rc = gemv_normed(m, y.lin_in, 1, GEMV_EPI_STORE, n1, o1, B, st))) return rc;
       const float *qkv = m->lin, *z = m->lin + r.C, *ga = m->lin + r.o_alpha, *gb = m->lin + r.o_beta;
       if ((rc = gdn_block_launch(y.gdn, qkv, r.lin, z, r.lin, ga, gb, r.lin, y.ssm_conv, y.ssm_norm, nullptr, 0, B,
                                  st, m->gh, r.Zh, y.ssm_a, y.ssm_dt)))
@@ -171,7 +184,7 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
     } else {
       const Rows r = rows_of(c);
       GemvOut o1 = {m->att, nullptr, nullptr, r.att, 0};
-      if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, nullptr, o1, B, st, &n1))) return rc;
+      if ((rc = gemv_normed(m, y.att_in, 1, GEMV_EPI_STORE, n1, o1, B, st))) return rc;
       if ((rc = attention_launch(m->att, r.att, m->att + r.Qo2, m->att + r.Qo2 + r.Ko, r.att, y.q_norm, y.k_norm,
                                  m->qbuf, y.K, y.V, m->ctl, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
                                  c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st)))
@@ -181,11 +194,11 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
       if ((rc = gemv_launch(ctx, y.wo, 1, 0, GEMV_EPI_STORE, m->yh, o5, B, st))) return rc;
       wout = y.wo;
     }
-    const GemvNorm n2 = {m->X, y.post_norm, m->ssq, gemv_row_tiles(wout), c.rms_eps};
+    const GemvNorm n2 = {m->X, y.post_norm, m->ssq, gemv_row_tiles(wout), c.rms_eps, H};
     GemvOut f1 = {nullptr, nullptr, m->hh, 0, 0};
     GemvOut f2 = {m->X, nullptr, nullptr, H, 1};
     f2.ssq = m->ssq;
-    if ((rc = gemv_launch(ctx, y.ffn_gu, 2, 0, GEMV_EPI_SWIGLU, nullptr, f1, B, st, &n2)) ||
+    if ((rc = gemv_normed(m, y.ffn_gu, 2, GEMV_EPI_SWIGLU, n2, f1, B, st)) ||
         (rc = gemv_launch(ctx, y.ffn_down, 1, 0, GEMV_EPI_STORE, m->hh, f2, B, st)))
       return rc;
     npart = gemv_row_tiles(y.ffn_down);
@@ -193,10 +206,10 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
   }
   if (mode != MODE_FWD) {
     const int E = mode == MODE_VERIFY ? B - 1 : 0;
-    const GemvNorm nh = {m->X, m->out_norm, m->ssq, npart, c.rms_eps};
+    const GemvNorm nh = {m->X, m->out_norm, m->ssq, npart, c.rms_eps, H};
     GemvOut o = {m->logits, nullptr, nullptr, c.vocab, 0,
                  {ctx->amax_keys, ctx->amax_cnt, m->toks + 1, E, m->res}};
-    if ((rc = gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, nullptr, o, B, st, &nh))) return rc;
+    if ((rc = gemv_normed(m, m->head, 1, GEMV_EPI_ARGMAX, nh, o, B, st))) return rc;
   }
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->ctl, mode == MODE_VERIFY ? m->res : nullptr, B, B,
                      CWEN_BMAX + 1);
@@ -434,7 +447,7 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
   }
   if (!rc)
     rc = (dmalloc(&m->toks, BM) || dmalloc(&m->res, 2 + BM) ||
-          dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->ssq, (size_t)64 * BM) ||
+          dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->ssq, (size_t)64 * BM) || dmalloc(&m->xh, (size_t)BM * H) ||
           dmalloc(&m->lin, (size_t)BM * R.lin) || dmalloc(&m->gh, (size_t)BM * Zh) ||
           dmalloc(&m->att, (size_t)BM * R.att) || dmalloc(&m->qbuf, (size_t)BM * Qo) ||
           dmalloc(&m->apart, attn_partial_floats(c.n_head, c.n_kv_head, c.max_ctx, BM)) ||
@@ -471,7 +484,7 @@ int cwen_model_free(cwen_model *m) {
   }
   delete[] m->L;
   for (void *p : {(void *)m->emb_qs, (void *)m->emb_sc, (void *)m->out_norm, (void *)m->toks, (void *)m->ctl,
-                  (void *)m->res, (void *)m->X, (void *)m->ssq, (void *)m->lin, (void *)m->gh, (void *)m->att,
+                  (void *)m->res, (void *)m->X, (void *)m->ssq, (void *)m->xh, (void *)m->lin, (void *)m->gh, (void *)m->att,
                   (void *)m->qbuf,
                   (void *)m->apart, (void *)m->yh, (void *)m->hh, (void *)m->logits})
     if (p) (void)hipFree(p);
@@ -489,7 +502,7 @@ int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data,
   const cwen_model_cfg &c = m->cfg;
   const int H = c.d_model, I = c.d_ffn;
   const int C = (2 * c.gdn_nkh + c.gdn_nvh) * 128, Zh = c.gdn_nvh * 128;
-  const int Qo = c.n_head * c.head_dim, Ko = c.n_kv_head * c.head_dim;
+  const int Qo = c.n_head * c.head_dim;
   CWEN_HIP_TRY(hipSetDevice(m->ctx->device));
   const bool f32 = type == CWEN_T_F32;
   if (id == CWEN_TOK_EMBD) {  // rows dequantised one token at a time (embed_token_to)
