@@ -108,6 +108,17 @@ __device__ __forceinline__ float sum64(float v) {
 // run.c:378-384 silu_one: x * (1 / (1 + exp(-x)))
 __device__ __forceinline__ float silu_f(float x) { return x * (1.f / (1.f + expf(-x))); }
 
+// Row-tile partials of a column's sum of squares, at most 128, summed in a
+// fixed order: lane p adds partials p and p + 64, then one DPP tree over the
+// wave.  Every reader (GEMV staging, norm_f16) uses this, so they agree bit
+// for bit whatever the block size.
+constexpr int CWEN_MAX_PARTS = 128;
+__device__ __forceinline__ float sum_partials(const float *ssq, int npart, int col, int lane) {
+  float v = lane < npart ? ssq[lane * CWEN_BMAX + col] : 0.f;
+  if (lane + 64 < npart) v += ssq[(lane + 64) * CWEN_BMAX + col];
+  return sum64(v);
+}
+
 // ------------------------------------------------------------ gemv.hip
 enum { GEMV_EPI_STORE = 0, GEMV_EPI_PAIR = 1, GEMV_EPI_SWIGLU = 2, GEMV_EPI_ARGMAX = 3 };
 struct ArgmaxOut {

@@ -241,7 +241,7 @@ struct GemvParams {
   int xfs;
   const float *nw;     // norm weight [K], or null
   const float *ssq;    // per-row-tile partial sums of squares [npart][CWEN_BMAX]
-  int npart;           // 1..64
+  int npart;           // 1..CWEN_MAX_PARTS
   float eps;
   int K, B;
   float *part;         // split-K partials
@@ -368,16 +368,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     __builtin_amdgcn_sched_barrier(0);  // issue the ring in slot order
   }
   // XN: column scales from the producer's partial sums of squares, summed
-  // in a fixed order (lane p holds partial p), so every workgroup and every
-  // block size gets the same scale for a column.
+  // in a fixed order (sum_partials), so every workgroup and every block size
+  // gets the same scale for a column.
   float scl[XL];
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
     scl[i] = 0.f;
     if constexpr (XN) {
       const int c = wave + WAVES * i;
-      const float v = (lane < p.npart && c < p.B) ? p.ssq[lane * CWEN_BMAX + c] : 0.f;
-      const float ss = sum64(v);
+      const float ss = c < p.B ? sum_partials(p.ssq, p.npart, c, lane) : 0.f;
       const float sc1 = c >= p.B ? 0.f : plain ? 1.f : 1.f / sqrtf(ss / (float)p.K + p.eps);
       scl[i] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc1)));  // uniform
     }
@@ -879,12 +878,11 @@ void launch_cb(const GemvParams &p, int nrt, hipStream_t st) {
 
 template <int FMT>
 int launch_fmt(const GemvParams &p, int nrt, int R, int nsides, int epi, hipStream_t st) {
+  if (R != 1) return CWEN_EINVAL;  // one row group per wave (gemv_choose_split)
   if (nsides == 1 && epi == GEMV_EPI_STORE) {
-    if (R == 2) launch_cb<FMT, 1, 2, GEMV_EPI_STORE>(p, nrt, st);
-    else launch_cb<FMT, 1, 1, GEMV_EPI_STORE>(p, nrt, st);
+    launch_cb<FMT, 1, 1, GEMV_EPI_STORE>(p, nrt, st);
   } else if (nsides == 1 && epi == GEMV_EPI_ARGMAX) {
-    if (R == 2) launch_cb<FMT, 1, 2, GEMV_EPI_ARGMAX>(p, nrt, st);
-    else launch_cb<FMT, 1, 1, GEMV_EPI_ARGMAX>(p, nrt, st);
+    launch_cb<FMT, 1, 1, GEMV_EPI_ARGMAX>(p, nrt, st);
   } else {
     return CWEN_EINVAL;
   }
@@ -941,9 +939,10 @@ int gemv_repack_part(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, i
 // bit is independent of the block size.  rows: row groups per wave for
 // single-sided use; split: K split across workgroups; rps: super-tiles per split.
 void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
-  const int R = (w->nside == 1 && w->nrg >= 2 * WAVES * 32) ? 2 : 1;
-  // A pair is computed two-sided (R = 1); single-side calls on it use R = 1 too.
-  const int Rs = (w->nside == 1) ? R : 1;
+  // One row group (16 rows) per wave: fewer registers and split partials than
+  // two, measured faster on every 27B-shape matrix (e.g. the 16480 x 5120
+  // GDN input projection at B=8: 14.8 vs 19.1 us).
+  const int Rs = 1;
   const int nrt = (w->nrg + WAVES * Rs - 1) / (WAVES * Rs);
   const int nrd = w->nst;                            // rounds of K
   int S = (ctx->wg_target + nrt - 1) / nrt;
@@ -962,9 +961,9 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   if (nrm) {
     const bool plain = !nrm->w && !nrm->ssq && nrm->npart == 0;
     if (xh || !nrm->x || ((uintptr_t)nrm->x & 15) || (nrm->xs & 3) || (B > 1 && nrm->xs < w->ne0)) return CWEN_EINVAL;
-    if (!plain && (!nrm->w || !nrm->ssq || nrm->npart < 1 || nrm->npart > 64)) return CWEN_EINVAL;
+    if (!plain && (!nrm->w || !nrm->ssq || nrm->npart < 1 || nrm->npart > CWEN_MAX_PARTS)) return CWEN_EINVAL;
   }
-  if (out.ssq && (epi != GEMV_EPI_STORE || gemv_row_tiles(w) > 64)) return CWEN_EINVAL;
+  if (out.ssq && (epi != GEMV_EPI_STORE || gemv_row_tiles(w) > CWEN_MAX_PARTS)) return CWEN_EINVAL;
   GemvParams p;
   p.w = w->dev;
   p.wbytes = (uint32_t)w->bytes;

@@ -76,8 +76,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uin
 
 // ---- RMSNorm of B rows into the f16 GEMV operand, the column's sum of
 // squares taken from a producer's row-tile partials summed exactly as the
-// normalising GEMV staging sums them (lane p holds partial p, one fixed DPP
-// tree) and the same (w * x) * s per element: the operand is bit-identical to
+// normalising GEMV staging sums them (sum_partials) and the same (w * x) * s
+// per element: the operand is bit-identical to
 // the one that staging builds (run.c:346-368 rmsnorm).  Grid B, 256
 // threads; K <= 8192, K % 4 == 0; all loads issued before the first use.
 constexpr int NORM_MAXV = 8;
@@ -93,8 +93,7 @@ __global__ __launch_bounds__(256) void norm_f16_kernel(const float *X, int xs, c
       ww[j] = *(const float4 *)(w + i);
     }
   }
-  const float v = lane < npart ? ssq[lane * CWEN_BMAX + b] : 0.f;
-  const float s = 1.f / sqrtf(sum64(v) / (float)K + eps);
+  const float s = 1.f / sqrtf(sum_partials(ssq, npart, b, lane) / (float)K + eps);
 #pragma unroll
   for (int j = 0; j < NORM_MAXV; ++j) {
     const int i = (j * 256 + threadIdx.x) * 4;
@@ -362,7 +361,7 @@ int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *tok
 }
 
 int norm_f16_launch(const GemvNorm &n, int K, int B, _Float16 *Y, int ys, hipStream_t st) {
-  if (K % 4 || K > NORM_MAXV * 1024 || (n.xs & 3) || (ys & 3) || n.npart < 1 || n.npart > 64 || !n.w || !n.ssq)
+  if (K % 4 || K > NORM_MAXV * 1024 || (n.xs & 3) || (ys & 3) || n.npart < 1 || n.npart > CWEN_MAX_PARTS || !n.w || !n.ssq)
     return CWEN_EINVAL;
   hipLaunchKernelGGL(norm_f16_kernel, dim3((unsigned)B), dim3(256), 0, st, n.x, n.xs, n.w, n.ssq, n.npart, K, n.eps,
                      Y, ys);

@@ -62,7 +62,7 @@ struct cwen_model {
   // device scratch
   int *toks = nullptr, *res = nullptr;
   float *X = nullptr;            // residual stream [BMAX][H]
-  float *ssq = nullptr;          // partial sums of squares of X [64][BMAX]
+  float *ssq = nullptr;          // partial sums of squares of X [CWEN_MAX_PARTS][BMAX]
   _Float16 *xh = nullptr;        // normalised f16 operand for blocks of more than 8 [BMAX][H]
   float *lin = nullptr;           // GDN layer input GEMV out [BMAX][lin_rows]
   _Float16 *gh = nullptr;        // GDN output f16 [BMAX][nvh*dk]
@@ -103,7 +103,7 @@ Rows rows_of(const cwen_model_cfg &c) {
 int check_cfg(const cwen_model_cfg *c) {
   if (!c || c->n_layers <= 0 || c->d_model <= 0 || c->d_ffn <= 0 || c->vocab <= 0) return CWEN_EINVAL;
   if (c->d_model % Q4_K_ALIGN || c->d_ffn % Q4_K_ALIGN) return CWEN_EINVAL;
-  if (c->d_model > 8192) return CWEN_EINVAL;  // <= 64 row-tile partials of the residual's sum of squares
+  if (c->d_model > 8192) return CWEN_EINVAL;  // <= CWEN_MAX_PARTS row-tile partials of the residual's sum of squares
   if (c->head_dim != 256 || c->n_head <= 0 || c->n_kv_head <= 0 || c->n_head % c->n_kv_head) return CWEN_EINVAL;
   if ((c->n_head * c->head_dim) % Q4_K_ALIGN) return CWEN_EINVAL;
   if (c->gdn_dk != 128 || c->gdn_nkh <= 0 || c->gdn_nvh % c->gdn_nkh || (c->gdn_nvh * 128) % Q4_K_ALIGN)
@@ -447,7 +447,7 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
   }
   if (!rc)
     rc = (dmalloc(&m->toks, BM) || dmalloc(&m->res, 2 + BM) ||
-          dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->ssq, (size_t)64 * BM) || dmalloc(&m->xh, (size_t)BM * H) ||
+          dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->ssq, (size_t)CWEN_MAX_PARTS * BM) || dmalloc(&m->xh, (size_t)BM * H) ||
           dmalloc(&m->lin, (size_t)BM * R.lin) || dmalloc(&m->gh, (size_t)BM * Zh) ||
           dmalloc(&m->att, (size_t)BM * R.att) || dmalloc(&m->qbuf, (size_t)BM * Qo) ||
           dmalloc(&m->apart, attn_partial_floats(c.n_head, c.n_kv_head, c.max_ctx, BM)) ||
