@@ -262,14 +262,16 @@ __device__ __forceinline__ uint4 norm8(const uint4 (&x)[2], const float4 *w, flo
                     __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3));
 }
 
-// FMT: weight format.  NS: sides per row group (2 = both halves of an
-// interleaved pair).  R: row groups per wave; each wave carries R*NS weight
-// streams.  EPI: epilogue.  CB: activation columns staged (4, 8 or 16; >= B).
-// XN: f32 activations normalised while staging (GemvParams::xf).
+// FMT: weight format.  NS: sides of an interleaved pair computed (2: both;
+// the two waves of a wave pair take sides 0 and 1 of the same row groups and
+// combine them through LDS).  R: row groups per wave; each wave carries R
+// weight streams.  EPI: epilogue.  CB: activation columns staged (4, 8 or
+// 16; >= B).  XN: f32 activations staged (and normalised) by the kernel.
 template <int FMT, int NS, int R, int EPI, int CB, bool XN>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   using F = Fmt<FMT>;
-  constexpr int NSET = NS * R;
+  constexpr int NSET = R;
+  constexpr int RPW = NS == 2 ? WAVES / 2 : WAVES;  // row-group slots per workgroup
   constexpr int XL = CB / WAVES;            // staging loads per wave per round
   constexpr int TV = F::TV;
   __shared__ uint4 act[2][16 * 64];         // [buf][column c][unit u ^ c], f16 x 8 per unit
@@ -292,17 +294,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   const __amdgpu_buffer_rsrc_t nwr = make_rsrc(p.nw, (XN && !plain) ? (uint32_t)p.K * 4u : 0u);
   const uint2 ones = {0x3f800000u, 0x3f800000u};
 
-  // Weight streams of this wave: set q = r*NS + s is row group rgs[r], side s.
+  // Weight streams of this wave: stream r is row group rgs[r], side `side`.
   const uint32_t sstride = (uint32_t)p.nsw * F::ST_BYTES;
+  const int side = NS == 2 ? (wave & 1) : p.side0;
   uint32_t wofs[NSET];
   int rgs[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    rgs[r] = (rt * WAVES + wave) * R + r;
+    rgs[r] = (rt * RPW + (NS == 2 ? wave >> 1 : wave)) * R + r;
     const int rgc = rgs[r] < p.nrg ? rgs[r] : p.nrg - 1;  // idle streams read a valid tile
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-      wofs[r * NS + s] = (((uint32_t)rgc * p.nst + st0) * p.nsw + (NS == 2 ? s : p.side0)) * F::ST_BYTES;
+    wofs[r] = (((uint32_t)rgc * p.nst + st0) * p.nsw + side) * F::ST_BYTES;
   }
   const uint32_t lq = lane * 16, ls = F::SC_OFS + lane * 8;
 
@@ -605,6 +606,20 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     return;
   }
 
+  floatx4_t up[NSET];  // SwiGLU: the up side from the partner wave
+  if constexpr (NS == 2 && EPI == GEMV_EPI_SWIGLU) {
+    __shared__ floatx4_t s_up[WAVES / 2][R][64];
+    if (wave & 1) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) s_up[wave >> 1][r][lane] = res[r];
+    }
+    __syncthreads();
+    if (wave & 1) return;  // the gate wave stores the pair's output
+#pragma unroll
+    for (int r = 0; r < R; ++r) up[r] = s_up[wave >> 1][r][lane];
+  }
+  float *const y0 = (NS == 2 && EPI == GEMV_EPI_PAIR && (wave & 1)) ? o.y1 : o.y;  // PAIR: each side its own output
+
   float sq[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of the row tile's sum of squares
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -613,15 +628,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     float v[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float a0 = res[r * NS][e];
-      v[e] = (EPI == GEMV_EPI_SWIGLU) ? silu_f(a0) * res[r * NS + NS - 1][e] : a0;
+      const float a0 = res[r][e];
+      if constexpr (NS == 2 && EPI == GEMV_EPI_SWIGLU) v[e] = silu_f(a0) * up[r][e];
+      else v[e] = a0;
     }
-    if (o.y && o.accumulate) {  // all residual loads in flight together
+    if (y0 && o.accumulate) {  // all residual loads in flight together
       float old[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int c = g * 4 + e;
-        old[e] = c < p.B ? o.y[(size_t)c * o.ys + row] : 0.f;
+        old[e] = c < p.B ? y0[(size_t)c * o.ys + row] : 0.f;
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] += old[e];
@@ -630,9 +646,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     for (int e = 0; e < 4; ++e) {
       const int c = g * 4 + e;
       if (c >= p.B) continue;
-      if (o.y) o.y[(size_t)c * o.ys + row] = v[e];
+      if (y0) y0[(size_t)c * o.ys + row] = v[e];
       if (o.yh) o.yh[(size_t)c * p.M + row] = (_Float16)v[e];
-      if (EPI == GEMV_EPI_PAIR) o.y1[(size_t)c * o.ys + row] = res[r * NS + NS - 1][e];
       sq[e] = fmaf(v[e], v[e], sq[e]);
     }
   }
@@ -943,7 +958,10 @@ void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
   // two, measured faster on every 27B-shape matrix (e.g. the 16480 x 5120
   // GDN input projection at B=8: 14.8 vs 19.1 us).
   const int Rs = 1;
-  const int nrt = (w->nrg + WAVES * Rs - 1) / (WAVES * Rs);
+  // An interleaved pair is computed with the two sides on a wave pair: half
+  // the row groups per workgroup.
+  const int rpw = w->nside == 2 ? WAVES / 2 : WAVES;
+  const int nrt = (w->nrg + rpw * Rs - 1) / (rpw * Rs);
   const int nrd = w->nst;                            // rounds of K
   int S = (ctx->wg_target + nrt - 1) / nrt;
   if (S > nrd / 2) S = nrd / 2;                      // keep >= 2 rounds per split
@@ -989,7 +1007,8 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   p.cnt = ctx->counters;
   p.out = out;
   const int R = w->rows;
-  const int nrt = (w->nrg + WAVES * R - 1) / (WAVES * R);
+  const int rpw = nsides == 2 ? WAVES / 2 : WAVES;  // row groups per workgroup
+  const int nrt = (w->nrg + rpw * R - 1) / (rpw * R);
   if (epi == GEMV_EPI_ARGMAX) {
     // The argmax needs final row values in one workgroup: no K split.
     if (p.S != 1) {
