@@ -238,7 +238,10 @@ def extra_leg(steps: int, warmup: int) -> dict:
                        steps, warmup, stream)
     out["c3_gdn_48x128_b8"] = {"ms": ms, "GB_s": C3_BYTES / (ms * 1e-3) / 1e9,
                                "frac_of_peak": C3_BYTES / (ms * 1e-3) / 1e9 / PEAK_GBS,
-                               "launches": "gdn block (conv + delta rule + snapshots)"}
+                               "launches": "gdn block: conv, delta rule (8 positions), gated norm",
+                               "note": "GB/s over the workload's algorithmic bytes, which count 8 per-position "
+                                       "state snapshots (25.2 MB); this build keeps two base states and replays "
+                                       "an accepted prefix instead, so its HBM traffic is ~7.8 MB per block"}
     for G in Gs:
         G.free()
     return {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in out.items()}

@@ -363,16 +363,17 @@ int cwen_gdn_create(cwen_ctx *ctx, int nkh, int nvh, int dk, cwen_gdn **out) {
   g->C = (2 * nkh + nvh) * dk;
   g->nslot = CWEN_BMAX + 1;
   const size_t sf = (size_t)nvh * dk * dk, hf = (size_t)g->C * 3;
-  if (hipMalloc((void **)&g->S, sf * g->nslot * sizeof(float)) != hipSuccess ||
+  if (hipMalloc((void **)&g->S, sf * 2 * sizeof(float)) != hipSuccess ||
       hipMalloc((void **)&g->H, hf * g->nslot * sizeof(float)) != hipSuccess ||
-      hipMalloc((void **)&g->xc, (size_t)CWEN_BMAX * g->C * sizeof(float)) != hipSuccess ||
+      hipMalloc((void **)&g->xc, (size_t)2 * CWEN_BMAX * g->C * sizeof(float)) != hipSuccess ||
+      hipMalloc((void **)&g->gates, (size_t)2 * CWEN_BMAX * 2 * nvh * sizeof(float)) != hipSuccess ||
       hipMalloc((void **)&g->ob, (size_t)CWEN_BMAX * nvh * dk * sizeof(float)) != hipSuccess ||
-      hipMalloc((void **)&g->dcur, sizeof(int)) != hipSuccess) {
+      hipMalloc((void **)&g->ctl, 4 * sizeof(int)) != hipSuccess) {
     cwen_gdn_free(g);
     return CWEN_ENOMEM;
   }
-  g->own_dcur = 1;
-  if (hipMemset(g->dcur, 0, sizeof(int)) != hipSuccess || hipMemset(g->S, 0, sf * sizeof(float)) != hipSuccess ||
+  g->own_ctl = 1;
+  if (hipMemset(g->ctl, 0, 4 * sizeof(int)) != hipSuccess || hipMemset(g->S, 0, sf * sizeof(float)) != hipSuccess ||
       hipMemset(g->H, 0, hf * sizeof(float)) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
     cwen_gdn_free(g);
     return CWEN_EHIP;
@@ -385,26 +386,35 @@ int cwen_gdn_free(cwen_gdn *g) {
   if (!g) return CWEN_EINVAL;
   (void)hipSetDevice(g->ctx->device);
   (void)hipDeviceSynchronize();
-  if (g->S) (void)hipFree(g->S);
-  if (g->H) (void)hipFree(g->H);
-  if (g->xc) (void)hipFree(g->xc);
-  if (g->ob) (void)hipFree(g->ob);
-  if (g->dcur && g->own_dcur) (void)hipFree(g->dcur);
+  for (float *p : {g->S, g->H, g->xc, g->gates, g->ob, g->S_peek})
+    if (p) (void)hipFree(p);
+  if (g->ctl && g->own_ctl) (void)hipFree(g->ctl);
   free(g);
+  return CWEN_OK;
+}
+
+// Write the host copy of the control word to the device (after queued work).
+static int gdn_sync_ctl(cwen_gdn *g) {
+  CWEN_HIP_TRY(hipDeviceSynchronize());
+  const int c[4] = {g->cur, g->X, g->L, g->P};
+  CWEN_HIP_TRY(hipMemcpy(g->ctl, c, sizeof(c), hipMemcpyHostToDevice));
   return CWEN_OK;
 }
 
 int cwen_gdn_set_state(cwen_gdn *g, const float *S, const float *hist) {
   if (!g) return CWEN_EINVAL;
   CWEN_HIP_TRY(hipSetDevice(g->ctx->device));
+  CWEN_HIP_TRY(hipDeviceSynchronize());
   const size_t sf = (size_t)g->nvh * g->dk * g->dk, hf = (size_t)g->C * 3;
-  float *Sd = g->S + (size_t)g->cur * sf, *Hd = g->H + (size_t)g->cur * hf;
+  float *Sd = g->S + (size_t)g->X * sf, *Hd = g->H + (size_t)g->cur * hf;
   if (S) CWEN_HIP_TRY(hipMemcpy(Sd, S, sf * sizeof(float), hipMemcpyHostToDevice));
   else CWEN_HIP_TRY(hipMemset(Sd, 0, sf * sizeof(float)));
   if (hist) CWEN_HIP_TRY(hipMemcpy(Hd, hist, hf * sizeof(float), hipMemcpyHostToDevice));
   else CWEN_HIP_TRY(hipMemset(Hd, 0, hf * sizeof(float)));
-  CWEN_HIP_TRY(hipDeviceSynchronize());
+  g->L = 0;
   g->last_B = 0;
+  if (g->own_ctl) return gdn_sync_ctl(g);
+  CWEN_HIP_TRY(hipDeviceSynchronize());
   return CWEN_OK;
 }
 
@@ -413,8 +423,17 @@ int cwen_gdn_get_state(cwen_gdn *g, int pos, float *S, float *hist) {
   CWEN_HIP_TRY(hipSetDevice(g->ctx->device));
   CWEN_HIP_TRY(hipDeviceSynchronize());
   const size_t sf = (size_t)g->nvh * g->dk * g->dk, hf = (size_t)g->C * 3;
+  if (S) {
+    // After a block (uncommitted): its start state is base X and its inputs
+    // are in buffer P; otherwise the committed state is base X plus the
+    // replay of L positions of buffer P ^ 1.
+    const int L = g->last_B ? pos : g->L, buf = g->last_B ? g->P : (g->P ^ 1);
+    if (!g->S_peek && hipMalloc((void **)&g->S_peek, sf * sizeof(float)) != hipSuccess) return CWEN_ENOMEM;
+    int rc;
+    if ((rc = gdn_peek_launch(g, L, buf, g->S_peek, nullptr))) return rc;
+    CWEN_HIP_TRY(hipMemcpy(S, g->S_peek, sf * sizeof(float), hipMemcpyDeviceToHost));
+  }
   const int slot = (g->cur + pos) % g->nslot;
-  if (S) CWEN_HIP_TRY(hipMemcpy(S, g->S + (size_t)slot * sf, sf * sizeof(float), hipMemcpyDeviceToHost));
   if (hist) CWEN_HIP_TRY(hipMemcpy(hist, g->H + (size_t)slot * hf, hf * sizeof(float), hipMemcpyDeviceToHost));
   return CWEN_OK;
 }
@@ -422,26 +441,29 @@ int cwen_gdn_get_state(cwen_gdn *g, int pos, float *S, float *hist) {
 int cwen_gdn_block(cwen_ctx *ctx, cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
                    const float *decay, const float *beta, int gs, const float *kw, const float *wn,
                    float *out, int os, int B, void *stream) {
-  if (!ctx || !g || g->ctx != ctx || B < 1 || B > CWEN_BMAX) return CWEN_EINVAL;
+  if (!ctx || !g || g->ctx != ctx || B < 1 || B > CWEN_BMAX || !g->own_ctl) return CWEN_EINVAL;
   if (!qkv || !z || !decay || !beta || !kw || !wn || !out) return CWEN_EINVAL;
   if (!aligned16(kw) || !aligned16(wn) || !aligned16(out) || (os & 3)) return CWEN_EINVAL;
   const int zh = g->nvh * g->dk;
   if ((B > 1 && (qs < g->C || zs < zh || gs < g->nvh || os < zh)) || qs < 0 || zs < 0 || gs < 0 || os < 0)
     return CWEN_EINVAL;
-  int rc = gdn_block_launch(g, qkv, qs, z, zs, decay, beta, gs, kw, wn, out, os, B, (hipStream_t)stream);
-  if (rc == CWEN_OK) g->last_B = B;
+  // A block after an uncommitted one restarts from that block's start state
+  // (commit(0)): its inputs are dropped, no replay.
+  const int force_L0 = g->last_B > 0;
+  int rc = gdn_block_launch(g, qkv, qs, z, zs, decay, beta, gs, kw, wn, out, os, B, (hipStream_t)stream,
+                            nullptr, 0, nullptr, nullptr, force_L0);
+  if (rc == CWEN_OK) {
+    if (force_L0) g->L = 0;
+    g->last_B = B;
+  }
   return rc;
 }
 
 int cwen_gdn_commit(cwen_gdn *g, int n) {
-  if (!g || n < 0 || n > g->last_B || !g->own_dcur) return CWEN_EINVAL;
+  if (!g || n < 0 || n > g->last_B || !g->own_ctl) return CWEN_EINVAL;
   CWEN_HIP_TRY(hipSetDevice(g->ctx->device));
-  CWEN_HIP_TRY(hipDeviceSynchronize());  // blocks already queued read the old slot
-  const int cur = (g->cur + n) % g->nslot;
-  CWEN_HIP_TRY(hipMemcpy(g->dcur, &cur, sizeof(int), hipMemcpyHostToDevice));
-  g->cur = cur;
-  g->last_B = 0;
-  return CWEN_OK;
+  gdn_commit_host(g, n, g->last_B);
+  return gdn_sync_ctl(g);
 }
 
 }  // extern "C"

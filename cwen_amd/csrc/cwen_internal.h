@@ -49,18 +49,41 @@ struct cwen_weight {
   int rows;                 // row groups per wave (shape-only)
 };
 
-// GatedDeltaNet layer state: a ring of nslot snapshots of the recurrent state
-// [nvh][dk][dk] and the conv history [C][3]; slot `cur` is the current state.
+// GatedDeltaNet layer state (gdn.hip): the recurrent state [nvh][dk][dk] in
+// two base slots, the conv history [C][3] in a ring of nslot slots, and the
+// pending inputs of the last block for a replay.  The device control word
+// ctl[4] = {ring slot, base slot X, replay count L, pending parity P} is what
+// the kernels read; the host keeps a copy.
 struct cwen_gdn {
   cwen_ctx *ctx;
   int nkh, nvh, dk, C;
-  int nslot, cur;           // host copy of the current slot
-  int *dcur;                // device copy of the current slot (what the kernels read)
-  int own_dcur;             // dcur allocated by this object (else borrowed from a model)
-  int last_B;               // positions of the last block (commit bound)
-  float *S, *H;             // device slot rings
-  float *xc, *ob;           // scratch: post-conv values [BMAX][C], pre-norm outputs [BMAX][nvh*dk]
+  int nslot;
+  int cur, X, L, P;         // host copy of ctl
+  int *ctl;                 // device control word
+  int own_ctl;              // ctl allocated by this object (else part of a model's)
+  int last_B;               // positions of the last, uncommitted block (0: none)
+  float *S, *H;             // device: base states [2][nvh][dk][dk], history ring [nslot][C][3]
+  float *xc, *gates;        // pending post-conv values [2][BMAX][C], g and beta [2][BMAX][2][nvh]
+  float *ob;                // scratch: pre-norm outputs [BMAX][nvh*dk]
+  float *S_peek;            // scratch for cwen_gdn_get_state (allocated on first use)
 };
+// Host copy of committing n positions of a block of B (0: no block, no-op):
+// the ring slot moves by n; a whole block makes its end state (the other
+// base slot) current, a prefix leaves the start state current with n
+// positions to replay; the pending parity flips.  The model's device commit
+// (advance_kernel) applies the same rule to the device word.
+inline void gdn_commit_host(cwen_gdn *g, int n, int B) {
+  if (B == 0) return;
+  g->cur = (g->cur + n) % g->nslot;
+  if (n == B) {
+    g->X ^= 1;
+    g->L = 0;
+  } else {
+    g->L = n;
+  }
+  g->P ^= 1;
+  g->last_B = 0;
+}
 
 #define CWEN_HIP_TRY(expr)                                   \
   do {                                                       \
@@ -173,7 +196,10 @@ int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &
 int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
                      const float *decay, const float *beta, int gs, const float *kw, const float *wn,
                      float *out, int os, int B, hipStream_t st, _Float16 *outh = nullptr, int ohs = 0,
-                     const float *A = nullptr, const float *dt = nullptr);
+                     const float *A = nullptr, const float *dt = nullptr, int force_L0 = 0);
+// The state after replaying L positions of pending buffer buf from base slot
+// X into S_out (device, [nvh][dk][dk]).
+int gdn_peek_launch(const cwen_gdn *g, int L, int buf, float *S_out, hipStream_t st);
 
 // ------------------------------------------------------------ model.hip
 // Also writes each row's sum of squares to ssq[b] (one partial per column).

@@ -1,11 +1,11 @@
 // GatedDeltaNet block verify: the depthwise causal conv and the gated delta
-// rule across the B positions of a draft block, with the recurrent state and
-// the conv history snapshotted in HBM after every position.
+// rule across the B positions of a draft block, with rollback to any
+// accepted prefix.
 //
 // Reference semantics (run.c): conv1d_update 2183-2200, gdn_step 2014-2180
 // (+ l2norm_rows 401-423), as called position by position in
 // layer_linear_blk 2700-2704; snap_save / snap_load 2787-2809 and the
-// short-walk replay 4975-4988 are replaced by the snapshot ring.
+// short-walk replay 4975-4988 are replaced as below.
 //
 // Per position b (C = 2*nkh*dk + nvh*dk channels):
 //   conv:  x_c = st0*w0 + st1*w1 + st2*w2 + cur*w3 (no FMA contraction, the
@@ -17,21 +17,30 @@
 //   gated RMSNorm: out = wn * o * (1/sqrt(mean(o^2) + 1e-6)) * silu(z)
 // S is [hv][i][j], row i the key dimension, as in the reference.
 //
+// Rollback.  The conv history (3 floats per channel) is kept after every
+// position in a ring of CWEN_BMAX+1 slots; accepting n positions moves the
+// ring index.  The recurrent state (3.1 MB at 48 heads) has two base slots
+// and is not snapshotted per position: a block keeps its inputs (post-conv
+// values, g, beta) in a pending buffer and writes its end state to the other
+// slot.  Accepting the whole block makes the end state the base; accepting
+// n < B keeps the start state as the base, and the next block first replays
+// those n positions from the pending buffer (the same instructions as the
+// block itself, so the same bits) before its own.  The device control word
+// ctl = {ring slot, base slot, replay count, pending parity} is advanced by
+// the commit (cwen_gdn_commit, or the model's device commit).
+//
 // Design (gfx950): three launches on the caller's stream.
 //  1. conv: one thread per channel runs the B positions in order, writes the
-//     post-SiLU values to scratch and the history after every position to
-//     the snapshot ring.
+//     post-SiLU values to the pending buffer and the history after every
+//     position to the ring.
 //  2. recurrence: the delta rule is column-local (sk[j], delta[j] and o[j]
 //     read only column j), so a head's 128 columns split over 8 single-wave
-//     workgroups of 16 columns; 384 workgroups keep the per-position state
-//     snapshot (3 MB per position) spread over the whole chip.  A lane owns a
-//     4-column x 8-row block in registers for the whole block; a column sum
-//     is a 16-lane DPP reduction.  The state after each position is stored
-//     to snapshot slot (cur + 1 + b) mod NSLOT.
+//     workgroups of 16 columns (384 workgroups at 48 heads).  A lane owns a
+//     4-column x 8-row block of S in registers for the whole block; a column
+//     sum is a 16-lane DPP reduction.
 //  3. norm: one wave per (position, value head) applies the gated RMSNorm.
-// Accepting the first n positions is then the host-side move cur += n:
-// rollback reads nothing.  Every position runs the same instructions whatever
-// B is, so a block of B equals B single-position blocks bit for bit.
+// Every position runs the same instructions whatever B is, so a block of B
+// equals B single-position blocks bit for bit.
 #include "cwen_internal.h"
 
 namespace {
@@ -42,15 +51,18 @@ constexpr int COLS = 16;            // columns of a head per recurrence workgrou
 
 __device__ __forceinline__ float silu_ref(float x) { return x * (1.f / (1.f + expf(-x))); }
 
-// Slot ring: the state before the block is slot *cur; the state after
-// position b is written to slot (*cur + 1 + b) % nslot.  The slot is read on
-// the device, so a captured launch replays at any ring position.
+// Control word ctl[4] (device): ring slot, base slot X, replay count L,
+// pending parity P.  Block inputs go to pending buffer P; a replay reads
+// buffer P ^ 1 (the previous block's).
 struct GdnParams {
-  float *S_slots;             // state ring [nslot][nvh][DK][DK]
+  float *S_base;              // two base states [2][nvh][DK][DK]
   float *H_slots;             // conv history ring [nslot][C][3]
-  size_t s_floats, h_floats;  // floats per slot
-  const int *cur;             // device: current slot
+  size_t s_floats, h_floats;  // floats per state / history slot
+  const int *ctl;
   int nslot;
+  int force_L0;               // replay nothing (the previous block was not committed)
+  float *S_peek;              // peek: replay peek_L positions of buffer peek_buf from base X into S_peek, no block
+  int peek_L, peek_buf;
   const float *qkv; int qs;   // raw (pre-conv) qkv [B][qs]
   const float *z; int zs;     // [B][zs]
   const float *decay, *beta; int gs;  // [B][gs]
@@ -59,7 +71,8 @@ struct GdnParams {
   float *out; int os;         // [B][os], nullable
   _Float16 *outh; int ohs;    // f16 copy [B][ohs], nullable
   const float *A, *dt;        // raw gates when non-null: decay = A*softplus(decay + dt), beta = sigmoid(beta)
-  float *xc;                  // scratch: post-conv values [B][C]
+  float *xc;                  // pending post-conv values [2][BMAX][C]
+  float *gates;               // pending g, beta [2][BMAX][2][nvh]
   float *ob;                  // scratch: pre-norm outputs [B][nvh*DK]
   int nkh, nvh, C, B;
 };
@@ -69,8 +82,9 @@ struct GdnParams {
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
   const int c = blockIdx.x * 256 + threadIdx.x;
   if (c >= p.C) return;
-  const int cur = *p.cur;
+  const int cur = p.ctl[0], P = p.ctl[3];
   const float *H_in = p.H_slots + (size_t)cur * p.h_floats;
+  float *xc = p.xc + (size_t)P * CWEN_BMAX * p.C;
   const float4 w = *(const float4 *)(p.kw + (size_t)c * 4);
   float h0 = H_in[(size_t)c * 3 + 0], h1 = H_in[(size_t)c * 3 + 1], h2 = H_in[(size_t)c * 3 + 2];
   float raw[MAXB];
@@ -84,7 +98,7 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
     const float x = __fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(h0, w.x), __fmul_rn(h1, w.y)), __fmul_rn(h2, w.z)),
                               __fmul_rn(xin, w.w));
     h0 = h1; h1 = h2; h2 = xin;
-    p.xc[(size_t)b * p.C + c] = silu_ref(x);
+    xc[(size_t)b * p.C + c] = silu_ref(x);
     float *hs = p.H_slots + (size_t)((cur + 1 + b) % p.nslot) * p.h_floats + (size_t)c * 3;
     hs[0] = h0; hs[1] = h1; hs[2] = h2;
   }
@@ -92,7 +106,9 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
 
 // 2. recurrence: workgroup (hv, slice) = one wave, columns
 // slice*16 .. slice*16+15 of head hv.  Lane: row group rg = lane & 15 (rows
-// 8rg..8rg+7), column group cg = lane >> 4 (4 columns).
+// 8rg..8rg+7), column group cg = lane >> 4 (4 columns).  The replay and the
+// block's own positions share one LDS layout per phase: q|k normalised, the
+// v slice, g and beta.
 __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
   __shared__ __align__(16) float qk[MAXB][2 * DK];   // normalised q | k per position
   __shared__ __align__(16) float vs[MAXB][COLS];
@@ -101,72 +117,122 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
   const int hv = blockIdx.x / (DK / COLS);
   const int slice = blockIdx.x % (DK / COLS);
   const int hk = hv % p.nkh;
-  const int B = p.B;
-  const int cur = *p.cur;
+  const bool peek = p.S_peek != nullptr;
+  const int X = p.ctl[1], P = p.ctl[3];
+  const int L = peek ? p.peek_L : (p.force_L0 ? 0 : p.ctl[2]);  // positions to replay
+  const int Pr = peek ? p.peek_buf : (P ^ 1);                   // their pending buffer
+  const int B = peek ? 0 : p.B;
   const int rg = lane & 15, cg = lane >> 4;
   const int i0 = rg * 8, j0 = slice * COLS + cg * 4;
+  const size_t xstride = (size_t)CWEN_BMAX * p.C;               // floats per pending buffer
+  const size_t gstride = (size_t)CWEN_BMAX * 2 * p.nvh;
 
   float4 s[8];
   {
-    const float *Sh = p.S_slots + (size_t)cur * p.s_floats + (size_t)hv * DK * DK;
+    const float *Sh = p.S_base + (size_t)X * p.s_floats + (size_t)hv * DK * DK;
 #pragma unroll
     for (int r = 0; r < 8; ++r) s[r] = *(const float4 *)(Sh + (size_t)(i0 + r) * DK + j0);
   }
-  if (lane < B) {
-    float dec = p.decay[(size_t)lane * p.gs + hv], bt = p.beta[(size_t)lane * p.gs + hv];
-    if (p.A) {  // run.c:2697-2698 (softplus, sigmoid: run.c:392-399)
-      const float x = dec + p.dt[hv];
-      dec = p.A[hv] * (x > 20.f ? x : logf(1.f + expf(x)));
-      bt = 1.f / (1.f + expf(-bt));
-    }
-    s_g[lane] = expf(dec);
-    s_beta[lane] = bt;
-  }
-  for (int e = lane; e < B * COLS; e += 64)
-    vs[e / COLS][e % COLS] = p.xc[(size_t)(e / COLS) * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
-  // q and k of key head hk, l2-normalised per position
-  for (int b = 0; b < B; ++b) {
-    const float *xq = p.xc + (size_t)b * p.C + hk * DK;
-    const float *xk = p.xc + (size_t)b * p.C + (p.nkh + hk) * DK;
-    const float q0 = xq[lane], q1 = xq[lane + 64], k0 = xk[lane], k1 = xk[lane + 64];
-    const float sq = 1.f / sqrtf(sum64(q0 * q0 + q1 * q1) + 1e-6f);
-    const float sk = 1.f / sqrtf(sum64(k0 * k0 + k1 * k1) + 1e-6f);
-    qk[b][lane] = q0 * sq; qk[b][lane + 64] = q1 * sq;
-    qk[b][DK + lane] = k0 * sk; qk[b][DK + lane + 64] = k1 * sk;
-  }
-  __syncthreads();
 
+  // Stage nb positions of pending buffer `buf` into LDS; gates from the
+  // buffer (replay) or computed from the raw inputs and saved (block).
+  auto stage = [&](int nb, int buf, bool fresh) {
+    const float *xc = p.xc + (size_t)buf * xstride;
+    float *gs = p.gates + (size_t)buf * gstride;
+    if (lane < nb) {
+      float g, bt;
+      if (fresh) {
+        float dec = p.decay[(size_t)lane * p.gs + hv];
+        bt = p.beta[(size_t)lane * p.gs + hv];
+        if (p.A) {  // run.c:2697-2698 (softplus, sigmoid: run.c:392-399)
+          const float x = dec + p.dt[hv];
+          dec = p.A[hv] * (x > 20.f ? x : logf(1.f + expf(x)));
+          bt = 1.f / (1.f + expf(-bt));
+        }
+        g = expf(dec);
+        if (slice == 0) {
+          gs[((size_t)lane * 2 + 0) * p.nvh + hv] = g;
+          gs[((size_t)lane * 2 + 1) * p.nvh + hv] = bt;
+        }
+      } else {
+        g = gs[((size_t)lane * 2 + 0) * p.nvh + hv];
+        bt = gs[((size_t)lane * 2 + 1) * p.nvh + hv];
+      }
+      s_g[lane] = g;
+      s_beta[lane] = bt;
+    }
+    for (int e = lane; e < nb * COLS; e += 64)
+      vs[e / COLS][e % COLS] = xc[(size_t)(e / COLS) * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
+    for (int b = 0; b < nb; ++b) {  // q and k of key head hk, l2-normalised
+      const float *xq = xc + (size_t)b * p.C + hk * DK;
+      const float *xk = xc + (size_t)b * p.C + (p.nkh + hk) * DK;
+      const float q0 = xq[lane], q1 = xq[lane + 64], k0 = xk[lane], k1 = xk[lane + 64];
+      const float sq = 1.f / sqrtf(sum64(q0 * q0 + q1 * q1) + 1e-6f);
+      const float sk = 1.f / sqrtf(sum64(k0 * k0 + k1 * k1) + 1e-6f);
+      qk[b][lane] = q0 * sq; qk[b][lane + 64] = q1 * sq;
+      qk[b][DK + lane] = k0 * sk; qk[b][DK + lane + 64] = k1 * sk;
+    }
+    __syncthreads();
+  };
+
+  // The delta rule over staged positions 0..nb-1; emit: write the outputs.
   const float scale = 1.f / sqrtf((float)DK);
-  for (int b = 0; b < B; ++b) {
-    const float g = s_g[b], beta = s_beta[b];
-    const float4 qa = *(const float4 *)&qk[b][i0], qb = *(const float4 *)&qk[b][i0 + 4];
-    const float4 ka = *(const float4 *)&qk[b][DK + i0], kb = *(const float4 *)&qk[b][DK + i0 + 4];
-    const float kr[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
-    const float qr[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-    float4 sk = {0.f, 0.f, 0.f, 0.f};
+  auto run = [&](int nb, bool emit) {
+    for (int b = 0; b < nb; ++b) {
+      const float g = s_g[b], beta = s_beta[b];
+      const float4 qa = *(const float4 *)&qk[b][i0], qb = *(const float4 *)&qk[b][i0 + 4];
+      const float4 ka = *(const float4 *)&qk[b][DK + i0], kb = *(const float4 *)&qk[b][DK + i0 + 4];
+      const float kr[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+      const float qr[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+      float4 sk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      s[r].x *= g; s[r].y *= g; s[r].z *= g; s[r].w *= g;
-      sk.x = fmaf(s[r].x, kr[r], sk.x); sk.y = fmaf(s[r].y, kr[r], sk.y);
-      sk.z = fmaf(s[r].z, kr[r], sk.z); sk.w = fmaf(s[r].w, kr[r], sk.w);
-    }
-    sk = (float4){sum16(sk.x), sum16(sk.y), sum16(sk.z), sum16(sk.w)};
-    const float4 v4 = *(const float4 *)&vs[b][cg * 4];
-    const float4 dl = {beta * (v4.x - sk.x), beta * (v4.y - sk.y), beta * (v4.z - sk.z), beta * (v4.w - sk.w)};
-    float4 o = {0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < 8; ++r) {
+        s[r].x *= g; s[r].y *= g; s[r].z *= g; s[r].w *= g;
+        sk.x = fmaf(s[r].x, kr[r], sk.x); sk.y = fmaf(s[r].y, kr[r], sk.y);
+        sk.z = fmaf(s[r].z, kr[r], sk.z); sk.w = fmaf(s[r].w, kr[r], sk.w);
+      }
+      sk = (float4){sum16(sk.x), sum16(sk.y), sum16(sk.z), sum16(sk.w)};
+      const float4 v4 = *(const float4 *)&vs[b][cg * 4];
+      const float4 dl = {beta * (v4.x - sk.x), beta * (v4.y - sk.y), beta * (v4.z - sk.z), beta * (v4.w - sk.w)};
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      s[r].x = fmaf(kr[r], dl.x, s[r].x); s[r].y = fmaf(kr[r], dl.y, s[r].y);
-      s[r].z = fmaf(kr[r], dl.z, s[r].z); s[r].w = fmaf(kr[r], dl.w, s[r].w);
-      o.x = fmaf(s[r].x, qr[r], o.x); o.y = fmaf(s[r].y, qr[r], o.y);
-      o.z = fmaf(s[r].z, qr[r], o.z); o.w = fmaf(s[r].w, qr[r], o.w);
+      for (int r = 0; r < 8; ++r) {
+        s[r].x = fmaf(kr[r], dl.x, s[r].x); s[r].y = fmaf(kr[r], dl.y, s[r].y);
+        s[r].z = fmaf(kr[r], dl.z, s[r].z); s[r].w = fmaf(kr[r], dl.w, s[r].w);
+      }
+      if (emit) {
+        float4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          o.x = fmaf(s[r].x, qr[r], o.x); o.y = fmaf(s[r].y, qr[r], o.y);
+          o.z = fmaf(s[r].z, qr[r], o.z); o.w = fmaf(s[r].w, qr[r], o.w);
+        }
+        o = (float4){sum16(o.x) * scale, sum16(o.y) * scale, sum16(o.z) * scale, sum16(o.w) * scale};
+        if (rg == 0) *(float4 *)(p.ob + (size_t)b * p.nvh * DK + hv * DK + j0) = o;
+      }
     }
-    o = (float4){sum16(o.x) * scale, sum16(o.y) * scale, sum16(o.z) * scale, sum16(o.w) * scale};
-    float *So = p.S_slots + (size_t)((cur + 1 + b) % p.nslot) * p.s_floats + (size_t)hv * DK * DK;
+  };
+  auto store = [&](float *S) {
+    float *So = S + (size_t)hv * DK * DK;
 #pragma unroll
     for (int r = 0; r < 8; ++r) *(float4 *)(So + (size_t)(i0 + r) * DK + j0) = s[r];
-    if (rg == 0) *(float4 *)(p.ob + (size_t)b * p.nvh * DK + hv * DK + j0) = o;
+  };
+
+  if (L > 0) {  // the previous block's accepted prefix
+    stage(L, Pr, false);
+    run(L, false);
+    if (peek) {
+      store(p.S_peek);
+      return;
+    }
+    store(p.S_base + (size_t)X * p.s_floats);   // this block's start state, in place
+    __syncthreads();                             // LDS reused below
+  } else if (peek) {
+    store(p.S_peek);
+    return;
   }
+  stage(B, P, true);
+  run(B, true);
+  store(p.S_base + (size_t)(X ^ 1) * p.s_floats);  // this block's end state
 }
 
 // 3. gated RMSNorm: one wave per (position, value head).
@@ -190,17 +256,27 @@ __global__ __launch_bounds__(64) void gdn_norm_kernel(GdnParams p) {
 
 }  // namespace
 
+static void fill_params(GdnParams &p, const cwen_gdn *g) {
+  p.s_floats = (size_t)g->nvh * DK * DK;
+  p.h_floats = (size_t)g->C * 3;
+  p.S_base = g->S;
+  p.H_slots = g->H;
+  p.ctl = g->ctl;
+  p.nslot = g->nslot;
+  p.force_L0 = 0;
+  p.S_peek = nullptr;
+  p.peek_L = p.peek_buf = 0;
+  p.xc = g->xc; p.gates = g->gates; p.ob = g->ob;
+  p.nkh = g->nkh; p.nvh = g->nvh; p.C = g->C;
+}
+
 int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
                      const float *decay, const float *beta, int gs, const float *kw, const float *wn,
                      float *out, int os, int B, hipStream_t st, _Float16 *outh, int ohs, const float *A,
-                     const float *dt) {
+                     const float *dt, int force_L0) {
   GdnParams p;
-  p.s_floats = (size_t)g->nvh * DK * DK;
-  p.h_floats = (size_t)g->C * 3;
-  p.S_slots = g->S;
-  p.H_slots = g->H;
-  p.cur = g->dcur;
-  p.nslot = g->nslot;
+  fill_params(p, g);
+  p.force_L0 = force_L0;
   p.qkv = qkv; p.qs = qs;
   p.z = z; p.zs = zs;
   p.decay = decay; p.beta = beta; p.gs = gs;
@@ -208,11 +284,24 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
   p.out = out; p.os = os;
   p.outh = outh; p.ohs = ohs;
   p.A = A; p.dt = dt;
-  p.xc = g->xc; p.ob = g->ob;
-  p.nkh = g->nkh; p.nvh = g->nvh; p.C = g->C; p.B = B;
+  p.B = B;
   hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((g->C + 255) / 256)), dim3(256), 0, st, p);
   hipLaunchKernelGGL(gdn_rec_kernel, dim3((unsigned)(g->nvh * (DK / COLS))), dim3(64), 0, st, p);
   hipLaunchKernelGGL(gdn_norm_kernel, dim3((unsigned)(g->nvh * B)), dim3(64), 0, st, p);
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}
+
+int gdn_peek_launch(const cwen_gdn *g, int L, int buf, float *S_out, hipStream_t st) {
+  GdnParams p;
+  fill_params(p, g);
+  p.S_peek = S_out;
+  p.peek_L = L;
+  p.peek_buf = buf;
+  p.qkv = nullptr; p.qs = 0; p.z = nullptr; p.zs = 0; p.decay = p.beta = nullptr; p.gs = 0;
+  p.kw = p.wn = nullptr; p.out = nullptr; p.os = 0; p.outh = nullptr; p.ohs = 0; p.A = p.dt = nullptr;
+  p.B = 0;
+  hipLaunchKernelGGL(gdn_rec_kernel, dim3((unsigned)(g->nvh * (DK / COLS))), dim3(64), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }

@@ -48,7 +48,7 @@ struct cwen_model {
   float *out_norm = nullptr;
   cwen_weight *head = nullptr;
   int pos = -1;                  // last filled slot (host copy)
-  int *ctl = nullptr;            // device: [0] last filled slot, [1] GDN ring slot
+  int *ctl = nullptr;            // device: [0] last filled slot, [1..4] the GDN layers' control word
   // With CWEN_GRAPHS=1 each (mode, B) block is captured once into a graph
   // and replayed: the launch shapes depend on (mode, B) and the weight
   // shapes only, the position and ring slot are read from ctl on the device.
@@ -129,25 +129,35 @@ int upload_w(cwen_model *m, int type, const void *data, const void *scales, int 
   return cwen_weight_upload(m->ctx, type, data, scales, ne0, ne1, out);
 }
 
-// A GEMV over the normalised residual stream: for blocks of up to 8
+// A GEMV over the normalised residual stream: for blocks of up to 4
 // columns the GEMV stages and normalises the f32 rows itself; for larger
-// blocks the f16 operand is written first (the 16-column normalising GEMV
-// needs more registers than 3 waves per SIMD allow).  Both give the same
-// operand bits.
+// blocks the f16 operand is written first by one small launch, which is
+// cheaper than every workgroup staging f32 rows (measured at B=8: the
+// gate/up GEMV takes 32.6 us normalising, 25.2 us on f16).  Both give the
+// same operand bits.
 int gemv_normed(cwen_model *m, const cwen_weight *w, int nsides, int epi, const GemvNorm &n, const GemvOut &o,
                 int B, hipStream_t st) {
-  if (B <= 8) return gemv_launch(m->ctx, w, nsides, 0, epi, nullptr, o, B, st, &n);
+  if (B <= 4) return gemv_launch(m->ctx, w, nsides, 0, epi, nullptr, o, B, st, &n);
   const int rc = norm_f16_launch(n, w->ne0, B, m->xh, w->ne0, st);
   return rc ? rc : gemv_launch(m->ctx, w, nsides, 0, epi, m->xh, o, B, st);
 }
 
-// Advance the device position and ring slot by the positions kept: n, or
-// res[0] + 1 (accepted drafts + bonus) when res is given, clamped to [1, nmax].
+// Device commit of a block of nmax positions: keep n, or res[0] + 1
+// (accepted drafts + bonus) when res is given, clamped to [1, nmax].  The
+// position and the GDN ring slot advance by n; the GDN base state and replay
+// count follow gdn_commit_host's rule.
 __global__ void advance_kernel(int *ctl, const int *res, int n, int nmax, int nslot) {
   if (res) n = res[0] + 1;
   n = n < 1 ? 1 : (n > nmax ? nmax : n);
   ctl[0] += n;
   ctl[1] = (ctl[1] + n) % nslot;
+  if (n == nmax) {
+    ctl[2] ^= 1;
+    ctl[3] = 0;
+  } else {
+    ctl[3] = n;
+  }
+  ctl[4] ^= 1;
 }
 
 enum { MODE_FWD = 0, MODE_FWD_HEAD = 1, MODE_VERIFY = 2 };
@@ -257,14 +267,10 @@ int run_block(cwen_model *m, const int *toks, int B, int mode, hipStream_t st) {
   return CWEN_OK;
 }
 
-// Host copy of the commit the block made on the device.
-void commit(cwen_model *m, int n) {
+// Host copy of the commit the block of B made on the device.
+void commit(cwen_model *m, int n, int B) {
   for (int l = 0; l < m->cfg.n_layers; ++l)
-    if (m->L[l].linear) {
-      cwen_gdn *g = m->L[l].gdn;
-      g->cur = (g->cur + n) % g->nslot;
-      g->last_B = 0;
-    }
+    if (m->L[l].linear) gdn_commit_host(m->L[l].gdn, n, B);
   m->pos += n;
 }
 
@@ -422,8 +428,8 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
   const int Zh = R.Zh, Qo = R.Qo2 / 2, Ko = R.Ko;
   const char *ge = getenv("CWEN_GRAPHS");
   m->use_graphs = ge && ge[0] == '1';
-  const int ctl0[2] = {-1, 0};
-  rc = dmalloc(&m->ctl, 2) ? CWEN_ENOMEM : CWEN_OK;
+  const int ctl0[5] = {-1, 0, 0, 0, 0};
+  rc = dmalloc(&m->ctl, 5) ? CWEN_ENOMEM : CWEN_OK;
   if (!rc && (hipMemcpy(m->ctl, ctl0, sizeof(ctl0), hipMemcpyHostToDevice) != hipSuccess ||
               hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking) != hipSuccess ||
               hipEventCreateWithFlags(&m->tok_ev, hipEventDisableTiming) != hipSuccess))
@@ -434,9 +440,9 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
     y.linear = !is_full(c, l);
     if (y.linear) {
       if (!(rc = cwen_gdn_create(ctx, c.gdn_nkh, c.gdn_nvh, 128, &y.gdn))) {
-        (void)hipFree(y.gdn->dcur);  // every layer's ring moves with the model's slot
-        y.gdn->dcur = m->ctl + 1;
-        y.gdn->own_dcur = 0;
+        (void)hipFree(y.gdn->ctl);  // every layer's state moves with the model's commit
+        y.gdn->ctl = m->ctl + 1;
+        y.gdn->own_ctl = 0;
         rc = gemv_alloc_q4(ctx, H, R.lin, &y.lin_in);
       }
     } else {
@@ -642,11 +648,12 @@ int cwen_model_reset(cwen_model *m) {
   CWEN_HIP_TRY(hipDeviceSynchronize());
   for (int l = 0; l < m->cfg.n_layers; ++l)
     if (m->L[l].linear) {
-      m->L[l].gdn->cur = 0;
-      int rc = cwen_gdn_set_state(m->L[l].gdn, nullptr, nullptr);
+      cwen_gdn *g = m->L[l].gdn;
+      g->cur = g->X = g->L = g->P = 0;
+      int rc = cwen_gdn_set_state(g, nullptr, nullptr);
       if (rc) return rc;
     }
-  const int ctl0[2] = {-1, 0};
+  const int ctl0[5] = {-1, 0, 0, 0, 0};
   CWEN_HIP_TRY(hipMemcpy(m->ctl, ctl0, sizeof(ctl0), hipMemcpyHostToDevice));
   m->pos = -1;
   return CWEN_OK;
@@ -667,7 +674,7 @@ int cwen_model_forward(cwen_model *m, const int *toks, int B, int want_argmax, i
     CWEN_HIP_TRY(hipStreamSynchronize(st));
     if (argmax_out) memcpy(argmax_out, m->hres + 2, (size_t)B * sizeof(int));
   }
-  commit(m, B);
+  commit(m, B, B);
   return CWEN_OK;
 }
 
@@ -681,7 +688,7 @@ int cwen_model_verify(cwen_model *m, const int *blk, int B, int *k_out, int *bon
   CWEN_HIP_TRY(hipStreamSynchronize(st));
   const int k = m->hres[0];
   if (k < 0 || k > B - 1) return CWEN_EHIP;
-  commit(m, k + 1);
+  commit(m, k + 1, B);
   if (k_out) *k_out = k;
   if (bonus_out) *bonus_out = m->hres[1];
   return CWEN_OK;

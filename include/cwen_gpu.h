@@ -134,19 +134,22 @@ int cwen_argmax_walk(cwen_ctx *ctx, const float *logits, int ls, int V, int B, c
 
 /* ---- GatedDeltaNet block verify ----
  * One linear-attention layer's recurrent state [nvh][dk][dk] (row = key
- * dimension) and conv history [C][3], C = (2*nkh + nvh)*dk, device-resident
- * in a ring of CWEN_BMAX+1 snapshot slots.  Replaces one layer's Srec/Cstate
- * and the snapshot copies SnapS/SnapC (run.c:171-172, 204, 3931-3932,
- * 2787-2809).  dk must be 128 and nvh a multiple of nkh (key head of value
- * head hv: hv % nkh, run.c:2027). */
+ * dimension) and conv history [C][3], C = (2*nkh + nvh)*dk, device-resident.
+ * Replaces one layer's Srec/Cstate and the snapshot copies SnapS/SnapC
+ * (run.c:171-172, 204, 3931-3932, 2787-2809): the history is kept after every
+ * position of a block; the state is kept at the block's start and end, and
+ * an accepted prefix is replayed (inside the next block) from the block's
+ * saved inputs, as the reference replays a short walk (run.c:4975-4988).
+ * dk must be 128 and nvh a multiple of nkh (key head of value head hv:
+ * hv % nkh, run.c:2027). */
 typedef struct cwen_gdn cwen_gdn;
 int cwen_gdn_create(cwen_ctx *ctx, int nkh, int nvh, int dk, cwen_gdn **out);
 int cwen_gdn_free(cwen_gdn *g);
 /* Current state from HOST arrays (NULL = zeros).  Synchronous. */
 int cwen_gdn_set_state(cwen_gdn *g, const float *S, const float *hist);
 /* Copy state `pos` to HOST arrays (either may be NULL): 0 = the current
- * state, p >= 1 = the snapshot after position p-1 of the last block (before
- * it is committed).  Synchronous. */
+ * state, p >= 1 = the state after position p-1 of the last block (before
+ * it is committed; replayed on the device).  Synchronous. */
 int cwen_gdn_get_state(cwen_gdn *g, int pos, float *S, float *hist);
 /* B positions of a verify block, in order, each exactly conv1d_update then
  * gdn_step of the reference (run.c:2183-2200, 2014-2180) as called by
@@ -155,17 +158,20 @@ int cwen_gdn_get_state(cwen_gdn *g, int pos, float *S, float *hist);
  * [b*gs + hv] the log-domain decay (g = exp(decay)) and beta [b*gs + hv],
  * kw [C][4] the conv taps, wn [dk] the gated-norm weight; out [b*os + i]
  * receives the gated-RMSNorm output (nvh*dk per position).  kw, wn and out
- * must be 16-byte aligned and os a multiple of 4.  The state after
- * each position is kept as a snapshot; the current state does not move until
- * cwen_gdn_commit. */
+ * must be 16-byte aligned and os a multiple of 4.  The state after any
+ * position stays reachable (cwen_gdn_get_state); the current state does not
+ * move until cwen_gdn_commit.  A block after an uncommitted one starts from
+ * that block's start state (as if it had been committed with n = 0). */
 int cwen_gdn_block(cwen_ctx *ctx, cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
                    const float *decay, const float *beta, int gs, const float *kw, const float *wn,
                    float *out, int os, int B, void *stream);
 /* Accept the first n positions (0..B) of the last block: the current state
  * becomes the snapshot after position n-1 (n = 0 keeps the state from
- * before the block).  Moves the ring index only (no state is copied);
- * waits for queued work first.  Replaces snap_load + the replaying
- * forward_block of a short walk (run.c:4975-4988) for this layer. */
+ * before the block).  No state is copied: the whole block makes the end
+ * state current; a prefix of n keeps the start state and the next block
+ * replays the n positions first.  Waits for queued work.  Replaces snap_load
+ * + the replaying forward_block of a short walk (run.c:4975-4988) for this
+ * layer. */
 int cwen_gdn_commit(cwen_gdn *g, int n);
 
 /* ---- the block-verify model ----
