@@ -23,7 +23,8 @@ enum { GEMV_Q4 = 0, GEMV_Q6K = 1, GEMV_Q8 = 2 };
 
 struct cwen_ctx {
   int device;
-  int wg_target;            // workgroups a GEMV launch aims for
+  int ncu;                  // compute units of the device
+  int wg_per_cu;            // GEMV workgroups per CU a split launch aims for
   _Float16 *xh;             // f16 activation scratch [BMAX][KMAX]
   _Float16 *hh;             // second f16 scratch (FFN hidden) [BMAX][KMAX]
   float *partials;          // split-K partial sums
@@ -33,6 +34,13 @@ struct cwen_ctx {
   unsigned long long *amax_keys;  // per-column argmax keys [CWEN_BMAX], zero between launches
   int *amax_cnt;            // argmax arrival counter, zero between launches
   int *res;                 // device result slots of the verify entry points [2 + CWEN_BMAX]
+};
+
+// A GEMV launch's work decomposition (gemv.hip): grid workgroups, the first
+// nsplit of which take pieces (S per tile, rps rounds each) of row tiles
+// tile0 .. tile0 + nsplit / S - 1; the others take whole row tiles.
+struct GemvGrid {
+  int grid, nsplit, S, rps, tile0;
 };
 
 struct cwen_weight {
@@ -45,7 +53,7 @@ struct cwen_weight {
   uint8_t *dev;             // tiled device data
   size_t bytes;             // device bytes of the tiled data
   size_t src_bytes;         // bytes of the reference layout (qs + scales)
-  int split, rps;           // K split across workgroups, super-tiles per split (shape-only)
+  GemvGrid cfg[2];          // decomposition for one side / both sides of a pair (shape-only)
   int rows;                 // row groups per wave (shape-only)
 };
 

@@ -53,7 +53,9 @@
 //    load in the loop is unconditional and issued in a fixed order (scales,
 //    staging, then tiles), so the in-order load counter only waits for the
 //    data being consumed.
+#include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "cwen_internal.h"
 
@@ -231,7 +233,10 @@ struct GemvParams {
   int nsw;             // sides stored per super-tile position (1 or 2)
   int side0;           // first side computed (NS == 1)
   int M, nrg, nst;
-  int S, rps;          // K split across workgroups, super-tiles (rounds) per split
+  // Workgroups [0, nsplit) each take one piece of a split row tile: piece
+  // i % S (rounds (i % S) * rps ..) of tile tile0 + i / S.  The others take
+  // whole row tiles 0, 1, ...
+  int nsplit, S, rps, tile0;
   const _Float16 *xh;  // activations f16 [B][K]
   uint32_t xbytes;     // B*K*2, or B*K*4 for XN (buffer range: columns >= B read as zero)
   // XN: the activations are RMSNorm(xf) applied while staging,
@@ -283,10 +288,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
-  const int rt = blockIdx.x / p.S;
-  const int sp = blockIdx.x - rt * p.S;
+  const bool split = (int)blockIdx.x < p.nsplit;
+  const int S = split ? p.S : 1;                   // pieces of this workgroup's row tile
+  const int rt = split ? p.tile0 + (int)blockIdx.x / p.S : (int)blockIdx.x - p.nsplit;
+  const int sp = split ? (int)blockIdx.x % p.S : 0;
   const int st0 = sp * p.rps;
-  const int nround = min(p.nst - st0, p.rps);
+  const int nround = split ? min(p.nst - st0, p.rps) : p.nst;
 
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.wbytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(XN ? (const void *)p.xf : (const void *)p.xh, p.xbytes);
@@ -507,7 +514,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 #pragma unroll
   for (int q = 0; q < NSET; ++q) res[q] = acc[q][0] + acc[q][1];
 
-  if (EPI != GEMV_EPI_ARGMAX && p.S > 1) {
+  if (EPI != GEMV_EPI_ARGMAX && S > 1) {
     // Publish this split's partials.  Agent-scope atomic stores reach the
     // device coherence point; the wait makes them complete before the
     // counter bump, and the last arriver reads them the same way.
@@ -515,7 +522,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     uint64_t *part = (uint64_t *)p.part;
 #pragma unroll
     for (int q = 0; q < NSET; ++q) {
-      const size_t base = ((((size_t)rt * WAVES + wave) * NSET + q) * p.S + sp) * 128 + lane * 2;
+      const size_t base = ((((size_t)rt * WAVES + wave) * NSET + q) * S + sp) * 128 + lane * 2;
       if (cols_on) {
         __hip_atomic_store(part + base, __builtin_bit_cast(uint64_t, (float2){res[q][0], res[q][1]}),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -526,7 +533,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // stores acknowledged
     __builtin_amdgcn_s_barrier();
     if (tid == 0)
-      s_last = __hip_atomic_fetch_add(p.cnt + rt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.S - 1;
+      s_last = __hip_atomic_fetch_add(p.cnt + rt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     if (!s_last) return;
@@ -537,14 +544,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int q = 0; q < NSET; ++q) res[q] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
     if (cols_on) {
-      for (int k0 = 0; k0 < p.S; k0 += KCH) {
+      for (int k0 = 0; k0 < S; k0 += KCH) {
         uint64_t lo[NSET][KCH], hi[NSET][KCH];
 #pragma unroll
         for (int q = 0; q < NSET; ++q) {
-          const size_t base = ((((size_t)rt * WAVES + wave) * NSET + q) * p.S) * 128 + lane * 2;
+          const size_t base = ((((size_t)rt * WAVES + wave) * NSET + q) * S) * 128 + lane * 2;
 #pragma unroll
           for (int u = 0; u < KCH; ++u) {
-            const size_t k = (size_t)min(k0 + u, p.S - 1);
+            const size_t k = (size_t)min(k0 + u, S - 1);
             lo[q][u] = __hip_atomic_load(part + base + k * 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             hi[q][u] = __hip_atomic_load(part + base + k * 128 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
@@ -553,7 +560,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
         for (int q = 0; q < NSET; ++q)
 #pragma unroll
           for (int u = 0; u < KCH; ++u)
-            if (k0 + u < p.S) {
+            if (k0 + u < S) {
               const float2 a = __builtin_bit_cast(float2, lo[q][u]);
               const float2 b = __builtin_bit_cast(float2, hi[q][u]);
               res[q] += (floatx4_t){a.x, a.y, b.x, b.y};
@@ -873,9 +880,8 @@ __global__ __launch_bounds__(256) void argmax_walk_kernel(const float *lg, long 
 }
 
 template <int FMT, int NS, int R, int EPI, int CB, bool XN>
-void launch_one(const GemvParams &p, int nrt, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_kernel<FMT, NS, R, EPI, CB, XN>), dim3((unsigned)(nrt * p.S)), dim3(64 * WAVES), 0,
-                     st, p);
+void launch_one(const GemvParams &p, int grid, hipStream_t st) {
+  hipLaunchKernelGGL((gemv_kernel<FMT, NS, R, EPI, CB, XN>), dim3((unsigned)grid), dim3(64 * WAVES), 0, st, p);
 }
 
 template <int FMT, int NS, int R, int EPI, bool XN>
@@ -950,26 +956,80 @@ int gemv_repack_part(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, i
   return CWEN_OK;
 }
 
+namespace {
+// Estimated length of a launch (microseconds at the 27B FFN shape's rates).
+// Workgroup i runs on CU i mod ncu (dispatch fills every CU's first slot,
+// then every second slot, ...).  A CU works through its workgroups' rounds,
+// plus one round of start-up each, at a rate that grows with the number of
+// workgroups it holds (measured: a lone four-wave workgroup is latency-bound);
+// the busiest CU sets the length.  Split remainder tiles add their
+// partial-sum hand-off, early in the launch: their pieces are dispatched
+// first, so they are the oldest workgroups on their CUs, which the hardware
+// serves first.
+constexpr double kSplitEarly = 0.3;
+double cu_rate(int wgs) {  // rounds per microsecond
+  return wgs <= 1 ? 0.6 : wgs == 2 ? 1.2 : wgs == 3 ? 1.35 : wgs == 4 ? 1.45 : 1.5;
+}
+double grid_cost(int ncu, int nst, const GemvGrid &c, double extra) {
+  std::vector<double> rounds((size_t)ncu, 0.0);
+  std::vector<int> wgs((size_t)ncu, 0);
+  for (int i = 0; i < c.grid; ++i) {
+    const int nr = i < c.nsplit ? std::min(nst - (i % c.S) * c.rps, c.rps) : nst;
+    rounds[(size_t)(i % ncu)] += nr + 1.0;
+    ++wgs[(size_t)(i % ncu)];
+  }
+  double worst = 0.0;
+  for (int k = 0; k < ncu; ++k)
+    if (wgs[(size_t)k]) worst = std::max(worst, rounds[(size_t)k] / cu_rate(wgs[(size_t)k]));
+  return worst + extra;
+}
+
+// Decomposition of ntile row tiles of nst rounds.  A launch with fewer tiles
+// than CUs splits every tile into S pieces (at least two rounds each) for
+// about wg_per_cu workgroups per CU.  A larger one takes whole tiles, except
+// that the ntile mod ncu remainder tiles are split into the pieces (chosen by
+// grid_cost) that spread them over the CUs: without that, the CUs that get
+// one whole tile more than the others would set the launch's length.
+GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
+  const size_t per_piece = (size_t)WAVES * 256;  // partial floats per tile and piece
+  GemvGrid best = {ntile, 0, 1, nst, 0};
+  if (ntile < ctx->ncu) {
+    const int target = ctx->wg_per_cu * ctx->ncu;
+    int S = std::min(std::max((target + ntile - 1) / ntile, 1), std::max(nst / 2, 1));
+    const int rps = (nst + S - 1) / S;
+    S = (nst + rps - 1) / rps;
+    const bool fits = (size_t)ntile * S * per_piece <= ctx->partials_floats && ntile <= ctx->ncounters;
+    if (S > 1 && fits) best = {ntile * S, ntile * S, S, rps, 0};
+    return best;
+  }
+  const int rem = ntile % ctx->ncu;
+  if (rem == 0) return best;
+  double best_cost = grid_cost(ctx->ncu, nst, best, 0.0);
+  for (int s = 2; s <= nst / 2; ++s) {
+    const int r = (nst + s - 1) / s, se = (nst + r - 1) / r;
+    if (se != s || (size_t)ntile * se * per_piece > ctx->partials_floats || ntile > ctx->ncounters) continue;
+    const GemvGrid part = {rem * se + ntile - rem, rem * se, se, r, ntile - rem};
+    const double c = grid_cost(ctx->ncu, nst, part, kSplitEarly);
+    if (c < best_cost) {
+      best = part;
+      best_cost = c;
+    }
+  }
+  return best;
+}
+}  // namespace
+
 // Launch shape from the weight's shape only (never from B), so every output
-// bit is independent of the block size.  rows: row groups per wave for
-// single-sided use; split: K split across workgroups; rps: super-tiles per split.
+// bit is independent of the block size.  One row group (16 rows) per wave:
+// fewer registers and split partials than two, measured faster on every
+// 27B-shape matrix.  An interleaved pair computed whole puts its two sides on
+// a wave pair: half the row groups per workgroup.
 void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
-  // One row group (16 rows) per wave: fewer registers and split partials than
-  // two, measured faster on every 27B-shape matrix (e.g. the 16480 x 5120
-  // GDN input projection at B=8: 14.8 vs 19.1 us).
-  const int Rs = 1;
-  // An interleaved pair is computed with the two sides on a wave pair: half
-  // the row groups per workgroup.
-  const int rpw = w->nside == 2 ? WAVES / 2 : WAVES;
-  const int nrt = (w->nrg + rpw * Rs - 1) / (rpw * Rs);
-  const int nrd = w->nst;                            // rounds of K
-  int S = (ctx->wg_target + nrt - 1) / nrt;
-  if (S > nrd / 2) S = nrd / 2;                      // keep >= 2 rounds per split
-  if (S < 1) S = 1;
-  const int rps = (nrd + S - 1) / S;
-  w->rows = Rs;
-  w->rps = rps;
-  w->split = (nrd + rps - 1) / rps;
+  w->rows = 1;
+  for (int ns = 1; ns <= w->nside; ++ns) {
+    const int rpw = ns == 2 ? WAVES / 2 : WAVES;
+    w->cfg[ns - 1] = choose_grid(ctx, (w->nrg + rpw - 1) / rpw, w->nst);
+  }
 }
 
 int gemv_row_tiles(const cwen_weight *w) { return (w->nrg + WAVES * w->rows - 1) / (WAVES * w->rows); }
@@ -990,8 +1050,7 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   p.M = w->ne1;
   p.nrg = w->nrg;
   p.nst = w->nst;
-  p.S = w->split;
-  p.rps = w->rps;
+  GemvGrid cfg = w->cfg[nsides - 1];
   p.xh = xh;
   const int xfs = nrm ? (B > 1 ? nrm->xs : w->ne0) : 0;
   p.xbytes = nrm ? (uint32_t)(((size_t)(B - 1) * xfs + w->ne0) * 4) : (uint32_t)((size_t)B * w->ne0 * 2);
@@ -1007,18 +1066,14 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   p.cnt = ctx->counters;
   p.out = out;
   const int R = w->rows;
-  const int rpw = nsides == 2 ? WAVES / 2 : WAVES;  // row groups per workgroup
-  const int nrt = (w->nrg + rpw * R - 1) / (rpw * R);
-  if (epi == GEMV_EPI_ARGMAX) {
-    // The argmax needs final row values in one workgroup: no K split.
-    if (p.S != 1) {
-      p.S = 1;
-      p.rps = w->nst;
-    }
-  } else if (p.S > 1) {
-    const size_t need = (size_t)nrt * WAVES * R * nsides * p.S * 256;
-    if (need > ctx->partials_floats || nrt > ctx->ncounters) return CWEN_ESCRATCH;
-  }
+  const int rpw = nsides == 2 ? WAVES / 2 : WAVES;  // row groups per row tile
+  const int ntile = (w->nrg + rpw * R - 1) / (rpw * R);
+  if (epi == GEMV_EPI_ARGMAX) cfg = {ntile, 0, 1, w->nst, 0};  // final row values in one workgroup
+  p.nsplit = cfg.nsplit;
+  p.S = cfg.S;
+  p.rps = cfg.rps;
+  p.tile0 = cfg.tile0;
+  const int nrt = cfg.grid;
   int rc = CWEN_EINVAL;
   if (w->fmt == GEMV_Q4) {
     if (nsides == 2 && epi == GEMV_EPI_PAIR) {
