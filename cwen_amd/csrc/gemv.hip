@@ -985,8 +985,8 @@ double grid_cost(int ncu, int nst, const GemvGrid &c, double extra) {
 }
 
 // Decomposition of ntile row tiles of nst rounds.  A launch with fewer tiles
-// than CUs splits every tile into S pieces (at least two rounds each) for
-// about wg_per_cu workgroups per CU.  A larger one takes whole tiles, except
+// than CUs splits every tile into S pieces (at least two rounds each) for at
+// most wg_per_cu workgroups per CU.  A larger one takes whole tiles, except
 // that the ntile mod ncu remainder tiles are split into the pieces (chosen by
 // grid_cost) that spread them over the CUs: without that, the CUs that get
 // one whole tile more than the others would set the launch's length.
@@ -995,7 +995,9 @@ GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
   GemvGrid best = {ntile, 0, 1, nst, 0};
   if (ntile < ctx->ncu) {
     const int target = ctx->wg_per_cu * ctx->ncu;
-    int S = std::min(std::max((target + ntile - 1) / ntile, 1), std::max(nst / 2, 1));
+    // At most wg_per_cu workgroups per CU: one more on some CUs than on the
+    // others would set the launch's length.
+    int S = std::min(std::max(target / ntile, 1), std::max(nst / 2, 1));
     const int rps = (nst + S - 1) / S;
     S = (nst + rps - 1) / rps;
     const bool fits = (size_t)ntile * S * per_piece <= ctx->partials_floats && ntile <= ctx->ncounters;
