@@ -141,7 +141,7 @@ __device__ __forceinline__ float silu_f(float x) { return x * (1.f / (1.f + expf
 
 // Row-tile partials of a column's sum of squares, at most 128, summed in a
 // fixed order: lane p adds partials p and p + 64, then one DPP tree over the
-// wave.  Every reader (GEMV staging, norm_f16) uses this, so they agree bit
+// wave.  Every reader (GEMV staging, post-scale) uses this, so they agree bit
 // for bit whatever the block size.
 constexpr int CWEN_MAX_PARTS = 128;
 __device__ __forceinline__ float sum_partials(const float *ssq, int npart, int col, int lane) {
@@ -167,6 +167,7 @@ struct GemvOut {
   int accumulate;    // y += result
   ArgmaxOut am;      // ARGMAX only
   float *ssq;        // STORE: per row tile, the sum of squares of the final y per column [row tile][CWEN_BMAX]
+  const float *nwh;  // with yh: the f16 copy holds y * nwh[row] (the next RMSNorm's weight), nullable
 };
 // f32 input staged by the GEMV itself: the activations are RMSNorm(x) with
 // weight w, applied while staging; the sum of squares per column comes from
@@ -195,8 +196,12 @@ int gemv_upload_part(cwen_weight *w, int type, const void *data, const void *sca
 void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w);
 // Row tiles of a launch over w: the number of ssq partials it writes.
 int gemv_row_tiles(const cwen_weight *w);
+// post (f16 operand only): the operand is w * x with x not yet normalised;
+// each output column c is scaled by 1 / sqrt(sum_p post->ssq[p][c] / K +
+// post->eps), completing the RMSNorm (post->x, post->w unused).
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
-                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvNorm *nrm = nullptr);
+                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvNorm *nrm = nullptr,
+                const GemvNorm *post = nullptr);
 int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st);
 int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &a, hipStream_t st);
 
@@ -210,12 +215,10 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
 int gdn_peek_launch(const cwen_gdn *g, int L, int buf, float *S_out, hipStream_t st);
 
 // ------------------------------------------------------------ model.hip
-// Also writes each row's sum of squares to ssq[b] (one partial per column).
+// Also writes each row's sum of squares to ssq[b] (one partial per column)
+// and, when xh is given, the f16 operand x * nw of the first RMSNorm.
 int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *toks, int B, int H, float *X,
-                 int xs, float *ssq, hipStream_t st);
-// The normalised f16 operand of a GemvNorm (non-plain) into Y [b*ys + k],
-// bit-identical to what the normalising GEMV stages.
-int norm_f16_launch(const GemvNorm &n, int K, int B, _Float16 *Y, int ys, hipStream_t st);
+                 int xs, float *ssq, hipStream_t st, _Float16 *xh = nullptr, const float *nw = nullptr);
 size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B);
 int attention_init();
 // `last` is a device int: the last filled cache slot before the block (the

@@ -248,6 +248,10 @@ struct GemvParams {
   const float *ssq;    // per-row-tile partial sums of squares [npart][CWEN_BMAX]
   int npart;           // 1..CWEN_MAX_PARTS
   float eps;
+  // Post-scale (f16 operand w * x, x not yet normalised): output column c is
+  // multiplied by 1 / sqrt(sum_p pss[p][c] / K + eps).
+  const float *pss;
+  int pnpart;
   int K, B;
   float *part;         // split-K partials
   int *cnt;            // per row-tile arrival counters (zero between launches)
@@ -295,6 +299,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   const int st0 = sp * p.rps;
   const int nround = split ? min(p.nst - st0, p.rps) : p.nst;
 
+  // Post-scale: the producer's partial sums of squares of every staged
+  // column, loaded first, so that waiting for them waits for nothing else
+  // (see psc below); ssq has CWEN_MAX_PARTS rows, so the loads need no guard.
+  float pa[CB], pb[CB];
+  if (p.pss) {
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      pa[c] = p.pss[lane * CWEN_BMAX + c];
+      pb[c] = p.pss[(lane + 64) * CWEN_BMAX + c];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.wbytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(XN ? (const void *)p.xf : (const void *)p.xh, p.xbytes);
   const bool plain = p.nw == nullptr;        // XN without a norm: conversion only
@@ -374,6 +390,23 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // issue the ring in slot order
+  }
+  // Post-scale: the scales of this lane's output columns 4g .. 4g+3, summed
+  // in sum_partials' order, while the first round's weights are in flight.
+  // Every column index is a compile-time constant and nothing branches per
+  // column (a private array indexed at run time would move to LDS; a uniform
+  // branch per column reloads kernel arguments).
+  float psc[4] = {1.f, 1.f, 1.f, 1.f};
+  if (p.pss) {
+    const float kf = (float)p.K, eps = p.eps;
+    const int nb = p.B, np = p.pnpart;
+#pragma unroll
+    for (int c = 0; c < CB; ++c) {
+      float v = lane < np ? pa[c] : 0.f;
+      if (lane + 64 < np) v += pb[c];
+      const float sc1 = 1.f / sqrtf(sum64(v) / kf + eps);
+      psc[c & 3] = ((c >> 2) == g && c < nb) ? sc1 : psc[c & 3];
+    }
   }
   // XN: column scales from the producer's partial sums of squares, summed
   // in a fixed order (sum_partials), so every workgroup and every block size
@@ -570,6 +603,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     if (tid == 0) __hip_atomic_store(p.cnt + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
+  if (p.pss) {
+#pragma unroll
+    for (int q = 0; q < NSET; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) res[q][e] *= psc[e];
+  }
   const GemvOut &o = p.out;
   if constexpr (EPI == GEMV_EPI_ARGMAX) {
     // Logits (optional), then the per-column argmax over this workgroup's
@@ -639,6 +678,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       if constexpr (NS == 2 && EPI == GEMV_EPI_SWIGLU) v[e] = silu_f(a0) * up[r][e];
       else v[e] = a0;
     }
+    const float nwr = o.yh && o.nwh ? o.nwh[row] : 1.f;  // loaded with the residual
     if (y0 && o.accumulate) {  // all residual loads in flight together
       float old[4];
 #pragma unroll
@@ -654,7 +694,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       const int c = g * 4 + e;
       if (c >= p.B) continue;
       if (y0) y0[(size_t)c * o.ys + row] = v[e];
-      if (o.yh) o.yh[(size_t)c * p.M + row] = (_Float16)v[e];
+      if (o.yh) o.yh[(size_t)c * p.M + row] = (_Float16)(o.nwh ? v[e] * nwr : v[e]);
       sq[e] = fmaf(v[e], v[e], sq[e]);
     }
   }
@@ -1037,7 +1077,9 @@ void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
 int gemv_row_tiles(const cwen_weight *w) { return (w->nrg + WAVES * w->rows - 1) / (WAVES * w->rows); }
 
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
-                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvNorm *nrm) {
+                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvNorm *nrm,
+                const GemvNorm *post) {
+  if (post && (nrm || !xh || !post->ssq || post->npart < 1 || post->npart > CWEN_MAX_PARTS)) return CWEN_EINVAL;
   if (nrm) {
     const bool plain = !nrm->w && !nrm->ssq && nrm->npart == 0;
     if (xh || !nrm->x || ((uintptr_t)nrm->x & 15) || (nrm->xs & 3) || (B > 1 && nrm->xs < w->ne0)) return CWEN_EINVAL;
@@ -1061,7 +1103,9 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   p.nw = nrm ? nrm->w : nullptr;
   p.ssq = nrm ? nrm->ssq : nullptr;
   p.npart = nrm ? nrm->npart : 0;
-  p.eps = nrm ? nrm->eps : 0.f;
+  p.eps = nrm ? nrm->eps : post ? post->eps : 0.f;
+  p.pss = post ? post->ssq : nullptr;
+  p.pnpart = post ? post->npart : 0;
   p.K = w->ne0;
   p.B = B;
   p.part = ctx->partials;

@@ -43,7 +43,8 @@ __device__ __forceinline__ float f16f(uint16_t h) { return (float)__builtin_bit_
 // ---- embedding: Q4_0 (GGUF blocks) or Q4_0RS (split scales) rows, exact
 // f32 dequant w = (n - 8) * d.  Grid: B, 256 threads, thread = block.
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uint16_t *sc, int type,
-                                                    const int *toks, int H, float *X, int xs, float *ssq) {
+                                                    const int *toks, int H, float *X, int xs, float *ssq,
+                                                    _Float16 *xh, const float *nw) {
   __shared__ float red[4];
   const int b = blockIdx.x;
   const size_t tok = (size_t)toks[b];
@@ -65,6 +66,10 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uin
       const float lo = (float)((int)(q[j] & 0xF) - 8) * d, hi = (float)((int)(q[j] >> 4) - 8) * d;
       dst[j] = lo;
       dst[j + 16] = hi;
+      if (xh) {
+        xh[(size_t)b * H + i * 32 + j] = (_Float16)(lo * nw[i * 32 + j]);
+        xh[(size_t)b * H + i * 32 + j + 16] = (_Float16)(hi * nw[i * 32 + j + 16]);
+      }
       sq = fmaf(lo, lo, sq);
       sq = fmaf(hi, hi, sq);
     }
@@ -72,36 +77,6 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uin
   // The row's sum of squares: the one partial a normalising GEMV reads.
   const float t = sum256(sq, red);
   if (threadIdx.x == 0) ssq[b] = t;
-}
-
-// ---- RMSNorm of B rows into the f16 GEMV operand, the column's sum of
-// squares taken from a producer's row-tile partials summed exactly as the
-// normalising GEMV staging sums them (sum_partials) and the same (w * x) * s
-// per element: the operand is bit-identical to
-// the one that staging builds (run.c:346-368 rmsnorm).  Grid B, 256
-// threads; K <= 8192, K % 4 == 0; all loads issued before the first use.
-constexpr int NORM_MAXV = 8;
-__global__ __launch_bounds__(256) void norm_f16_kernel(const float *X, int xs, const float *w, const float *ssq,
-                                                       int npart, int K, float eps, _Float16 *Y, int ys) {
-  const int b = blockIdx.x, lane = threadIdx.x & 63;
-  float4 x[NORM_MAXV], ww[NORM_MAXV];
-#pragma unroll
-  for (int j = 0; j < NORM_MAXV; ++j) {
-    const int i = (j * 256 + threadIdx.x) * 4;
-    if (i < K) {
-      x[j] = *(const float4 *)(X + (size_t)b * xs + i);
-      ww[j] = *(const float4 *)(w + i);
-    }
-  }
-  const float s = 1.f / sqrtf(sum_partials(ssq, npart, b, lane) / (float)K + eps);
-#pragma unroll
-  for (int j = 0; j < NORM_MAXV; ++j) {
-    const int i = (j * 256 + threadIdx.x) * 4;
-    if (i >= K) break;
-    const half2_t h0 = {(_Float16)(ww[j].x * x[j].x * s), (_Float16)(ww[j].y * x[j].y * s)};
-    const half2_t h1 = {(_Float16)(ww[j].z * x[j].z * s), (_Float16)(ww[j].w * x[j].w * s)};
-    *(uint2 *)(Y + (size_t)b * ys + i) = make_uint2(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1));
-  }
 }
 
 // ---- full attention, part 1: per (position, head) q/k RMSNorm (one shared
@@ -354,17 +329,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
 }  // namespace
 
 int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *toks, int B, int H, float *X,
-                 int xs, float *ssq, hipStream_t st) {
-  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)B), dim3(256), 0, st, qs, sc, type, toks, H, X, xs, ssq);
-  CWEN_HIP_TRY(hipGetLastError());
-  return CWEN_OK;
-}
-
-int norm_f16_launch(const GemvNorm &n, int K, int B, _Float16 *Y, int ys, hipStream_t st) {
-  if (K % 4 || K > NORM_MAXV * 1024 || (n.xs & 3) || (ys & 3) || n.npart < 1 || n.npart > CWEN_MAX_PARTS || !n.w || !n.ssq)
-    return CWEN_EINVAL;
-  hipLaunchKernelGGL(norm_f16_kernel, dim3((unsigned)B), dim3(256), 0, st, n.x, n.xs, n.w, n.ssq, n.npart, K, n.eps,
-                     Y, ys);
+                 int xs, float *ssq, hipStream_t st, _Float16 *xh, const float *nw) {
+  if ((xh == nullptr) != (nw == nullptr)) return CWEN_EINVAL;
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)B), dim3(256), 0, st, qs, sc, type, toks, H, X, xs, ssq, xh, nw);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }

@@ -63,7 +63,7 @@ struct cwen_model {
   int *toks = nullptr, *res = nullptr;
   float *X = nullptr;            // residual stream [BMAX][H]
   float *ssq = nullptr;          // partial sums of squares of X [CWEN_MAX_PARTS][BMAX]
-  _Float16 *xh = nullptr;        // normalised f16 operand for blocks of more than 8 [BMAX][H]
+  _Float16 *xh = nullptr;        // f16 operand x * w of the next RMSNorm [BMAX][H]
   float *lin = nullptr;           // GDN layer input GEMV out [BMAX][lin_rows]
   _Float16 *gh = nullptr;        // GDN output f16 [BMAX][nvh*dk]
   float *att = nullptr;           // attention input GEMV out [BMAX][att_rows]
@@ -129,19 +129,6 @@ int upload_w(cwen_model *m, int type, const void *data, const void *scales, int 
   return cwen_weight_upload(m->ctx, type, data, scales, ne0, ne1, out);
 }
 
-// A GEMV over the normalised residual stream: for blocks of up to 4
-// columns the GEMV stages and normalises the f32 rows itself; for larger
-// blocks the f16 operand is written first by one small launch, which is
-// cheaper than every workgroup staging f32 rows (measured at B=8: the
-// gate/up GEMV takes 32.6 us normalising, 25.2 us on f16).  Both give the
-// same operand bits.
-int gemv_normed(cwen_model *m, const cwen_weight *w, int nsides, int epi, const GemvNorm &n, const GemvOut &o,
-                int B, hipStream_t st) {
-  if (B <= 4) return gemv_launch(m->ctx, w, nsides, 0, epi, nullptr, o, B, st, &n);
-  const int rc = norm_f16_launch(n, w->ne0, B, m->xh, w->ne0, st);
-  return rc ? rc : gemv_launch(m->ctx, w, nsides, 0, epi, m->xh, o, B, st);
-}
-
 // Device commit of a block of nmax positions: keep n, or res[0] + 1
 // (accepted drafts + bonus) when res is given, clamped to [1, nmax].  The
 // position and the GDN ring slot advance by n; the GDN base state and replay
@@ -170,45 +157,53 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
   cwen_ctx *ctx = m->ctx;
   const int H = c.d_model, I = c.d_ffn;
   int rc;
-  // The residual stream X is normalised inside the GEMVs that read it: each
-  // producer of X (embed, the accumulating GEMVs) leaves per-row-tile sums
-  // of squares in m->ssq, `npart` of them, for the next consumer.
-  if ((rc = embed_launch(m->emb_qs, m->emb_sc, m->emb_type, m->toks, B, H, m->X, H, m->ssq, st))) return rc;
+  // RMSNorm of the residual stream X, split between producer and consumer:
+  // each producer of X (embed, the accumulating GEMVs) also writes the f16
+  // operand x * w of the next norm (weight w) to m->xh, and per-row-tile
+  // sums of squares of x to m->ssq (`npart` of them); the consuming GEMV
+  // scales its outputs by each column's 1 / rms.  Every block size takes
+  // this one path, so blocks and single positions agree bit for bit.
+  if ((rc = embed_launch(m->emb_qs, m->emb_sc, m->emb_type, m->toks, B, H, m->X, H, m->ssq, st, m->xh,
+                         m->L[0].attn_norm)))
+    return rc;
   int npart = 1;
   for (int l = 0; l < c.n_layers; ++l) {
     Layer &y = m->L[l];
-    const GemvNorm n1 = {m->X, y.attn_norm, m->ssq, npart, c.rms_eps, H};
+    const GemvNorm n1 = {nullptr, nullptr, m->ssq, npart, c.rms_eps, H};
     const cwen_weight *wout;
     if (y.linear) {
       const Rows r = rows_of(c);
       GemvOut o1 = {m->lin, nullptr, nullptr, r.lin, 0};
-      if ((rc = gemv_normed(m, y.lin_in, 1, GEMV_EPI_STORE, n1, o1, B, st))) return rc;
+      if ((rc = gemv_launch(ctx, y.lin_in, 1, 0, GEMV_EPI_STORE, m->xh, o1, B, st, nullptr, &n1))) return rc;
       const float *qkv = m->lin, *z = m->lin + r.C, *ga = m->lin + r.o_alpha, *gb = m->lin + r.o_beta;
       if ((rc = gdn_block_launch(y.gdn, qkv, r.lin, z, r.lin, ga, gb, r.lin, y.ssm_conv, y.ssm_norm, nullptr, 0, B,
                                  st, m->gh, r.Zh, y.ssm_a, y.ssm_dt)))
         return rc;
-      GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
+      GemvOut o5 = {m->X, nullptr, m->xh, H, 1};
       o5.ssq = m->ssq;
+      o5.nwh = y.post_norm;
       if ((rc = gemv_launch(ctx, y.ssm_out, 1, 0, GEMV_EPI_STORE, m->gh, o5, B, st))) return rc;
       wout = y.ssm_out;
     } else {
       const Rows r = rows_of(c);
       GemvOut o1 = {m->att, nullptr, nullptr, r.att, 0};
-      if ((rc = gemv_normed(m, y.att_in, 1, GEMV_EPI_STORE, n1, o1, B, st))) return rc;
+      if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, m->xh, o1, B, st, nullptr, &n1))) return rc;
       if ((rc = attention_launch(m->att, r.att, m->att + r.Qo2, m->att + r.Qo2 + r.Ko, r.att, y.q_norm, y.k_norm,
                                  m->qbuf, y.K, y.V, m->ctl, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
                                  c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st)))
         return rc;
-      GemvOut o5 = {m->X, nullptr, nullptr, H, 1};
+      GemvOut o5 = {m->X, nullptr, m->xh, H, 1};
       o5.ssq = m->ssq;
+      o5.nwh = y.post_norm;
       if ((rc = gemv_launch(ctx, y.wo, 1, 0, GEMV_EPI_STORE, m->yh, o5, B, st))) return rc;
       wout = y.wo;
     }
-    const GemvNorm n2 = {m->X, y.post_norm, m->ssq, gemv_row_tiles(wout), c.rms_eps, H};
+    const GemvNorm n2 = {nullptr, nullptr, m->ssq, gemv_row_tiles(wout), c.rms_eps, H};
     GemvOut f1 = {nullptr, nullptr, m->hh, 0, 0};
-    GemvOut f2 = {m->X, nullptr, nullptr, H, 1};
+    GemvOut f2 = {m->X, nullptr, m->xh, H, 1};
     f2.ssq = m->ssq;
-    if ((rc = gemv_normed(m, y.ffn_gu, 2, GEMV_EPI_SWIGLU, n2, f1, B, st)) ||
+    f2.nwh = l + 1 < c.n_layers ? m->L[l + 1].attn_norm : m->out_norm;
+    if ((rc = gemv_launch(ctx, y.ffn_gu, 2, 0, GEMV_EPI_SWIGLU, m->xh, f1, B, st, nullptr, &n2)) ||
         (rc = gemv_launch(ctx, y.ffn_down, 1, 0, GEMV_EPI_STORE, m->hh, f2, B, st)))
       return rc;
     npart = gemv_row_tiles(y.ffn_down);
@@ -216,10 +211,10 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
   }
   if (mode != MODE_FWD) {
     const int E = mode == MODE_VERIFY ? B - 1 : 0;
-    const GemvNorm nh = {m->X, m->out_norm, m->ssq, npart, c.rms_eps, H};
+    const GemvNorm nh = {nullptr, nullptr, m->ssq, npart, c.rms_eps, H};
     GemvOut o = {m->logits, nullptr, nullptr, c.vocab, 0,
                  {ctx->amax_keys, ctx->amax_cnt, m->toks + 1, E, m->res}};
-    if ((rc = gemv_normed(m, m->head, 1, GEMV_EPI_ARGMAX, nh, o, B, st))) return rc;
+    if ((rc = gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, m->xh, o, B, st, nullptr, &nh))) return rc;
   }
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->ctl, mode == MODE_VERIFY ? m->res : nullptr, B, B,
                      CWEN_BMAX + 1);

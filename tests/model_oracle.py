@@ -8,8 +8,13 @@ T_F32, T_Q4_0RS, T_Q4_0RSI, T_Q6_K = 0, 101, 102, 14
 
 
 class OracleModel:
-    def __init__(self, O, cfg: dict, tensors):
+    """f16_inputs: round every GEMV input to f16 first -- the one precision
+    choice of the device path (its MFMA operands are f16), used by the tests
+    to measure how sensitive a position's logits are to that rounding."""
+
+    def __init__(self, O, cfg: dict, tensors, f16_inputs: bool = False):
         self.O, self.c = O, cfg
+        self.f16_inputs = f16_inputs
         self.g = {}
         self.t = {}
         for layer, tid, wtype, data, sc, ne0, ne1 in tensors:
@@ -34,6 +39,8 @@ class OracleModel:
 
     def mv(self, layer, tid, x, side=0):
         wtype, data, sc, ne0, ne1 = self.t[(layer, tid)]
+        if self.f16_inputs:
+            x = x.astype(np.float16).astype(np.float32)
         return self.O.gemvb(wtype, data, sc, ne0, ne1, x[None, :], side)[0]
 
     def f32(self, layer, tid):

@@ -4,9 +4,16 @@ on a small config of the same hybrid architecture.
 Checked:
   * forward parity: per-position logits of the device forward pass vs the
     oracle's serial forward composed from its C restatements
-    (tests/model_oracle.py).  Tolerance (stated): rel_err <= 1e-2 on the
-    logits; every GEMV and state on the path is within 1e-3 of the oracle
-    (their own tests), and the f16 operand rounding compounds over the layers.
+    (tests/model_oracle.py).  Tolerance (stated), per position p:
+        rel_err(device, oracle) <= 1e-2 + 2 * rel_err(oracle16, oracle)
+    where oracle16 is the same oracle with every GEMV input rounded to f16
+    (the device's operand precision).  Every GEMV and state on the path is
+    within 1e-3 of the oracle (their own tests); over the layers the f16
+    operand rounding compounds, and at an ill-conditioned position of this
+    random-init model (position 14 of the 70-token case) rounding the inputs
+    alone moves the oracle's own logits by 1.4e-2 -- in either direction,
+    depending on how the roundings fall.  The second term allows exactly
+    that measured spread, nothing else.
   * block == serial, bit for bit: one block of B positions gives the same
     logits as B single-position passes (the property spec == serial rests on).
   * verify with crafted drafts walks and rolls back exactly: accepted drafts
@@ -43,13 +50,24 @@ def env():
     torch.cuda.synchronize()
 
 
-def test_forward_parity_vs_oracle(env, oracle):
+def _oracle_logits(oracle, tensors, toks):
+    """The oracle's logits per position and the stated tolerance per position
+    (module docstring): 1e-2 plus twice the spread that rounding the GEMV
+    inputs to f16 causes in the oracle itself."""
     from model_oracle import OracleModel
-    gpu, ctx, m, tensors = env
     OM = OracleModel(oracle, CFG, tensors)
+    ref = np.stack([OM.step(t, p) for p, t in enumerate(toks)])
+    O16 = OracleModel(oracle, CFG, tensors, f16_inputs=True)
+    ref16 = np.stack([O16.step(t, p) for p, t in enumerate(toks)])
+    tol = np.array([1e-2 + 2 * rel_err(ref16[p], ref[p]) for p in range(len(toks))])
+    return ref, tol
+
+
+def test_forward_parity_vs_oracle(env, oracle):
+    gpu, ctx, m, tensors = env
     toks = synth.prompt_tokens(1, 12, CFG["vocab"])
     m.reset()
-    ref = np.stack([OM.step(t, p) for p, t in enumerate(toks)])
+    ref, tol = _oracle_logits(oracle, tensors, toks)
     got = []
     for b0, B in ((0, 5), (5, 7)):          # two blocks of different size
         am = m.forward(toks[b0:b0 + B])
@@ -59,7 +77,7 @@ def test_forward_parity_vs_oracle(env, oracle):
             assert am[b] == oracle.argmax(lg[b])   # the head's argmax is exact on its own logits
     got = np.concatenate(got)
     for p in range(len(toks)):
-        assert rel_err(got[p], ref[p]) <= 1e-2, (p, rel_err(got[p], ref[p]))
+        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
     assert m.pos == len(toks) - 1
 
 
@@ -68,12 +86,10 @@ def test_forward_parity_across_key_chunks(env, oracle):
     32-key chunk boundaries of the attention, so the chunk partials, their
     merge and the per-query masks inside a chunk are all exercised.  Same
     tolerance as the single-chunk parity test."""
-    from model_oracle import OracleModel
     gpu, ctx, m, tensors = env
-    OM = OracleModel(oracle, CFG, tensors)
     toks = synth.prompt_tokens(7, 70, CFG["vocab"])
     m.reset()
-    ref = np.stack([OM.step(t, p) for p, t in enumerate(toks)])
+    ref, tol = _oracle_logits(oracle, tensors, toks)
     got, b0 = [], 0
     for B in (16, 16, 3, 13, 16, 6):
         am = m.forward(toks[b0:b0 + B])       # with the head: logits are written
@@ -82,14 +98,15 @@ def test_forward_parity_across_key_chunks(env, oracle):
         b0 += B
     got = np.concatenate(got)
     for p in range(len(toks)):
-        assert rel_err(got[p], ref[p]) <= 1e-2, (p, rel_err(got[p], ref[p]))
+        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
 
 
 @pytest.mark.parametrize("B", [4, 8, 16])
 def test_block_equals_serial_bitwise(env, B):
-    """Blocks of more than 4 normalise the residual in a separate f16 pass,
-    smaller blocks (and the single positions) inside the GEMV staging: both
-    must give the same bits."""
+    """Every block size takes the same path (the producer writes the f16
+    operand x * w of the next RMSNorm, the consuming GEMV scales its output
+    columns by 1 / rms), so a block and its single positions agree bit for
+    bit."""
     gpu, ctx, m, _ = env
     toks = synth.prompt_tokens(2, 12 + B, CFG["vocab"])
     m.reset()
