@@ -78,10 +78,14 @@ struct GdnParams {
 };
 
 // 1. conv: thread = channel.  All loads of a channel are issued before its
-// first use.
+// first use.  A workgroup's 256 channels are two whole heads, all q/k or all
+// v (the q/k channels are 2 * nkh * 128); q and k are l2-normalised here
+// (run.c:401-423), once per position, so the recurrence and a later replay
+// read the same normalised values.
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
+  __shared__ float s_ss[4][MAXB];  // per wave and position: the wave's sum of squares
   const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= p.C) return;
+  if (c >= p.C) return;           // whole waves (C is a multiple of 128)
   const int cur = p.ctl[0], P = p.ctl[3];
   const float *H_in = p.H_slots + (size_t)cur * p.h_floats;
   float *xc = p.xc + (size_t)P * CWEN_BMAX * p.C;
@@ -98,9 +102,30 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
     const float x = __fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(h0, w.x), __fmul_rn(h1, w.y)), __fmul_rn(h2, w.z)),
                               __fmul_rn(xin, w.w));
     h0 = h1; h1 = h2; h2 = xin;
-    xc[(size_t)b * p.C + c] = silu_ref(x);
+    raw[b] = silu_ref(x);
     float *hs = p.H_slots + (size_t)((cur + 1 + b) % p.nslot) * p.h_floats + (size_t)c * 3;
     hs[0] = h0; hs[1] = h1; hs[2] = h2;
+  }
+  if (blockIdx.x * 256 < 2 * p.nkh * DK) {  // q / k heads: x / sqrt(sum x^2 + 1e-6)
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int b = 0; b < MAXB; ++b) {
+      if (b >= p.B) break;
+      const float t = sum64(raw[b] * raw[b]);
+      if (lane == 0) s_ss[wave][b] = t;
+    }
+    __syncthreads();
+    const int w0 = wave & ~1;  // the head's two waves, in order
+#pragma unroll
+    for (int b = 0; b < MAXB; ++b) {
+      if (b >= p.B) break;
+      raw[b] *= 1.f / sqrtf(s_ss[w0][b] + s_ss[w0 + 1][b] + 1e-6f);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < MAXB; ++b) {
+    if (b >= p.B) break;
+    xc[(size_t)b * p.C + c] = raw[b];
   }
 }
 
@@ -163,14 +188,13 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
     }
     for (int e = lane; e < nb * COLS; e += 64)
       vs[e / COLS][e % COLS] = xc[(size_t)(e / COLS) * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
-    for (int b = 0; b < nb; ++b) {  // q and k of key head hk, l2-normalised
+#pragma unroll
+    for (int b = 0; b < MAXB; ++b) {  // q and k of key head hk (l2-normalised by the conv)
+      if (b >= nb) break;
       const float *xq = xc + (size_t)b * p.C + hk * DK;
       const float *xk = xc + (size_t)b * p.C + (p.nkh + hk) * DK;
-      const float q0 = xq[lane], q1 = xq[lane + 64], k0 = xk[lane], k1 = xk[lane + 64];
-      const float sq = 1.f / sqrtf(sum64(q0 * q0 + q1 * q1) + 1e-6f);
-      const float sk = 1.f / sqrtf(sum64(k0 * k0 + k1 * k1) + 1e-6f);
-      qk[b][lane] = q0 * sq; qk[b][lane + 64] = q1 * sq;
-      qk[b][DK + lane] = k0 * sk; qk[b][DK + lane + 64] = k1 * sk;
+      qk[b][lane] = xq[lane]; qk[b][lane + 64] = xq[lane + 64];
+      qk[b][DK + lane] = xk[lane]; qk[b][DK + lane + 64] = xk[lane + 64];
     }
     __syncthreads();
   };
