@@ -228,10 +228,10 @@ static int check_w(const cwen_ctx *ctx, const cwen_weight *W) {
 // converts them itself (one launch); for larger blocks a separate conversion
 // into ctx->xh is faster (the f32 staging adds registers and L2 traffic to
 // every workgroup of the GEMV), measured on the FFN shapes.
-static int f32_operand(cwen_ctx *ctx, const float *X, int xs, int K, int B, hipStream_t st, GemvNorm *n,
+static int f32_operand(cwen_ctx *ctx, const float *X, int xs, int K, int B, hipStream_t st, GemvF32 *n,
                        const _Float16 **xh) {
   if (B <= 4) {
-    *n = {X, nullptr, nullptr, 0, 0.f, xs};
+    *n = {X, xs};
     *xh = nullptr;
     return CWEN_OK;
   }
@@ -253,7 +253,7 @@ int cwen_gemvb(cwen_ctx *ctx, const cwen_weight *W, int side, const float *X, in
   if (side < 0 || side >= W->nside) return CWEN_EINVAL;
   if ((rc = check_act(X, xs, W->ne0, B)) || (rc = check_out(Y, ys, W->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
-  GemvNorm x;
+  GemvF32 x;
   const _Float16 *xh;
   if ((rc = f32_operand(ctx, X, xs, W->ne0, B, st, &x, &xh))) return rc;
   GemvOut o = {Y, nullptr, nullptr, ys, 0};
@@ -269,7 +269,7 @@ int cwen_gemvb_pair(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs,
       (rc = check_out(YB, ys, W->ne1, B)))
     return rc;
   hipStream_t st = (hipStream_t)stream;
-  GemvNorm x;
+  GemvF32 x;
   const _Float16 *xh;
   if ((rc = f32_operand(ctx, X, xs, W->ne0, B, st, &x, &xh))) return rc;
   GemvOut o = {YA, YB, nullptr, ys, 0};
@@ -283,7 +283,7 @@ int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int x
   if (W->nside != 2) return CWEN_EINVAL;
   if ((rc = check_act(X, xs, W->ne0, B)) || (rc = check_out(H, hs, W->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
-  GemvNorm x;
+  GemvF32 x;
   const _Float16 *xh;
   if ((rc = f32_operand(ctx, X, xs, W->ne0, B, st, &x, &xh))) return rc;
   GemvOut o = {H, nullptr, nullptr, hs, 0};
@@ -322,7 +322,7 @@ int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd,
     return CWEN_EINVAL;
   if ((rc = check_act(X, xs, Wgu->ne0, B)) || (rc = check_out(Y, ys, Wd->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
-  GemvNorm x;
+  GemvF32 x;
   const _Float16 *xh;
   if ((rc = f32_operand(ctx, X, xs, Wgu->ne0, B, st, &x, &xh))) return rc;
   GemvOut o1 = {nullptr, nullptr, ctx->hh, 0, 0};
@@ -340,7 +340,7 @@ int cwen_head_verify(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs
   if (E < 0 || E > B - 1 || (E > 0 && !drafts)) return CWEN_EINVAL;
   if (logits && (rc = check_out(logits, ls, W->ne1, B))) return rc;
   hipStream_t st = (hipStream_t)stream;
-  GemvNorm x;
+  GemvF32 x;
   const _Float16 *xh;
   if ((rc = f32_operand(ctx, X, xs, W->ne0, B, st, &x, &xh))) return rc;
   GemvOut o = {logits, nullptr, nullptr, ls, 0, {ctx->amax_keys, ctx->amax_cnt, drafts, E, res}};

@@ -139,16 +139,8 @@ __device__ __forceinline__ float sum64(float v) {
 // run.c:378-384 silu_one: x * (1 / (1 + exp(-x)))
 __device__ __forceinline__ float silu_f(float x) { return x * (1.f / (1.f + expf(-x))); }
 
-// Row-tile partials of a column's sum of squares, at most 128, summed in a
-// fixed order: lane p adds partials p and p + 64, then one DPP tree over the
-// wave.  Every reader (GEMV staging, post-scale) uses this, so they agree bit
-// for bit whatever the block size.
+// Row-tile partials of a column's sum of squares: at most 128 per column.
 constexpr int CWEN_MAX_PARTS = 128;
-__device__ __forceinline__ float sum_partials(const float *ssq, int npart, int col, int lane) {
-  float v = lane < npart ? ssq[lane * CWEN_BMAX + col] : 0.f;
-  if (lane + 64 < npart) v += ssq[(lane + 64) * CWEN_BMAX + col];
-  return sum64(v);
-}
 
 // ------------------------------------------------------------ gemv.hip
 enum { GEMV_EPI_STORE = 0, GEMV_EPI_PAIR = 1, GEMV_EPI_SWIGLU = 2, GEMV_EPI_ARGMAX = 3 };
@@ -169,17 +161,18 @@ struct GemvOut {
   float *ssq;        // STORE: per row tile, the sum of squares of the final y per column [row tile][CWEN_BMAX]
   const float *nwh;  // with yh: the f16 copy holds y * nwh[row] (the next RMSNorm's weight), nullable
 };
-// f32 input staged by the GEMV itself: the activations are RMSNorm(x) with
-// weight w, applied while staging; the sum of squares per column comes from
-// the producer's ssq partials (npart of them).  Plain conversion to the f16
-// operand when w and ssq are null and npart is 0.
-struct GemvNorm {
+// f32 activations that the GEMV converts to its f16 operand while staging.
+struct GemvF32 {
   const float *x;    // [c*xs + k], 16-byte aligned, xs % 4 == 0
-  const float *w;    // [K]
-  const float *ssq;  // [npart][CWEN_BMAX]
-  int npart;
-  float eps;
   int xs;            // row stride of x in floats (>= K when B > 1)
+};
+// RMSNorm split between producer and consumer: the f16 operand holds w * x
+// (x not yet normalised) and output column c is multiplied by
+// 1 / sqrt(sum_p ssq[p][c] / K + eps), the partials summed in a fixed order.
+struct GemvPost {
+  const float *ssq;  // [npart][CWEN_BMAX]
+  int npart;         // 1 .. CWEN_MAX_PARTS
+  float eps;
 };
 int gemv_fmt_of(int type);
 size_t gemv_st_bytes(int fmt);
@@ -200,8 +193,8 @@ int gemv_row_tiles(const cwen_weight *w);
 // each output column c is scaled by 1 / sqrt(sum_p post->ssq[p][c] / K +
 // post->eps), completing the RMSNorm (post->x, post->w unused).
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
-                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvNorm *nrm = nullptr,
-                const GemvNorm *post = nullptr);
+                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvF32 *xf = nullptr,
+                const GemvPost *post = nullptr);
 int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st);
 int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &a, hipStream_t st);
 

@@ -238,35 +238,25 @@ struct GemvParams {
   // whole row tiles 0, 1, ...
   int nsplit, S, rps, tile0;
   const _Float16 *xh;  // activations f16 [B][K]
-  uint32_t xbytes;     // B*K*2, or B*K*4 for XN (buffer range: columns >= B read as zero)
-  // XN: the activations are RMSNorm(xf) applied while staging,
-  // f16((nw[k] * x[k]) * s_c), s_c = 1 / sqrt(sum_p ssq[p][c] / K + eps);
-  // plain f16(x[k]) when nw is null.
-  const float *xf;     // f32 rows [c*xfs + k]
+  uint32_t xbytes;     // buffer range of the activations: columns >= B read as zero
+  const float *xf;     // XN: f32 rows [c*xfs + k], converted to f16 while staging
   int xfs;
-  const float *nw;     // norm weight [K], or null
-  const float *ssq;    // per-row-tile partial sums of squares [npart][CWEN_BMAX]
-  int npart;           // 1..CWEN_MAX_PARTS
-  float eps;
   // Post-scale (f16 operand w * x, x not yet normalised): output column c is
   // multiplied by 1 / sqrt(sum_p pss[p][c] / K + eps).
   const float *pss;
   int pnpart;
+  float eps;
   int K, B;
   float *part;         // split-K partials
   int *cnt;            // per row-tile arrival counters (zero between launches)
   GemvOut out;
 };
 
-// 8 f32 activations x and norm weights w -> 8 f16 (w * x) * s (the RMSNorm
-// of run.c:346-368 rmsnorm, rounded to the f16 operand).
-__device__ __forceinline__ uint4 norm8(const uint4 (&x)[2], const float4 *w, float s) {
+// 8 f32 activations -> 8 f16, rounded to nearest.
+__device__ __forceinline__ uint4 cvt8(const uint4 (&x)[2]) {
   const float4 x0 = __builtin_bit_cast(float4, x[0]), x1 = __builtin_bit_cast(float4, x[1]);
-  const float4 w0 = w[0], w1 = w[1];
-  const half2_t h0 = {(_Float16)(w0.x * x0.x * s), (_Float16)(w0.y * x0.y * s)};
-  const half2_t h1 = {(_Float16)(w0.z * x0.z * s), (_Float16)(w0.w * x0.w * s)};
-  const half2_t h2 = {(_Float16)(w1.x * x1.x * s), (_Float16)(w1.y * x1.y * s)};
-  const half2_t h3 = {(_Float16)(w1.z * x1.z * s), (_Float16)(w1.w * x1.w * s)};
+  const half2_t h0 = {(_Float16)x0.x, (_Float16)x0.y}, h1 = {(_Float16)x0.z, (_Float16)x0.w};
+  const half2_t h2 = {(_Float16)x1.x, (_Float16)x1.y}, h3 = {(_Float16)x1.z, (_Float16)x1.w};
   return make_uint4(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
                     __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3));
 }
@@ -275,7 +265,7 @@ __device__ __forceinline__ uint4 norm8(const uint4 (&x)[2], const float4 *w, flo
 // the two waves of a wave pair take sides 0 and 1 of the same row groups and
 // combine them through LDS).  R: row groups per wave; each wave carries R
 // weight streams.  EPI: epilogue.  CB: activation columns staged (4, 8 or
-// 16; >= B).  XN: f32 activations staged (and normalised) by the kernel.
+// 16; >= B).  XN: f32 activations, converted to f16 while staging.
 template <int FMT, int NS, int R, int EPI, int CB, bool XN>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   using F = Fmt<FMT>;
@@ -313,9 +303,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   __builtin_amdgcn_sched_barrier(0);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.wbytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(XN ? (const void *)p.xf : (const void *)p.xh, p.xbytes);
-  const bool plain = p.nw == nullptr;        // XN without a norm: conversion only
-  const __amdgpu_buffer_rsrc_t nwr = make_rsrc(p.nw, (XN && !plain) ? (uint32_t)p.K * 4u : 0u);
-  const uint2 ones = {0x3f800000u, 0x3f800000u};
 
   // Weight streams of this wave: stream r is row group rgs[r], side `side`.
   const uint32_t sstride = (uint32_t)p.nsw * F::ST_BYTES;
@@ -343,11 +330,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     xofs[i] = (uint32_t)c * (uint32_t)(XN ? p.xfs : p.K) * XE + (uint32_t)st0 * xround + lane * 8 * XE;  // range-checked
     xslot[i] = c * 64 + (lane ^ c);
   }
-  // XN: the norm weights of a round (512 floats) pass through LDS, two
-  // rounds ahead: thread t loads floats 2t, 2t+1 of round r + 2 during round
-  // r and stores them into nwl[r % 2] at its end.
-  __shared__ float2 nwl[XN ? 2 : 1][XN ? 64 * WAVES : 1];
-  const uint32_t nofs = (uint32_t)st0 * xround + tid * 8;
 
   // Loads of one round's weight data.  Tile u, vector v of a stream.
   auto tile_ofs = [&](int u, int v) -> uint32_t {
@@ -355,7 +337,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   };
 
   uint4 xs[XL][XN ? 2 : 1];
-  uint2 nv = {0u, 0u};        // XN: this thread's norm weights of the round two ahead
   uint4 wq[TILES][NSET][TV];
   uint2 sc[NSET];
   uint32_t dq[NSET];          // Q6_K: f16 d of the round's two super-blocks
@@ -373,10 +354,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     }
   };
   stage_load(0);
-  if constexpr (XN) {
-    nwl[0][tid] = __builtin_bit_cast(float2, plain ? ones : bload8(nwr, nofs, 0));
-    nwl[1][tid] = __builtin_bit_cast(float2, plain ? ones : bload8(nwr, nofs, nround > 1 ? xround : 0u));
-  }
 #pragma unroll
   for (int j = 0; j < TILES; ++j) {
 #pragma unroll
@@ -391,8 +368,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);  // issue the ring in slot order
   }
-  // Post-scale: the scales of this lane's output columns 4g .. 4g+3, summed
-  // in sum_partials' order, while the first round's weights are in flight.
+  // Post-scale: the scales of this lane's output columns 4g .. 4g+3, while
+  // the first round's weights are in flight.  Lane p adds partials p and
+  // p + 64, then one DPP tree over the wave: a fixed order, so every
+  // workgroup and every block size gets the same scale for a column.
   // Every column index is a compile-time constant and nothing branches per
   // column (a private array indexed at run time would move to LDS; a uniform
   // branch per column reloads kernel arguments).
@@ -408,29 +387,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       psc[c & 3] = ((c >> 2) == g && c < nb) ? sc1 : psc[c & 3];
     }
   }
-  // XN: column scales from the producer's partial sums of squares, summed
-  // in a fixed order (sum_partials), so every workgroup and every block size
-  // gets the same scale for a column.
-  float scl[XL];
-#pragma unroll
-  for (int i = 0; i < XL; ++i) {
-    scl[i] = 0.f;
-    if constexpr (XN) {
-      const int c = wave + WAVES * i;
-      const float ss = c < p.B ? sum_partials(p.ssq, p.npart, c, lane) : 0.f;
-      const float sc1 = c >= p.B ? 0.f : plain ? 1.f : 1.f / sqrtf(ss / (float)p.K + p.eps);
-      scl[i] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sc1)));  // uniform
-    }
-  }
-  auto stage_store = [&](uint4 *buf, int nb) __attribute__((always_inline)) {
+  auto stage_store = [&](uint4 *buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
-      if constexpr (XN) buf[xslot[i]] = norm8(xs[i], (const float4 *)&nwl[nb][0] + 2 * lane, scl[i]);
+      if constexpr (XN) buf[xslot[i]] = cvt8(xs[i]);
       else buf[xslot[i]] = xs[i][0];
     }
   };
-  if constexpr (XN) lds_barrier();  // nwl[0], nwl[1] written
-  stage_store(act[0], 0);
+  stage_store(act[0]);
   lds_barrier();
 
   const Unpack uc = unpack_consts();
@@ -479,10 +443,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
         dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q] + nr * sstride, 0);
     }
     stage_load(nr * xround);
-    if constexpr (XN) {
-      nv = bload8(nwr, nofs, (uint32_t)(rd + 2 < nround ? rd + 2 : nround - 1) * xround);
-      if (plain) nv = ones;
-    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < TILES; ++j) {
@@ -532,8 +492,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
           acc[q][m & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b[q][m], acc[q][m & 1], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);  // keep slots in issue order
     }
-    stage_store(act[cur ^ 1], cur ^ 1);
-    if constexpr (XN) nwl[cur][tid] = __builtin_bit_cast(float2, nv);
+    stage_store(act[cur ^ 1]);
     lds_barrier();
   };
   int rd = 0;
@@ -1077,14 +1036,11 @@ void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
 int gemv_row_tiles(const cwen_weight *w) { return (w->nrg + WAVES * w->rows - 1) / (WAVES * w->rows); }
 
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
-                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvNorm *nrm,
-                const GemvNorm *post) {
-  if (post && (nrm || !xh || !post->ssq || post->npart < 1 || post->npart > CWEN_MAX_PARTS)) return CWEN_EINVAL;
-  if (nrm) {
-    const bool plain = !nrm->w && !nrm->ssq && nrm->npart == 0;
-    if (xh || !nrm->x || ((uintptr_t)nrm->x & 15) || (nrm->xs & 3) || (B > 1 && nrm->xs < w->ne0)) return CWEN_EINVAL;
-    if (!plain && (!nrm->w || !nrm->ssq || nrm->npart < 1 || nrm->npart > CWEN_MAX_PARTS)) return CWEN_EINVAL;
-  }
+                const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvF32 *xf,
+                const GemvPost *post) {
+  if (post && (xf || !xh || !post->ssq || post->npart < 1 || post->npart > CWEN_MAX_PARTS)) return CWEN_EINVAL;
+  if (xf && (xh || !xf->x || ((uintptr_t)xf->x & 15) || (xf->xs & 3) || (B > 1 && xf->xs < w->ne0)))
+    return CWEN_EINVAL;
   if (out.ssq && (epi != GEMV_EPI_STORE || gemv_row_tiles(w) > CWEN_MAX_PARTS)) return CWEN_EINVAL;
   GemvParams p;
   p.w = w->dev;
@@ -1096,16 +1052,13 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   p.nst = w->nst;
   GemvGrid cfg = w->cfg[nsides - 1];
   p.xh = xh;
-  const int xfs = nrm ? (B > 1 ? nrm->xs : w->ne0) : 0;
-  p.xbytes = nrm ? (uint32_t)(((size_t)(B - 1) * xfs + w->ne0) * 4) : (uint32_t)((size_t)B * w->ne0 * 2);
-  p.xf = nrm ? nrm->x : nullptr;
+  const int xfs = xf ? (B > 1 ? xf->xs : w->ne0) : 0;
+  p.xbytes = xf ? (uint32_t)(((size_t)(B - 1) * xfs + w->ne0) * 4) : (uint32_t)((size_t)B * w->ne0 * 2);
+  p.xf = xf ? xf->x : nullptr;
   p.xfs = xfs;
-  p.nw = nrm ? nrm->w : nullptr;
-  p.ssq = nrm ? nrm->ssq : nullptr;
-  p.npart = nrm ? nrm->npart : 0;
-  p.eps = nrm ? nrm->eps : post ? post->eps : 0.f;
   p.pss = post ? post->ssq : nullptr;
   p.pnpart = post ? post->npart : 0;
+  p.eps = post ? post->eps : 0.f;
   p.K = w->ne0;
   p.B = B;
   p.part = ctx->partials;

@@ -169,7 +169,7 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
   int npart = 1;
   for (int l = 0; l < c.n_layers; ++l) {
     Layer &y = m->L[l];
-    const GemvNorm n1 = {nullptr, nullptr, m->ssq, npart, c.rms_eps, H};
+    const GemvPost n1 = {m->ssq, npart, c.rms_eps};
     const cwen_weight *wout;
     if (y.linear) {
       const Rows r = rows_of(c);
@@ -198,7 +198,7 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
       if ((rc = gemv_launch(ctx, y.wo, 1, 0, GEMV_EPI_STORE, m->yh, o5, B, st))) return rc;
       wout = y.wo;
     }
-    const GemvNorm n2 = {nullptr, nullptr, m->ssq, gemv_row_tiles(wout), c.rms_eps, H};
+    const GemvPost n2 = {m->ssq, gemv_row_tiles(wout), c.rms_eps};
     GemvOut f1 = {nullptr, nullptr, m->hh, 0, 0};
     GemvOut f2 = {m->X, nullptr, m->xh, H, 1};
     f2.ssq = m->ssq;
@@ -211,7 +211,7 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
   }
   if (mode != MODE_FWD) {
     const int E = mode == MODE_VERIFY ? B - 1 : 0;
-    const GemvNorm nh = {nullptr, nullptr, m->ssq, npart, c.rms_eps, H};
+    const GemvPost nh = {m->ssq, npart, c.rms_eps};
     GemvOut o = {m->logits, nullptr, nullptr, c.vocab, 0,
                  {ctx->amax_keys, ctx->amax_cnt, m->toks + 1, E, m->res}};
     if ((rc = gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, m->xh, o, B, st, nullptr, &nh))) return rc;
