@@ -139,6 +139,14 @@ __device__ __forceinline__ float sum64(float v) {
 // run.c:378-384 silu_one: x * (1 / (1 + exp(-x)))
 __device__ __forceinline__ float silu_f(float x) { return x * (1.f / (1.f + expf(-x))); }
 
+// An f16 operand that is not finite: the f32 value left f16's range (or was
+// not finite itself).  Writers of f16 operands raise a sticky flag, which the
+// model's entry points report.
+__device__ __forceinline__ bool f16_bad(_Float16 h) { return !(__builtin_fabsf((float)h) <= 65504.f); }
+__device__ __forceinline__ void raise_flag(int *flag) {
+  if (flag) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Row-tile partials of a column's sum of squares: at most 128 per column.
 constexpr int CWEN_MAX_PARTS = 128;
 
@@ -160,6 +168,7 @@ struct GemvOut {
   ArgmaxOut am;      // ARGMAX only
   float *ssq;        // STORE: per row tile, the sum of squares of the final y per column [row tile][CWEN_BMAX]
   const float *nwh;  // with yh: the f16 copy holds y * nwh[row] (the next RMSNorm's weight), nullable
+  int *rflag;        // with yh: set to 1 when an f16 value written is not finite (out of f16's range), nullable
 };
 // f32 activations that the GEMV converts to its f16 operand while staging.
 struct GemvF32 {
@@ -202,7 +211,8 @@ int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &
 int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
                      const float *decay, const float *beta, int gs, const float *kw, const float *wn,
                      float *out, int os, int B, hipStream_t st, _Float16 *outh = nullptr, int ohs = 0,
-                     const float *A = nullptr, const float *dt = nullptr, int force_L0 = 0);
+                     const float *A = nullptr, const float *dt = nullptr, int force_L0 = 0,
+                     int *rflag = nullptr);
 // The state after replaying L positions of pending buffer buf from base slot
 // X into S_out (device, [nvh][dk][dk]).
 int gdn_peek_launch(const cwen_gdn *g, int L, int buf, float *S_out, hipStream_t st);
@@ -210,8 +220,10 @@ int gdn_peek_launch(const cwen_gdn *g, int L, int buf, float *S_out, hipStream_t
 // ------------------------------------------------------------ model.hip
 // Also writes each row's sum of squares to ssq[b] (one partial per column)
 // and, when xh is given, the f16 operand x * nw of the first RMSNorm.
+// rflag (nullable) is set to 1 when an f16 value written is not finite.
 int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *toks, int B, int H, float *X,
-                 int xs, float *ssq, hipStream_t st, _Float16 *xh = nullptr, const float *nw = nullptr);
+                 int xs, float *ssq, hipStream_t st, _Float16 *xh = nullptr, const float *nw = nullptr,
+                 int *rflag = nullptr);
 size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B);
 int attention_init();
 // `last` is a device int: the last filled cache slot before the block (the
@@ -220,4 +232,4 @@ int attention_init();
 int attention_launch(const float *qfull, int qfs, const float *kx, const float *vx, int kvs, const float *qn,
                      const float *kn, float *qbuf, float *K, float *V, const int *last, int B, int NH, int NKV,
                      int npairs, int nrot, float theta, float eps, float *part, int max_ctx, _Float16 *yh,
-                     hipStream_t st);
+                     hipStream_t st, int *rflag = nullptr);

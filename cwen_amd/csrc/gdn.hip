@@ -70,6 +70,7 @@ struct GdnParams {
   const float *wn;            // gated-norm weight [DK]
   float *out; int os;         // [B][os], nullable
   _Float16 *outh; int ohs;    // f16 copy [B][ohs], nullable
+  int *rflag;                 // set to 1 when an f16 copy is out of f16's range, nullable
   const float *A, *dt;        // raw gates when non-null: decay = A*softplus(decay + dt), beta = sigmoid(beta)
   float *xc;                  // pending post-conv values [2][BMAX][C]
   float *gates;               // pending g, beta [2][BMAX][2][nvh]
@@ -275,6 +276,7 @@ __global__ __launch_bounds__(64) void gdn_norm_kernel(GdnParams p) {
   if (p.outh) {
     const half2_t h = {(_Float16)r.x, (_Float16)r.y};
     *(half2_t *)(p.outh + (size_t)b * p.ohs + hv * DK + 2 * lane) = h;
+    if (f16_bad(h[0]) || f16_bad(h[1])) raise_flag(p.rflag);
   }
 }
 
@@ -290,6 +292,7 @@ static void fill_params(GdnParams &p, const cwen_gdn *g) {
   p.force_L0 = 0;
   p.S_peek = nullptr;
   p.peek_L = p.peek_buf = 0;
+  p.rflag = nullptr;
   p.xc = g->xc; p.gates = g->gates; p.ob = g->ob;
   p.nkh = g->nkh; p.nvh = g->nvh; p.C = g->C;
 }
@@ -297,7 +300,7 @@ static void fill_params(GdnParams &p, const cwen_gdn *g) {
 int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
                      const float *decay, const float *beta, int gs, const float *kw, const float *wn,
                      float *out, int os, int B, hipStream_t st, _Float16 *outh, int ohs, const float *A,
-                     const float *dt, int force_L0) {
+                     const float *dt, int force_L0, int *rflag) {
   GdnParams p;
   fill_params(p, g);
   p.force_L0 = force_L0;
@@ -307,6 +310,7 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
   p.kw = kw; p.wn = wn;
   p.out = out; p.os = os;
   p.outh = outh; p.ohs = ohs;
+  p.rflag = rflag;
   p.A = A; p.dt = dt;
   p.B = B;
   hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((g->C + 255) / 256)), dim3(256), 0, st, p);

@@ -626,6 +626,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   float *const y0 = (NS == 2 && EPI == GEMV_EPI_PAIR && (wave & 1)) ? o.y1 : o.y;  // PAIR: each side its own output
 
   float sq[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of the row tile's sum of squares
+  bool bad = false;                    // an f16 copy out of range
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = rgs[r] * Q4_ROWS + n;
@@ -653,10 +654,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       const int c = g * 4 + e;
       if (c >= p.B) continue;
       if (y0) y0[(size_t)c * o.ys + row] = v[e];
-      if (o.yh) o.yh[(size_t)c * p.M + row] = (_Float16)(o.nwh ? v[e] * nwr : v[e]);
+      if (o.yh) {
+        const _Float16 h = (_Float16)(o.nwh ? v[e] * nwr : v[e]);
+        o.yh[(size_t)c * p.M + row] = h;
+        bad |= f16_bad(h);
+      }
       sq[e] = fmaf(v[e], v[e], sq[e]);
     }
   }
+  if (bad) raise_flag(o.rflag);
   if (o.ssq) {
     // Sum of squares of this row tile's outputs per column, in a fixed order
     // (rows of a wave by the DPP tree, then waves in order): ssq[rt][c], the

@@ -44,7 +44,7 @@ __device__ __forceinline__ float f16f(uint16_t h) { return (float)__builtin_bit_
 // f32 dequant w = (n - 8) * d.  Grid: B, 256 threads, thread = block.
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uint16_t *sc, int type,
                                                     const int *toks, int H, float *X, int xs, float *ssq,
-                                                    _Float16 *xh, const float *nw) {
+                                                    _Float16 *xh, const float *nw, int *rflag) {
   __shared__ float red[4];
   const int b = blockIdx.x;
   const size_t tok = (size_t)toks[b];
@@ -67,8 +67,10 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uin
       dst[j] = lo;
       dst[j + 16] = hi;
       if (xh) {
-        xh[(size_t)b * H + i * 32 + j] = (_Float16)(lo * nw[i * 32 + j]);
-        xh[(size_t)b * H + i * 32 + j + 16] = (_Float16)(hi * nw[i * 32 + j + 16]);
+        const _Float16 h0 = (_Float16)(lo * nw[i * 32 + j]), h1 = (_Float16)(hi * nw[i * 32 + j + 16]);
+        xh[(size_t)b * H + i * 32 + j] = h0;
+        xh[(size_t)b * H + i * 32 + j + 16] = h1;
+        if (f16_bad(h0) || f16_bad(h1)) raise_flag(rflag);
       }
       sq = fmaf(lo, lo, sq);
       sq = fmaf(hi, hi, sq);
@@ -97,6 +99,7 @@ struct AttnParams {
   float *pm, *pl;      // partial max / sum [NKV][nchunk][B*kvm]
   int nchunk;
   _Float16 *yh;        // gated outputs f16 [B][NH*HD]
+  int *rflag;          // set to 1 when a gated output is out of f16's range, nullable
 };
 
 __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
@@ -323,15 +326,17 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
   }
   const float g = p.qfull[(size_t)b * p.qfs + (size_t)h * 2 * HD + HD + d];
   const float y = (O / L) * (1.f / (1.f + expf(-g)));
-  p.yh[(size_t)b * p.NH * HD + (size_t)h * HD + d] = (_Float16)y;
+  const _Float16 yh = (_Float16)y;
+  p.yh[(size_t)b * p.NH * HD + (size_t)h * HD + d] = yh;
+  if (f16_bad(yh)) raise_flag(p.rflag);
 }
 
 }  // namespace
 
 int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *toks, int B, int H, float *X,
-                 int xs, float *ssq, hipStream_t st, _Float16 *xh, const float *nw) {
+                 int xs, float *ssq, hipStream_t st, _Float16 *xh, const float *nw, int *rflag) {
   if ((xh == nullptr) != (nw == nullptr)) return CWEN_EINVAL;
-  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)B), dim3(256), 0, st, qs, sc, type, toks, H, X, xs, ssq, xh, nw);
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)B), dim3(256), 0, st, qs, sc, type, toks, H, X, xs, ssq, xh, nw, rflag);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }
@@ -360,7 +365,7 @@ constexpr int ATTN_CHUNK_WGS = 128;
 int attention_launch(const float *qfull, int qfs, const float *kx, const float *vx, int kvs, const float *qn,
                      const float *kn, float *qbuf, float *K, float *V, const int *last, int B, int NH, int NKV,
                      int npairs, int nrot, float theta, float eps, float *part, int max_ctx, _Float16 *yh,
-                     hipStream_t st) {
+                     hipStream_t st, int *rflag) {
   AttnParams p;
   p.qfull = qfull; p.qfs = qfs; p.kx = kx; p.vx = vx; p.kvs = kvs;
   p.qn = qn; p.kn = kn;
@@ -373,6 +378,7 @@ int attention_launch(const float *qfull, int qfs, const float *kx, const float *
   p.pm = part + (size_t)NKV * p.nchunk * nq * HD;
   p.pl = p.pm + (size_t)NKV * p.nchunk * nq;
   p.yh = yh;
+  p.rflag = rflag;
   hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
   const int nwg = p.nchunk < ATTN_CHUNK_WGS ? p.nchunk : ATTN_CHUNK_WGS;
   const int MT = (nq + 15) / 16;

@@ -60,7 +60,8 @@ struct cwen_model {
   int *htok = nullptr;           // pinned token staging [BMAX]
   hipEvent_t tok_ev = nullptr;   // the last staging copy has been issued past this
   // device scratch
-  int *toks = nullptr, *res = nullptr;
+  int *toks = nullptr;
+  int *res = nullptr;            // [0] range flag copy, [1] k, [2] bonus, [3..] argmax per column
   float *X = nullptr;            // residual stream [BMAX][H]
   float *ssq = nullptr;          // partial sums of squares of X [CWEN_MAX_PARTS][BMAX]
   _Float16 *xh = nullptr;        // f16 operand x * w of the next RMSNorm [BMAX][H]
@@ -129,12 +130,14 @@ int upload_w(cwen_model *m, int type, const void *data, const void *scales, int 
   return cwen_weight_upload(m->ctx, type, data, scales, ne0, ne1, out);
 }
 
-// Device commit of a block of nmax positions: keep n, or res[0] + 1
-// (accepted drafts + bonus) when res is given, clamped to [1, nmax].  The
+// Device commit of a block of nmax positions: keep n, or walk[0] + 1
+// (accepted drafts + bonus) when walk is given, clamped to [1, nmax].  The
 // position and the GDN ring slot advance by n; the GDN base state and replay
-// count follow gdn_commit_host's rule.
-__global__ void advance_kernel(int *ctl, const int *res, int n, int nmax, int nslot) {
-  if (res) n = res[0] + 1;
+// count follow gdn_commit_host's rule.  The sticky range flag ctl[5] is
+// copied to *flag_out, next to the walk's result, for the host to read.
+__global__ void advance_kernel(int *ctl, const int *walk, int n, int nmax, int nslot, int *flag_out) {
+  *flag_out = ctl[5];
+  if (walk) n = walk[0] + 1;
   n = n < 1 ? 1 : (n > nmax ? nmax : n);
   ctl[0] += n;
   ctl[1] = (ctl[1] + n) % nslot;
@@ -163,8 +166,11 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
   // sums of squares of x to m->ssq (`npart` of them); the consuming GEMV
   // scales its outputs by each column's 1 / rms.  Every block size takes
   // this one path, so blocks and single positions agree bit for bit.
+  // Every f16 operand written raises the sticky flag ctl[5] when it is out
+  // of f16's range.
+  int *const rflag = m->ctl + 5;
   if ((rc = embed_launch(m->emb_qs, m->emb_sc, m->emb_type, m->toks, B, H, m->X, H, m->ssq, st, m->xh,
-                         m->L[0].attn_norm)))
+                         m->L[0].attn_norm, rflag)))
     return rc;
   int npart = 1;
   for (int l = 0; l < c.n_layers; ++l) {
@@ -177,11 +183,12 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
       if ((rc = gemv_launch(ctx, y.lin_in, 1, 0, GEMV_EPI_STORE, m->xh, o1, B, st, nullptr, &n1))) return rc;
       const float *qkv = m->lin, *z = m->lin + r.C, *ga = m->lin + r.o_alpha, *gb = m->lin + r.o_beta;
       if ((rc = gdn_block_launch(y.gdn, qkv, r.lin, z, r.lin, ga, gb, r.lin, y.ssm_conv, y.ssm_norm, nullptr, 0, B,
-                                 st, m->gh, r.Zh, y.ssm_a, y.ssm_dt)))
+                                 st, m->gh, r.Zh, y.ssm_a, y.ssm_dt, 0, rflag)))
         return rc;
       GemvOut o5 = {m->X, nullptr, m->xh, H, 1};
       o5.ssq = m->ssq;
       o5.nwh = y.post_norm;
+      o5.rflag = rflag;
       if ((rc = gemv_launch(ctx, y.ssm_out, 1, 0, GEMV_EPI_STORE, m->gh, o5, B, st))) return rc;
       wout = y.ssm_out;
     } else {
@@ -190,18 +197,21 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
       if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, m->xh, o1, B, st, nullptr, &n1))) return rc;
       if ((rc = attention_launch(m->att, r.att, m->att + r.Qo2, m->att + r.Qo2 + r.Ko, r.att, y.q_norm, y.k_norm,
                                  m->qbuf, y.K, y.V, m->ctl, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
-                                 c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st)))
+                                 c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st, rflag)))
         return rc;
       GemvOut o5 = {m->X, nullptr, m->xh, H, 1};
       o5.ssq = m->ssq;
       o5.nwh = y.post_norm;
+      o5.rflag = rflag;
       if ((rc = gemv_launch(ctx, y.wo, 1, 0, GEMV_EPI_STORE, m->yh, o5, B, st))) return rc;
       wout = y.wo;
     }
     const GemvPost n2 = {m->ssq, gemv_row_tiles(wout), c.rms_eps};
     GemvOut f1 = {nullptr, nullptr, m->hh, 0, 0};
+    f1.rflag = rflag;
     GemvOut f2 = {m->X, nullptr, m->xh, H, 1};
     f2.ssq = m->ssq;
+    f2.rflag = rflag;
     f2.nwh = l + 1 < c.n_layers ? m->L[l + 1].attn_norm : m->out_norm;
     if ((rc = gemv_launch(ctx, y.ffn_gu, 2, 0, GEMV_EPI_SWIGLU, m->xh, f1, B, st, nullptr, &n2)) ||
         (rc = gemv_launch(ctx, y.ffn_down, 1, 0, GEMV_EPI_STORE, m->hh, f2, B, st)))
@@ -213,11 +223,11 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
     const int E = mode == MODE_VERIFY ? B - 1 : 0;
     const GemvPost nh = {m->ssq, npart, c.rms_eps};
     GemvOut o = {m->logits, nullptr, nullptr, c.vocab, 0,
-                 {ctx->amax_keys, ctx->amax_cnt, m->toks + 1, E, m->res}};
+                 {ctx->amax_keys, ctx->amax_cnt, m->toks + 1, E, m->res + 1}};
     if ((rc = gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, m->xh, o, B, st, nullptr, &nh))) return rc;
   }
-  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->ctl, mode == MODE_VERIFY ? m->res : nullptr, B, B,
-                     CWEN_BMAX + 1);
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->ctl, mode == MODE_VERIFY ? m->res + 1 : nullptr, B,
+                     B, CWEN_BMAX + 1, m->res);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }
@@ -423,8 +433,8 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
   const int Zh = R.Zh, Qo = R.Qo2 / 2, Ko = R.Ko;
   const char *ge = getenv("CWEN_GRAPHS");
   m->use_graphs = ge && ge[0] == '1';
-  const int ctl0[5] = {-1, 0, 0, 0, 0};
-  rc = dmalloc(&m->ctl, 5) ? CWEN_ENOMEM : CWEN_OK;
+  const int ctl0[6] = {-1, 0, 0, 0, 0, 0};  // position, ring slot, base slot, replay count, buffer, range flag
+  rc = dmalloc(&m->ctl, 6) ? CWEN_ENOMEM : CWEN_OK;
   if (!rc && (hipMemcpy(m->ctl, ctl0, sizeof(ctl0), hipMemcpyHostToDevice) != hipSuccess ||
               hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking) != hipSuccess ||
               hipEventCreateWithFlags(&m->tok_ev, hipEventDisableTiming) != hipSuccess))
@@ -447,7 +457,7 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
     }
   }
   if (!rc)
-    rc = (dmalloc(&m->toks, BM) || dmalloc(&m->res, 2 + BM) ||
+    rc = (dmalloc(&m->toks, BM) || dmalloc(&m->res, 3 + BM) ||
           dmalloc(&m->X, (size_t)BM * H) || dmalloc(&m->ssq, (size_t)CWEN_MAX_PARTS * BM) || dmalloc(&m->xh, (size_t)BM * H) ||
           dmalloc(&m->lin, (size_t)BM * R.lin) || dmalloc(&m->gh, (size_t)BM * Zh) ||
           dmalloc(&m->att, (size_t)BM * R.att) || dmalloc(&m->qbuf, (size_t)BM * Qo) ||
@@ -456,7 +466,7 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
           dmalloc(&m->logits, (size_t)BM * c.vocab))
              ? CWEN_ENOMEM
              : CWEN_OK;
-  if (!rc && (hipHostMalloc((void **)&m->hres, (2 + BM) * sizeof(int), hipHostMallocDefault) != hipSuccess ||
+  if (!rc && (hipHostMalloc((void **)&m->hres, (3 + BM) * sizeof(int), hipHostMallocDefault) != hipSuccess ||
               hipHostMalloc((void **)&m->htok, BM * sizeof(int), hipHostMallocDefault) != hipSuccess))
     rc = CWEN_ENOMEM;
   if (rc) {
@@ -648,7 +658,7 @@ int cwen_model_reset(cwen_model *m) {
       int rc = cwen_gdn_set_state(g, nullptr, nullptr);
       if (rc) return rc;
     }
-  const int ctl0[5] = {-1, 0, 0, 0, 0};
+  const int ctl0[6] = {-1, 0, 0, 0, 0, 0};  // clears the range flag too
   CWEN_HIP_TRY(hipMemcpy(m->ctl, ctl0, sizeof(ctl0), hipMemcpyHostToDevice));
   m->pos = -1;
   return CWEN_OK;
@@ -665,12 +675,12 @@ int cwen_model_forward(cwen_model *m, const int *toks, int B, int want_argmax, i
   int rc;
   if ((rc = run_block(m, toks, B, want_argmax ? MODE_FWD_HEAD : MODE_FWD, st))) return rc;
   if (want_argmax) {
-    CWEN_HIP_TRY(hipMemcpyAsync(m->hres, m->res, (2 + B) * sizeof(int), hipMemcpyDeviceToHost, st));
+    CWEN_HIP_TRY(hipMemcpyAsync(m->hres, m->res, (3 + B) * sizeof(int), hipMemcpyDeviceToHost, st));
     CWEN_HIP_TRY(hipStreamSynchronize(st));
-    if (argmax_out) memcpy(argmax_out, m->hres + 2, (size_t)B * sizeof(int));
+    if (argmax_out) memcpy(argmax_out, m->hres + 3, (size_t)B * sizeof(int));
   }
   commit(m, B, B);
-  return CWEN_OK;
+  return want_argmax && m->hres[0] ? CWEN_ERANGE : CWEN_OK;
 }
 
 int cwen_model_verify(cwen_model *m, const int *blk, int B, int *k_out, int *bonus_out, void *stream) {
@@ -679,14 +689,14 @@ int cwen_model_verify(cwen_model *m, const int *blk, int B, int *k_out, int *bon
   hipStream_t st = (hipStream_t)stream;
   int rc;
   if ((rc = run_block(m, blk, B, MODE_VERIFY, st))) return rc;
-  CWEN_HIP_TRY(hipMemcpyAsync(m->hres, m->res, 2 * sizeof(int), hipMemcpyDeviceToHost, st));
+  CWEN_HIP_TRY(hipMemcpyAsync(m->hres, m->res, 3 * sizeof(int), hipMemcpyDeviceToHost, st));
   CWEN_HIP_TRY(hipStreamSynchronize(st));
-  const int k = m->hres[0];
+  const int k = m->hres[1];
   if (k < 0 || k > B - 1) return CWEN_EHIP;
   commit(m, k + 1, B);
   if (k_out) *k_out = k;
-  if (bonus_out) *bonus_out = m->hres[1];
-  return CWEN_OK;
+  if (bonus_out) *bonus_out = m->hres[2];
+  return m->hres[0] ? CWEN_ERANGE : CWEN_OK;
 }
 
 int cwen_model_logits(cwen_model *m, float *host, int rows) {

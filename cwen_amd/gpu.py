@@ -15,7 +15,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libcwen_gpu.so"
 HOST_LIB_PATH = Path(__file__).resolve().parent / "libcwen_host.so"
 
 CWEN_OK = 0
-ERRORS = {-1: "EINVAL", -2: "EHIP", -3: "ENOMEM", -4: "ETYPE", -5: "ESCRATCH"}
+CWEN_ERANGE = -6
+ERRORS = {-1: "EINVAL", -2: "EHIP", -3: "ENOMEM", -4: "ETYPE", -5: "ESCRATCH", -6: "ERANGE"}
 
 T_F32, T_Q4_0, T_Q8_0, T_Q6_K, T_Q4_0RS, T_Q4_0RSI = 0, 2, 8, 14, 101, 102
 BMAX = 16

@@ -35,6 +35,9 @@ extern "C" {
 #define CWEN_ENOMEM   (-3)   /* device allocation failed                 */
 #define CWEN_ETYPE    (-4)   /* weight type not supported by this call   */
 #define CWEN_ESCRATCH (-5)   /* a shape exceeds the context's scratch    */
+#define CWEN_ERANGE   (-6)   /* an f16 activation operand left f16's     */
+                             /* range; the model's state is invalid      */
+                             /* until cwen_model_reset                   */
 
 /* Largest K (inputs) of a weight; sizes the context's f16 activation scratch. */
 #define CWEN_KMAX 65536
@@ -240,7 +243,11 @@ int cwen_model_capacity(const cwen_model *m);
  * positions pos+1..pos+B and advance by B.  With want_argmax the head runs
  * on every row and argmax_out (HOST, B ints, nullable) receives each row's
  * argmax_of; without it the head is skipped (prefill chunks).  Synchronous
- * when want_argmax. */
+ * when want_argmax.  Returns CWEN_ERANGE (after the block has run and been
+ * committed) when any f16 activation operand written since the last reset
+ * was out of f16's range, e.g. a residual element times its RMSNorm weight
+ * of magnitude 65520 or more; without want_argmax the next synchronous call
+ * reports it. */
 int cwen_model_forward(cwen_model *m, const int *toks, int B, int want_argmax, int *argmax_out, void *stream);
 /* One speculative verify cycle on the device: score blk[0..B-1] (blk[0] the
  * pending token, blk[1..B-1] the drafts), take the per-row argmax, walk the
@@ -248,7 +255,7 @@ int cwen_model_forward(cwen_model *m, const int *toks, int B, int want_argmax, i
  * by k+1 positions (GDN snapshots committed, KV slots past the prefix are
  * rewritten before any read).  Only k and the bonus token return to the
  * host.  B = 1 is the serial decode step (forward_ex + argmax_of).
- * Synchronous. */
+ * Synchronous.  CWEN_ERANGE as for cwen_model_forward. */
 int cwen_model_verify(cwen_model *m, const int *blk, int B, int *k, int *bonus, void *stream);
 /* Copy the f32 logits of the last head pass (rows 0..rows-1) to HOST. */
 int cwen_model_logits(cwen_model *m, float *host, int rows);

@@ -168,6 +168,34 @@ def test_spec_decode_equals_serial(env, n_key):
         assert st.drafted > 0
 
 
+def test_out_of_range_operand_is_reported(env):
+    """The RMSNorm is split between producer and consumer, so the f16 operand
+    holds a residual element times its norm weight before normalisation.
+    When that leaves f16's range the operand is infinite: verify and
+    forward-with-argmax then return CWEN_ERANGE (sticky until reset) instead
+    of tokens silently computed from it.  In range, the same model gives the
+    ordinary result, before and after."""
+    gpu, ctx, m, tensors = env
+    mb = gpu.Model(ctx, **CFG)
+    for t in tensors:
+        mb.set(*t)
+    toks = synth.prompt_tokens(6, 8, CFG["vocab"])
+    ok = mb.verify(toks)
+    layer, tid, wtype, w, _, ne0, ne1 = next(t for t in tensors if t[0] == 1 and t[1] == gpu.POST_NORM)
+    mb.set(layer, tid, wtype, (w * 1e6).astype(np.float32), None, ne0, ne1)
+    mb.reset()
+    with pytest.raises(gpu.CwenError) as e:
+        mb.verify(toks)
+    assert e.value.rc == gpu.CWEN_ERANGE
+    with pytest.raises(gpu.CwenError) as e:   # sticky: the next synchronous call reports it too
+        mb.forward(toks[:1])
+    assert e.value.rc == gpu.CWEN_ERANGE
+    mb.set(layer, tid, wtype, w, None, ne0, ne1)
+    mb.reset()
+    assert mb.verify(toks) == ok
+    mb.free()
+
+
 def test_graph_replay_equals_eager(env, monkeypatch):
     """CWEN_GRAPHS=1: each (mode, B) block is captured once and replayed at
     later positions (position and ring slot read on the device).  Replays
