@@ -78,56 +78,46 @@ struct GdnParams {
   int nkh, nvh, C, B;
 };
 
-// 1. conv: thread = channel.  All loads of a channel are issued before its
-// first use.  A workgroup's 256 channels are two whole heads, all q/k or all
-// v (the q/k channels are 2 * nkh * 128); q and k are l2-normalised here
-// (run.c:401-423), once per position, so the recurrence and a later replay
-// read the same normalised values.
+// 1. conv: thread = (channel, position); workgroup = 256 channels of one
+// position (blockIdx.y).  The 4-tap filter needs no running state: the
+// inputs at b-3 .. b-1 come from the block's own rows or, before the block,
+// from the history slot the block starts from, so every position is
+// computed at once with run.c's product/sum order.  A workgroup's 256
+// channels are two whole heads, all q/k or all v (the q/k channels are
+// 2 * nkh * 128); q and k are l2-normalised here (run.c:401-423), once per
+// position, so the recurrence and a later replay read the same normalised
+// values.  Each position's thread also writes that position's history slot
+// (inputs b-2, b-1, b).
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
-  __shared__ float s_ss[4][MAXB];  // per wave and position: the wave's sum of squares
-  const int c = blockIdx.x * 256 + threadIdx.x;
+  __shared__ float s_ss[4];        // per wave: the wave's sum of squares
+  const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
   if (c >= p.C) return;           // whole waves (C is a multiple of 128)
   const int cur = p.ctl[0], P = p.ctl[3];
-  const float *H_in = p.H_slots + (size_t)cur * p.h_floats;
-  float *xc = p.xc + (size_t)P * CWEN_BMAX * p.C;
+  const float *H_in = p.H_slots + (size_t)cur * p.h_floats + (size_t)c * 3;
   const float4 w = *(const float4 *)(p.kw + (size_t)c * 4);
-  float h0 = H_in[(size_t)c * 3 + 0], h1 = H_in[(size_t)c * 3 + 1], h2 = H_in[(size_t)c * 3 + 2];
-  float raw[MAXB];
+  // inputs at positions b-3, b-2, b-1, b (history slot entries 0..2 are the
+  // inputs at -3, -2, -1)
+  float in[4];
 #pragma unroll
-  for (int b = 0; b < MAXB; ++b) raw[b] = b < p.B ? p.qkv[(size_t)b * p.qs + c] : 0.f;
-#pragma unroll
-  for (int b = 0; b < MAXB; ++b) {
-    if (b >= p.B) break;
-    const float xin = raw[b];
-    // ((st0*w0 + st1*w1) + st2*w2) + xin*w3, each product and sum rounded
-    const float x = __fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(h0, w.x), __fmul_rn(h1, w.y)), __fmul_rn(h2, w.z)),
-                              __fmul_rn(xin, w.w));
-    h0 = h1; h1 = h2; h2 = xin;
-    raw[b] = silu_ref(x);
-    float *hs = p.H_slots + (size_t)((cur + 1 + b) % p.nslot) * p.h_floats + (size_t)c * 3;
-    hs[0] = h0; hs[1] = h1; hs[2] = h2;
+  for (int j = 0; j < 4; ++j) {
+    const int t = b - 3 + j;
+    in[j] = t >= 0 ? p.qkv[(size_t)t * p.qs + c] : H_in[t + 3];
   }
+  // ((st0*w0 + st1*w1) + st2*w2) + xin*w3, each product and sum rounded
+  const float x = __fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(in[0], w.x), __fmul_rn(in[1], w.y)), __fmul_rn(in[2], w.z)),
+                            __fmul_rn(in[3], w.w));
+  float y = silu_ref(x);
+  float *hs = p.H_slots + (size_t)((cur + 1 + b) % p.nslot) * p.h_floats + (size_t)c * 3;
+  hs[0] = in[1]; hs[1] = in[2]; hs[2] = in[3];
   if (blockIdx.x * 256 < 2 * p.nkh * DK) {  // q / k heads: x / sqrt(sum x^2 + 1e-6)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-#pragma unroll
-    for (int b = 0; b < MAXB; ++b) {
-      if (b >= p.B) break;
-      const float t = sum64(raw[b] * raw[b]);
-      if (lane == 0) s_ss[wave][b] = t;
-    }
+    const float t = sum64(y * y);
+    if (lane == 0) s_ss[wave] = t;
     __syncthreads();
     const int w0 = wave & ~1;  // the head's two waves, in order
-#pragma unroll
-    for (int b = 0; b < MAXB; ++b) {
-      if (b >= p.B) break;
-      raw[b] *= 1.f / sqrtf(s_ss[w0][b] + s_ss[w0 + 1][b] + 1e-6f);
-    }
+    y *= 1.f / sqrtf(s_ss[w0] + s_ss[w0 + 1] + 1e-6f);
   }
-#pragma unroll
-  for (int b = 0; b < MAXB; ++b) {
-    if (b >= p.B) break;
-    xc[(size_t)b * p.C + c] = raw[b];
-  }
+  p.xc[((size_t)P * CWEN_BMAX + b) * p.C + c] = y;
 }
 
 // 2. recurrence: workgroup (hv, slice) = one wave, columns
@@ -313,7 +303,7 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
   p.rflag = rflag;
   p.A = A; p.dt = dt;
   p.B = B;
-  hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((g->C + 255) / 256)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((g->C + 255) / 256), (unsigned)B), dim3(256), 0, st, p);
   hipLaunchKernelGGL(gdn_rec_kernel, dim3((unsigned)(g->nvh * (DK / COLS))), dim3(64), 0, st, p);
   hipLaunchKernelGGL(gdn_norm_kernel, dim3((unsigned)(g->nvh * B)), dim3(64), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());

@@ -194,3 +194,38 @@ def test_ffn_block_full_size(env, oracle):
     assert rel_err(Hd.cpu().numpy(), h_want) <= TOL
     y_want = oracle.gemvb(T_RS, dq, ds, I, H, h_want)
     assert rel_err(Yd.cpu().numpy(), y_want) <= TOL
+
+
+@pytest.mark.parametrize("H,I", [(1024, 2048), (1024, 9216), (5120, 17408)])
+def test_mlp_block(env, oracle, H, I):
+    """cwen_mlp_block (f32 in, Y += down(SwiGLU(gate/up X))) is
+    bit-identical to the f16 entry points run one by one (f32 -> f16,
+    SwiGLU GEMV, accumulating down GEMV), repeats exactly, and matches the
+    oracle's mlp_blk within TOL.  The shapes cover split gate/up tiles
+    (2048), whole tiles plus split remainder tiles (9216: 288 tiles) and the
+    27B FFN."""
+    torch, gpu, ctx = env
+    gq, gs = synth.q4_rsi(110, I, H)
+    dq, ds = synth.q4_rs(110, H, I, key=1)
+    Wgu = gpu.Weight(ctx, T_RSI, gq, gs, H, I)
+    Wd = gpu.Weight(ctx, T_RS, dq, ds, I, H)
+    for B in (1, 5, 8, 16):
+        X = synth.activations(110, B, H, key=B)
+        Y0 = synth.activations(111, B, H, key=B)
+        Xd = torch.from_numpy(X).cuda()
+        Xh = torch.empty(B, H, dtype=torch.float16, device="cuda")
+        Hh = torch.empty(B, I, dtype=torch.float16, device="cuda")
+        ref = torch.from_numpy(Y0).cuda()
+        gpu.act_to_f16(ctx, Xd, Xh, H, B)
+        gpu.gemvb_swiglu_f16(ctx, Wgu, Xh, None, B, Hh=Hh)
+        gpu.gemvb_f16(ctx, Wd, Hh, ref, B, accumulate=True)
+        ref = ref.cpu().numpy()
+        for rep in range(2):
+            Y = torch.from_numpy(Y0).cuda()
+            gpu.mlp_block(ctx, Wgu, Wd, Xd, Y, B)
+            torch.cuda.synchronize()
+            got = Y.cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (B, rep)
+        if B == 8:
+            h = oracle.silu_mul(oracle.gemvb(T_RSI, gq, gs, H, I, X, 0), oracle.gemvb(T_RSI, gq, gs, H, I, X, 1))
+            assert rel_err(got - Y0, oracle.gemvb(T_RS, dq, ds, I, H, h)) <= TOL
