@@ -174,7 +174,7 @@ def time_each(fn, n: int, warmup: int, stream) -> list[float]:
 
 
 def extra_leg(steps: int, warmup: int) -> dict:
-    """c0 GGUF Q4_0 GEMV B=1, c2 Q6_K head + argmax + walk at B=8, c3 GDN block
+    """c0 GGUF Q4_0 GEMV B=1, Q4_1 down GEMV B=8, c2 Q6_K head + argmax + walk at B=8, c3 GDN block
     at B=8: average launch time over back-to-back launches (rotating enough
     copies that each launch streams from HBM), GB/s from the algorithmic bytes."""
     import torch
@@ -197,6 +197,20 @@ def extra_leg(steps: int, warmup: int) -> dict:
                                         "frac_of_peak": C0_BYTES / (ms * 1e-3) / 1e9 / PEAK_GBS,
                                         "launches": "q4 GEMV on f16 x (one launch)",
                                         "ms_f32_entry": ms32}
+    del Ws
+
+    # The next format on the path: Q4_1 (the real model's ffn_down), the 27B
+    # down shape 5120 x 17408 at B=8 on f16 activations; 6 copies x 55.7 MB > MALL.
+    M1, K1, B1 = 5120, 17408, 8
+    Ws = [gpu.Weight(ctx, gpu.T_Q4_1, synth.q4_1(0, M1, K1, key=c), None, K1, M1) for c in range(6)]
+    xh = torch.from_numpy(synth.activations(0, B1, K1)).cuda().half()
+    y = torch.empty(B1, M1, device="cuda")
+    ms = time_launches(lambda i: gpu.gemvb_f16(ctx, Ws[i % len(Ws)], xh, y, B1, stream=stream), steps, warmup,
+                       stream)
+    q41_bytes = M1 * (K1 // 32) * 20 + B1 * K1 * 2 + B1 * M1 * 4
+    out["q4_1_down_5120x17408_b8"] = {"ms": ms, "GB_s": q41_bytes / (ms * 1e-3) / 1e9,
+                                      "frac_of_peak": q41_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
+                                      "bytes": q41_bytes, "launches": "Q4_1 GEMV on f16 x (one launch)"}
     del Ws
 
     # c2: 638 MB head (> MALL), B=8, drafts = argmax w.p. 0.6

@@ -82,6 +82,11 @@ template <> struct Fmt<GEMV_Q8> {
   static constexpr uint32_t ST_BYTES = 8704, SC_OFS = 8192;
   static constexpr int TV = 2;
 };
+// Q4_1: the Q4_0 nibble layout, then per lane the 4 blocks' (d, m) f16 pairs.
+template <> struct Fmt<GEMV_Q41> {
+  static constexpr uint32_t ST_BYTES = 5120, SC_OFS = 4096;
+  static constexpr int TV = 1;
+};
 
 // (q & mask) | magic in one VOP3 op.  gfx9 VOP3 takes no literal and reads at
 // most one scalar, so the mask comes from an SGPR and the magic from a VGPR.
@@ -129,6 +134,22 @@ __device__ __forceinline__ half8_t unpack8_q4(uint32_t q, const Unpack &u, half2
   const half2_t h2 = (__builtin_bit_cast(half2_t, t2) - h2c(1032.f)) * dd;
   const half2_t h3 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t3), h2c(0.0625f), h2c(-72.f)) * dd;
   return pack8(h0, h1, h2, h3);
+}
+
+// Q4_1 (w = n*d + m): the nibble extraction of unpack8_q4, n exact, then
+// one fma per pair, rounded once to f16.
+__device__ __forceinline__ half8_t unpack8_q41(uint32_t q, const Unpack &u, half2_t dd, half2_t mm) {
+  const uint32_t q2 = q >> 8;
+  const uint32_t t0 = and_or(q, u.lo, u.magic);    // 1024 + n0, 1024 + n4
+  const uint32_t t1 = and_or(q, u.hi, u.magic);    // 1024 + 16 n1, 1024 + 16 n5
+  const uint32_t t2 = and_or(q2, u.lo, u.magic);
+  const uint32_t t3 = and_or(q2, u.hi, u.magic);
+  const half2_t n0 = __builtin_bit_cast(half2_t, t0) - h2c(1024.f);
+  const half2_t n1 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t1), h2c(0.0625f), h2c(-64.f));
+  const half2_t n2 = __builtin_bit_cast(half2_t, t2) - h2c(1024.f);
+  const half2_t n3 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t3), h2c(0.0625f), h2c(-64.f));
+  return pack8(__builtin_elementwise_fma(n0, dd, mm), __builtin_elementwise_fma(n1, dd, mm),
+               __builtin_elementwise_fma(n2, dd, mm), __builtin_elementwise_fma(n3, dd, mm));
 }
 
 // Q6_K: low nibbles as Q4_0 plus the 2 high bits of each weight, laid out in
@@ -315,7 +336,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     const int rgc = rgs[r] < p.nrg ? rgs[r] : p.nrg - 1;  // idle streams read a valid tile
     wofs[r] = (((uint32_t)rgc * p.nst + st0) * p.nsw + side) * F::ST_BYTES;
   }
-  const uint32_t lq = lane * 16, ls = F::SC_OFS + lane * 8;
+  const uint32_t lq = lane * 16, ls = F::SC_OFS + lane * (FMT == GEMV_Q41 ? 16 : 8);
 
   // Activation staging: this wave copies columns c = wave + WAVES*i; lane
   // copies f16 unit `lane` (K elements 8*lane .. 8*lane+7) of the column's
@@ -338,12 +359,18 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 
   uint4 xs[XL][XN ? 2 : 1];
   uint4 wq[TILES][NSET][TV];
-  uint2 sc[NSET];
+  // Scales of a round: 4 f16 (one per tile), or for Q4_1 4 (d, m) pairs.
+  using ScT = std::conditional_t<FMT == GEMV_Q41, uint4, uint2>;
+  ScT sc[NSET];
+  auto sc_load = [&](uint32_t soff) __attribute__((always_inline)) -> ScT {
+    if constexpr (FMT == GEMV_Q41) return bload16(wr, ls, soff);
+    else return bload8(wr, ls, soff);
+  };
   uint32_t dq[NSET];          // Q6_K: f16 d of the round's two super-blocks
   uint4 hq[2][NSET];          // Q6_K: high bits of tile pairs (0,1) and (2,3)
 #pragma unroll
   for (int q = 0; q < NSET; ++q) {
-    sc[q] = bload8(wr, ls, wofs[q]);
+    sc[q] = sc_load(wofs[q]);
     if constexpr (FMT == GEMV_Q6K) dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q], 0);
   }
   auto stage_load = [&](uint32_t soff) __attribute__((always_inline)) {
@@ -430,15 +457,24 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
           dd[q][u][1] = (half2_t){ds[1], ds[1]};
         }
       } else {
-        dd[q][0][0] = dd[q][0][1] = bcast_half(sc[q].x, false);
-        dd[q][1][0] = dd[q][1][1] = bcast_half(sc[q].x, true);
-        dd[q][2][0] = dd[q][2][1] = bcast_half(sc[q].y, false);
-        dd[q][3][0] = dd[q][3][1] = bcast_half(sc[q].y, true);
+        if constexpr (FMT == GEMV_Q41) {  // dd[q][u][0] = d, dd[q][u][1] = m
+          const uint32_t w4[4] = {sc[q].x, sc[q].y, sc[q].z, sc[q].w};
+#pragma unroll
+          for (int u = 0; u < TILES; ++u) {
+            dd[q][u][0] = bcast_half(w4[u], false);
+            dd[q][u][1] = bcast_half(w4[u], true);
+          }
+        } else {
+          dd[q][0][0] = dd[q][0][1] = bcast_half(sc[q].x, false);
+          dd[q][1][0] = dd[q][1][1] = bcast_half(sc[q].x, true);
+          dd[q][2][0] = dd[q][2][1] = bcast_half(sc[q].y, false);
+          dd[q][3][0] = dd[q][3][1] = bcast_half(sc[q].y, true);
+        }
       }
     }
 #pragma unroll
     for (int q = 0; q < NSET; ++q) {
-      sc[q] = bload8(wr, ls, wofs[q] + nr * sstride);
+      sc[q] = sc_load(wofs[q] + nr * sstride);
       if constexpr (FMT == GEMV_Q6K)
         dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q] + nr * sstride, 0);
     }
@@ -454,6 +490,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
           b[q][1] = unpack8_q4(wq[j][q][0].y, uc, dd[q][j][0]);
           b[q][2] = unpack8_q4(wq[j][q][0].z, uc, dd[q][j][0]);
           b[q][3] = unpack8_q4(wq[j][q][0].w, uc, dd[q][j][0]);
+        } else if constexpr (FMT == GEMV_Q41) {
+          b[q][0] = unpack8_q41(wq[j][q][0].x, uc, dd[q][j][0], dd[q][j][1]);
+          b[q][1] = unpack8_q41(wq[j][q][0].y, uc, dd[q][j][0], dd[q][j][1]);
+          b[q][2] = unpack8_q41(wq[j][q][0].z, uc, dd[q][j][0], dd[q][j][1]);
+          b[q][3] = unpack8_q41(wq[j][q][0].w, uc, dd[q][j][0], dd[q][j][1]);
         } else if constexpr (FMT == GEMV_Q6K) {
           const uint4 &h4 = hq[j >> 1][q];
           const uint32_t ha = (j & 1) ? h4.z : h4.x;   // runs 0, 1
@@ -688,9 +729,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 // One thread per (row group, super-tile, side, lane).  Rows past M get zero
 // weights (zero scales).
 
-// Q4_0 family: lane l = 16g + n gets, for each tile u, block g of that tile
-// for row n -- 4 dwords, dword j holding K run j (weights 8j..8j+7 of the
-// block) in kNibPos order -- and the 4 blocks' f16 scales.  The source (M rows,
+// Q4_0 family and Q4_1: lane l = 16g + n gets, for each tile u, block g of
+// that tile for row n -- 4 dwords, dword j holding K run j (weights 8j..8j+7
+// of the block) in kNibPos order -- and the 4 blocks' f16 scales (Q4_1: the 4
+// blocks' (d, m) pairs).  The source (M rows,
 // nrg row groups) lands at destination row group rg_off onward; side_sel >= 0
 // takes that side of a Q4_0RSI source into a single-sided destination.
 __global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_t *sc, int type,
@@ -707,18 +749,25 @@ __global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_
   const int row = rg * Q4_ROWS + n;
   const int nb = K / 32;
   const int sside = side_sel >= 0 ? side_sel : side;
-  uint8_t *stile = dst + (((size_t)(rg + rg_off) * nst + st) * nsw + side) * Fmt<GEMV_Q4>::ST_BYTES;
-  uint16_t d[TILES];
+  const bool q41 = type == CWEN_T_Q4_1;
+  const uint32_t stb = q41 ? Fmt<GEMV_Q41>::ST_BYTES : Fmt<GEMV_Q4>::ST_BYTES;
+  uint8_t *stile = dst + (((size_t)(rg + rg_off) * nst + st) * nsw + side) * stb;
+  uint16_t d[TILES], m[TILES];
   for (int u = 0; u < TILES; ++u) {
     const int blk = (st * TILES + u) * 4 + g;
     const uint8_t *qs = nullptr;
-    d[u] = 0;
+    d[u] = m[u] = 0;  // rows past M: zero weights
     if (row < M) {
       const size_t bi = (size_t)row * nb + blk;
       if (type == CWEN_T_Q4_0) {
         const uint8_t *b = src + bi * 18;
         d[u] = (uint16_t)(b[0] | (b[1] << 8));
         qs = b + 2;
+      } else if (q41) {  // {f16 d; f16 m; u8 qs[16]}
+        const uint8_t *b = src + bi * 20;
+        d[u] = (uint16_t)(b[0] | (b[1] << 8));
+        m[u] = (uint16_t)(b[2] | (b[3] << 8));
+        qs = b + 4;
       } else if (type == CWEN_T_Q4_0RS) {
         qs = src + bi * 16;
         d[u] = sc[bi];
@@ -740,8 +789,13 @@ __global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_
     }
     *(uint4 *)(stile + u * 1024 + lane * 16) = make_uint4(out[0], out[1], out[2], out[3]);
   }
-  *(uint2 *)(stile + Fmt<GEMV_Q4>::SC_OFS + lane * 8) =
-      make_uint2((uint32_t)d[0] | ((uint32_t)d[1] << 16), (uint32_t)d[2] | ((uint32_t)d[3] << 16));
+  if (q41)
+    *(uint4 *)(stile + Fmt<GEMV_Q41>::SC_OFS + lane * 16) =
+        make_uint4((uint32_t)d[0] | ((uint32_t)m[0] << 16), (uint32_t)d[1] | ((uint32_t)m[1] << 16),
+                   (uint32_t)d[2] | ((uint32_t)m[2] << 16), (uint32_t)d[3] | ((uint32_t)m[3] << 16));
+  else
+    *(uint2 *)(stile + Fmt<GEMV_Q4>::SC_OFS + lane * 8) =
+        make_uint2((uint32_t)d[0] | ((uint32_t)d[1] << 16), (uint32_t)d[2] | ((uint32_t)d[3] << 16));
 }
 
 // Q6_K (run.c:115, 1212-1229): weight j of a super-block (j = 0..255) is
@@ -922,20 +976,21 @@ int gemv_fmt_of(int type) {
     case CWEN_T_Q4_0: case CWEN_T_Q4_0RS: case CWEN_T_Q4_0RSI: return GEMV_Q4;
     case CWEN_T_Q6_K: return GEMV_Q6K;
     case CWEN_T_Q8_0: return GEMV_Q8;
+    case CWEN_T_Q4_1: return GEMV_Q41;
     default: return -1;
   }
 }
 
 size_t gemv_st_bytes(int fmt) {
   return fmt == GEMV_Q4 ? Fmt<GEMV_Q4>::ST_BYTES : fmt == GEMV_Q6K ? Fmt<GEMV_Q6K>::ST_BYTES
-                                                                   : Fmt<GEMV_Q8>::ST_BYTES;
+       : fmt == GEMV_Q41  ? Fmt<GEMV_Q41>::ST_BYTES : Fmt<GEMV_Q8>::ST_BYTES;
 }
 
 int gemv_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStream_t st) {
   const size_t threads = (size_t)w->nrg * w->nst * w->nside * 64;
   const int blk = 256;
   const size_t grid = (threads + blk - 1) / blk;
-  if (w->fmt == GEMV_Q4)
+  if (w->fmt == GEMV_Q4 || w->fmt == GEMV_Q41)
     hipLaunchKernelGGL(repack_q4_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, dsc,
                        w->type, w->ne1, w->ne0, w->nrg, w->nst, w->nside, 0, -1);
   else if (w->fmt == GEMV_Q6K)
@@ -1094,6 +1149,8 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
     rc = launch_fmt<GEMV_Q6K>(p, nrt, R, nsides, epi, st);
   } else if (w->fmt == GEMV_Q8) {
     rc = launch_fmt<GEMV_Q8>(p, nrt, R, nsides, epi, st);
+  } else if (w->fmt == GEMV_Q41) {
+    rc = launch_fmt<GEMV_Q41>(p, nrt, R, nsides, epi, st);
   }
   if (rc) return rc;
   CWEN_HIP_TRY(hipGetLastError());

@@ -65,6 +65,22 @@ def q4_gguf(seed: int, M: int, K: int, key: int = 0) -> np.ndarray:
     return out.reshape(-1)
 
 
+def q4_1(seed: int, M: int, K: int, key: int = 0) -> np.ndarray:
+    """GGUF Q4_1: 20-byte blocks {f16 d; f16 m; u8 qs[16]}, w = n*d + m.  As a
+    quantiser would set them, m is near the block minimum: m = -(8 + N(0,1)/2) d."""
+    nb = K // QK4
+    g = rng(seed, 7, key)
+    sc = q4_scales(g, M * nb)
+    d = sc.view(np.float16).astype(np.float32)
+    m = _f16_bits(-(np.float32(8) + g.standard_normal(M * nb, dtype=np.float32) / np.float32(2)) * d)
+    qs = q4_nibble_bytes(g, M * nb * 16)
+    out = np.empty((M * nb, 20), dtype=np.uint8)
+    out[:, 0:2] = sc.view(np.uint8).reshape(-1, 2)
+    out[:, 2:4] = m.view(np.uint8).reshape(-1, 2)
+    out[:, 4:] = qs.reshape(-1, 16)
+    return out.reshape(-1)
+
+
 def q6_k(seed: int, M: int, K: int, key: int = 0) -> np.ndarray:
     """GGUF Q6_K: 210-byte super-blocks {ql[128] qh[64] i8 sc[16] f16 d}."""
     nsb = M * (K // QK_K)

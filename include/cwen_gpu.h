@@ -45,6 +45,8 @@ extern "C" {
 /* ggml / CWENR weight type ids -- the same numeric ids as run.c:97-103 */
 #define CWEN_T_F32      0
 #define CWEN_T_Q4_0     2    /* GGUF 18-byte blocks {f16 d; u8 qs[16]}          */
+#define CWEN_T_Q4_1     3    /* GGUF 20-byte blocks {f16 d; f16 m; u8 qs[16]},
+                                w = n*d + m (run.c:111, 571-588, 1026-1099)     */
 #define CWEN_T_Q8_0     8    /* GGUF 34-byte blocks {f16 d; i8 qs[32]}          */
 #define CWEN_T_Q6_K    14    /* GGUF 210-byte super-blocks of 256                */
 #define CWEN_T_Q4_0RS  101   /* CWENR split: qs[ne1][nb][16] + f16 sc[ne1][nb]   */

@@ -95,6 +95,23 @@ float orc_dot_q4_rsi(const uint8_t *qs, const uint16_t *sc, int side, const floa
   return sum;
 }
 
+/* run.c:1087-1096 scalar branch (GGUF 20-byte blocks {d, m, qs}): w = n*d + m,
+ * lo nibble -> y[j], hi -> y[j+16] */
+float orc_dot_q4_1(const uint8_t *blk20, const float *y, int K) {
+  int nb = K / 32;
+  float sum = 0;
+  for (int i = 0; i < nb; i++) {
+    const uint8_t *b = blk20 + (size_t)i * 20;
+    float d = orc_f16_to_f32(ld16(b)), m = orc_f16_to_f32(ld16(b + 2));
+    const float *yy = y + i * 32;
+    for (int j = 0; j < 16; j++) {
+      int x0 = b[4 + j] & 0xF, x1 = b[4 + j] >> 4;
+      sum += (x0 * d + m) * yy[j] + (x1 * d + m) * yy[j + 16];
+    }
+  }
+  return sum;
+}
+
 /* run.c:1248-1274 scalar branch */
 float orc_dot_q8_0(const uint8_t *blk34, const float *y, int K) {
   int nb = K / 32;
@@ -145,6 +162,7 @@ static float row_dot(const orc_tensor *W, const float *y, int i) {
                                            (const uint16_t *)W->scales + (size_t)i * nb * 2,
                                            W->pair_side, y, K);
     case ORC_Q8_0:   return orc_dot_q8_0(d + (size_t)i * nb * 34, y, K);
+    case ORC_Q4_1:   return orc_dot_q4_1(d + (size_t)i * nb * 20, y, K);
     case ORC_Q6_K:   return orc_dot_q6_K(d + (size_t)i * (K / 256) * 210, y, K);
     case ORC_F32: {
       const float *w = (const float *)W->data + (size_t)i * K;

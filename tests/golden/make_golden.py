@@ -92,7 +92,7 @@ def main() -> int:
     from oracle.binding import Reference
     R = Reference("avx2")
     v = {}
-    # batched GEMV, the five weight formats (B = 3)
+    # batched GEMV, the six weight formats (B = 3)
     M, K, B = 32, 512, 3
     X = synth.activations(31, B, K)
     v["gemv_X"] = X
@@ -105,6 +105,8 @@ def main() -> int:
     v["gemv_q4_0"], v["gemv_q4_0_Y"] = blk, R.gemvb(2, blk, None, K, M, X)
     blk = synth.q8_0(31, M, K)
     v["gemv_q8_0"], v["gemv_q8_0_Y"] = blk, R.gemvb(8, blk, None, K, M, X)
+    blk = synth.q4_1(31, M, K)
+    v["gemv_q4_1"], v["gemv_q4_1_Y"] = blk, R.gemvb(3, blk, None, K, M, X)
     K6 = 1024
     X6 = synth.activations(32, B, K6)
     blk = synth.q6_k(31, M, K6)

@@ -50,6 +50,8 @@ def test_gemvb_rsi_both_sides_bit_exact(oracle, gv):
 def test_gemvb_gguf_and_q6_k(oracle, gv):
     Y = oracle.gemvb(2, gv["gemv_q4_0"], None, 512, 32, gv["gemv_X"])
     assert rel_err(Y, gv["gemv_q4_0_Y"]) < 1e-5
+    Y = oracle.gemvb(3, gv["gemv_q4_1"], None, 512, 32, gv["gemv_X"])   # Q4_1: the AVX2 kernel's order
+    assert rel_err(Y, gv["gemv_q4_1_Y"]) < 1e-5
     Y = oracle.gemvb(14, gv["gemv_q6_k"], None, 1024, 32, gv["gemv_q6_k_X"])
     assert rel_err(Y, gv["gemv_q6_k_Y"]) < 1e-5
 

@@ -17,7 +17,7 @@ import pytest
 from cwen_amd import synth
 from util import rel_err
 
-T_Q4_0, T_Q8_0, T_Q6_K, T_RS, T_RSI = 2, 8, 14, 101, 102
+T_Q4_0, T_Q4_1, T_Q8_0, T_Q6_K, T_RS, T_RSI = 2, 3, 8, 14, 101, 102
 
 
 # ---------------------------------------------------------------- f16
@@ -106,6 +106,20 @@ def test_q4_gguf_vs_f64(oracle):
     assert rel_err(got, X.astype(np.float64) @ W.reshape(M, K).T) < 2e-6
 
 
+def test_q4_1_vs_f64(oracle):
+    """Q4_1 blocks {d, m, qs}: w = n*d + m, lo nibbles -> w[0..15], hi -> w[16..31]."""
+    M, K = 24, 512
+    blk = synth.q4_1(16, M, K).reshape(-1, 20)
+    d = np.ascontiguousarray(blk[:, 0:2]).view(np.float16).astype(np.float64)
+    m = np.ascontiguousarray(blk[:, 2:4]).view(np.float16).astype(np.float64)
+    q = blk[:, 4:].astype(np.int64)
+    n = np.concatenate([q & 0xF, q >> 4], axis=1).astype(np.float64)
+    W = (n * d + m).reshape(M, K)
+    X = synth.activations(16, 2, K)
+    got = oracle.gemvb(T_Q4_1, blk.ravel(), None, K, M, X)
+    assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
+
+
 def test_q8_0_vs_f64(oracle):
     M, K = 24, 256
     blk = synth.q8_0(14, M, K).reshape(-1, 34)
@@ -144,7 +158,7 @@ def test_scalar_paths_bit_exact_vs_reference_avx2(oracle, ref_avx2, wtype):
 
 
 @pytest.mark.parametrize("isa", ["avx2", "avx512"])
-@pytest.mark.parametrize("wtype", [T_Q4_0, T_RS, T_RSI, T_Q8_0, T_Q6_K])
+@pytest.mark.parametrize("wtype", [T_Q4_0, T_Q4_1, T_RS, T_RSI, T_Q8_0, T_Q6_K])
 def test_gemvb_vs_reference(oracle, isa, wtype):
     from oracle.binding import Reference, ref_lib_path, cpu_has_avx512
     if not ref_lib_path(isa).exists():
@@ -161,6 +175,8 @@ def test_gemvb_vs_reference(oracle, isa, wtype):
         data, sc = synth.q4_rsi(22, M, K)
     elif wtype == T_Q8_0:
         data, sc = synth.q8_0(22, M, K), None
+    elif wtype == T_Q4_1:
+        data, sc = synth.q4_1(22, M, K), None
     else:
         data, sc = synth.q6_k(22, M, K), None
     for B in (1, 3, 8, 16):

@@ -171,7 +171,7 @@ def test_argument_errors(env):
     with pytest.raises(gpu.CwenError):
         gpu.Weight(ctx, T_RS, qs2, sc2, 96, M)             # K not a multiple of 512
     with pytest.raises(gpu.CwenError):
-        gpu.Weight(ctx, 3, qs, sc, K, M)                   # Q4_1 is not a supported type
+        gpu.Weight(ctx, 13, qs, sc, K, M)                  # Q5_K is not a supported type
 
 
 @pytest.mark.slow
@@ -229,3 +229,23 @@ def test_mlp_block(env, oracle, H, I):
         if B == 8:
             h = oracle.silu_mul(oracle.gemvb(T_RSI, gq, gs, H, I, X, 0), oracle.gemvb(T_RSI, gq, gs, H, I, X, 1))
             assert rel_err(got - Y0, oracle.gemvb(T_RS, dq, ds, I, H, h)) <= TOL
+
+
+@pytest.mark.parametrize("M,K", [(16, 512), (100, 1024), (5120, 17408)])
+def test_q4_1_parity(env, oracle, M, K):
+    """Q4_1 (GGUF {d, m, qs}, w = n*d + m; the real model's ffn_down type):
+    the same GEMV kernel with its own dequant, vs the oracle's dot_q4_1 within
+    TOL, at the 27B down shape too; a column is bit-identical alone and
+    inside a block."""
+    torch, gpu, ctx = env
+    blk = synth.q4_1(109, M, K)
+    W = gpu.Weight(ctx, gpu.T_Q4_1, blk, None, K, M)
+    X = synth.activations(109, 16, K)
+    full = None
+    for B in (1, 5, 8, 16):
+        got = _run(env, W, X[:B])
+        assert rel_err(got, oracle.gemvb(gpu.T_Q4_1, blk, None, K, M, X[:B])) <= TOL, B
+        if B == 16:
+            full = got
+    one = _run(env, W, X[9:10])
+    assert np.array_equal(one[0].view(np.uint32), full[9].view(np.uint32))
