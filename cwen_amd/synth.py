@@ -81,6 +81,18 @@ def q4_1(seed: int, M: int, K: int, key: int = 0) -> np.ndarray:
     return out.reshape(-1)
 
 
+def q5_k(seed: int, M: int, K: int, key: int = 0) -> np.ndarray:
+    """GGUF Q5_K: 176-byte super-blocks {f16 d; f16 dmin; u8 scales[12];
+    u8 qh[32]; u8 qs[128]}: 5-bit quants and 6-bit scales/mins uniform,
+    d = |N(0, 0.002)|, dmin = |N(0, 0.002)|."""
+    nsb = M * (K // QK_K)
+    g = rng(seed, 8, key)
+    blk = g.integers(0, 256, size=(nsb, 176), dtype=np.uint8)
+    blk[:, 0:2] = _f16_bits(np.abs(g.standard_normal(nsb, dtype=np.float32) * np.float32(0.002))).view(np.uint8).reshape(-1, 2)
+    blk[:, 2:4] = _f16_bits(np.abs(g.standard_normal(nsb, dtype=np.float32) * np.float32(0.002))).view(np.uint8).reshape(-1, 2)
+    return blk.reshape(-1)
+
+
 def q6_k(seed: int, M: int, K: int, key: int = 0) -> np.ndarray:
     """GGUF Q6_K: 210-byte super-blocks {ql[128] qh[64] i8 sc[16] f16 d}."""
     nsb = M * (K // QK_K)

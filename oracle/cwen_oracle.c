@@ -112,6 +112,45 @@ float orc_dot_q4_1(const uint8_t *blk20, const float *y, int K) {
   return sum;
 }
 
+/* run.c:426-429 get_scale_min_k4: the 6-bit scale and min of sub-block j */
+static void scale_min_k4(int j, const uint8_t *q, uint8_t *d, uint8_t *m) {
+  if (j < 4) {
+    *d = q[j] & 63;
+    *m = q[j + 4] & 63;
+  } else {
+    *d = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+    *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+  }
+}
+
+/* run.c:1142-1156 scalar branch.  Super-block {f16 d; f16 dmin; u8 scales[12];
+ * u8 qh[32]; u8 qs[128]} (176 B per 256): for 64-group jj, weight l < 32 is
+ * (qs[32jj+l] & 15) + 16*(qh[l] bit 2jj), scale/min of sub-block 2jj; weight
+ * 32 + l is (qs[32jj+l] >> 4) + 16*(qh[l] bit 2jj+1), sub-block 2jj+1;
+ * w = d*sc*q - dmin*m. */
+float orc_dot_q5_K(const uint8_t *blk176, const float *y, int K) {
+  float sum = 0;
+  const float *yy = y;
+  for (int i = 0, nb = K / 256; i < nb; i++) {
+    const uint8_t *b = blk176 + (size_t)i * 176;
+    const uint8_t *scales = b + 4, *qh = b + 16, *ql = b + 48;
+    float d = orc_f16_to_f32(ld16(b)), min = orc_f16_to_f32(ld16(b + 2));
+    int is = 0;
+    uint8_t u1 = 1, u2 = 2;
+    for (int j = 0; j < 256; j += 64) {
+      uint8_t sc, m;
+      scale_min_k4(is + 0, scales, &sc, &m);
+      float d1 = d * sc, m1 = min * m;
+      scale_min_k4(is + 1, scales, &sc, &m);
+      float d2 = d * sc, m2 = min * m;
+      for (int l = 0; l < 32; l++) sum += (d1 * ((ql[l] & 0xF) + (qh[l] & u1 ? 16 : 0)) - m1) * yy[l];
+      for (int l = 0; l < 32; l++) sum += (d2 * ((ql[l] >> 4) + (qh[l] & u2 ? 16 : 0)) - m2) * yy[32 + l];
+      yy += 64; ql += 32; is += 2; u1 <<= 2; u2 <<= 2;
+    }
+  }
+  return sum;
+}
+
 /* run.c:1248-1274 scalar branch */
 float orc_dot_q8_0(const uint8_t *blk34, const float *y, int K) {
   int nb = K / 32;
@@ -163,6 +202,7 @@ static float row_dot(const orc_tensor *W, const float *y, int i) {
                                            W->pair_side, y, K);
     case ORC_Q8_0:   return orc_dot_q8_0(d + (size_t)i * nb * 34, y, K);
     case ORC_Q4_1:   return orc_dot_q4_1(d + (size_t)i * nb * 20, y, K);
+    case ORC_Q5_K:   return orc_dot_q5_K(d + (size_t)i * (K / 256) * 176, y, K);
     case ORC_Q6_K:   return orc_dot_q6_K(d + (size_t)i * (K / 256) * 210, y, K);
     case ORC_F32: {
       const float *w = (const float *)W->data + (size_t)i * K;
@@ -177,7 +217,7 @@ static float row_dot(const orc_tensor *W, const float *y, int i) {
 /* run.c:1577-1680 gemvb; per-column dots (the generic path, run.c:1666-1679) */
 int orc_gemvb(const orc_tensor *W, const float *X, int xs, float *Y, int ys, int B) {
   if (!W || W->ne0 <= 0 || W->ne1 <= 0 || B < 1) return -1;
-  if (W->ne0 % (W->type == ORC_Q6_K ? 256 : 32) != 0 && W->type != ORC_F32) return -1;
+  if (W->ne0 % (W->type == ORC_Q6_K || W->type == ORC_Q5_K ? 256 : 32) != 0 && W->type != ORC_F32) return -1;
   for (int i = 0; i < W->ne1; i++)
     for (int b = 0; b < B; b++)
       Y[(size_t)b * ys + i] = row_dot(W, X + (size_t)b * xs, i);

@@ -28,7 +28,7 @@ extern "C" {
 #endif
 
 /* ggml / CWENR type ids (run.c:97-103) */
-enum { ORC_F32 = 0, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8, ORC_Q6_K = 14,
+enum { ORC_F32 = 0, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 8, ORC_Q5_K = 13, ORC_Q6_K = 14,
        ORC_Q4_0RS = 101, ORC_Q4_0RSI = 102 };
 
 /* Mirrors the reference Tensor (run.c:132): ne0 = K (inputs), ne1 = M (rows). */
@@ -49,6 +49,7 @@ float orc_dot_q4_rsi(const uint8_t *qs, const uint16_t *sc, int side,
                      const float *y, int K);                                 /* run.c:942-975 */
 float orc_dot_q4_1(const uint8_t *blk20, const float *y, int K);            /* run.c:1087-1096 */
 float orc_dot_q8_0(const uint8_t *blk34, const float *y, int K);            /* run.c:1248-1274 */
+float orc_dot_q5_K(const uint8_t *blk176, const float *y, int K);           /* run.c:1142-1156 */
 float orc_dot_q6_K(const uint8_t *blk210, const float *y, int K);           /* run.c:1226-1245 */
 
 /* Y[b*ys+i] = row i of W . X[b*xs ..], b < B (run.c:1577-1680). */

@@ -92,7 +92,7 @@ def main() -> int:
     from oracle.binding import Reference
     R = Reference("avx2")
     v = {}
-    # batched GEMV, the six weight formats (B = 3)
+    # batched GEMV, the seven weight formats (B = 3)
     M, K, B = 32, 512, 3
     X = synth.activations(31, B, K)
     v["gemv_X"] = X
@@ -111,6 +111,8 @@ def main() -> int:
     X6 = synth.activations(32, B, K6)
     blk = synth.q6_k(31, M, K6)
     v["gemv_q6_k_X"], v["gemv_q6_k"], v["gemv_q6_k_Y"] = X6, blk, R.gemvb(14, blk, None, K6, M, X6)
+    blk = synth.q5_k(31, M, K6)
+    v["gemv_q5_k"], v["gemv_q5_k_Y"] = blk, R.gemvb(13, blk, None, K6, M, X6)
     # elementwise
     a, b, x, w = elementwise_inputs()
     v["silu_out"], v["rms_out"] = R.silu_mul(a, b), R.rmsnorm(x, w)

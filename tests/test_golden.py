@@ -54,6 +54,8 @@ def test_gemvb_gguf_and_q6_k(oracle, gv):
     assert rel_err(Y, gv["gemv_q4_1_Y"]) < 1e-5
     Y = oracle.gemvb(14, gv["gemv_q6_k"], None, 1024, 32, gv["gemv_q6_k_X"])
     assert rel_err(Y, gv["gemv_q6_k_Y"]) < 1e-5
+    Y = oracle.gemvb(13, gv["gemv_q5_k"], None, 1024, 32, gv["gemv_q6_k_X"])   # Q5_K: the AVX2 kernel's order
+    assert rel_err(Y, gv["gemv_q5_k_Y"]) < 1e-5
 
 
 def test_silu_mul_and_rmsnorm(oracle, gv):

@@ -17,7 +17,7 @@ import pytest
 from cwen_amd import synth
 from util import rel_err
 
-T_Q4_0, T_Q4_1, T_Q8_0, T_Q6_K, T_RS, T_RSI = 2, 3, 8, 14, 101, 102
+T_Q4_0, T_Q4_1, T_Q8_0, T_Q5_K, T_Q6_K, T_RS, T_RSI = 2, 3, 8, 13, 14, 101, 102
 
 
 # ---------------------------------------------------------------- f16
@@ -120,6 +120,28 @@ def test_q4_1_vs_f64(oracle):
     assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
 
 
+def test_q5_k_vs_f64(oracle):
+    """Q5_K from the GGUF block definition in f64 (6-bit scale/min unpacking
+    as ggml defines it, 5-bit quants split over qs nibbles and qh bits)."""
+    M, K = 4, 512
+    blk = synth.q5_k(17, M, K).reshape(-1, 176)
+    W = np.empty((blk.shape[0], 256))
+    for s, b in enumerate(blk):
+        d, dmin = (float(v) for v in b[0:4].view(np.float16))
+        sc8, qh, qs = b[4:16].astype(np.int64), b[16:48].astype(np.int64), b[48:176].astype(np.int64)
+        sc = [sc8[j] & 63 if j < 4 else (sc8[j + 4] & 15) | ((sc8[j - 4] >> 6) << 4) for j in range(8)]
+        mn = [sc8[j + 4] & 63 if j < 4 else (sc8[j + 4] >> 4) | ((sc8[j] >> 6) << 4) for j in range(8)]
+        for jj in range(4):
+            for l in range(32):
+                for half in range(2):
+                    q = ((qs[32 * jj + l] >> (4 * half)) & 15) + 16 * ((qh[l] >> (2 * jj + half)) & 1)
+                    sb = 2 * jj + half
+                    W[s, 64 * jj + 32 * half + l] = d * sc[sb] * q - dmin * mn[sb]
+    X = synth.activations(17, 2, K)
+    got = oracle.gemvb(T_Q5_K, blk.ravel(), None, K, M, X)
+    assert rel_err(got, X.astype(np.float64) @ W.reshape(M, K).T) < 2e-6
+
+
 def test_q8_0_vs_f64(oracle):
     M, K = 24, 256
     blk = synth.q8_0(14, M, K).reshape(-1, 34)
@@ -158,7 +180,7 @@ def test_scalar_paths_bit_exact_vs_reference_avx2(oracle, ref_avx2, wtype):
 
 
 @pytest.mark.parametrize("isa", ["avx2", "avx512"])
-@pytest.mark.parametrize("wtype", [T_Q4_0, T_Q4_1, T_RS, T_RSI, T_Q8_0, T_Q6_K])
+@pytest.mark.parametrize("wtype", [T_Q4_0, T_Q4_1, T_RS, T_RSI, T_Q8_0, T_Q5_K, T_Q6_K])
 def test_gemvb_vs_reference(oracle, isa, wtype):
     from oracle.binding import Reference, ref_lib_path, cpu_has_avx512
     if not ref_lib_path(isa).exists():
@@ -177,6 +199,8 @@ def test_gemvb_vs_reference(oracle, isa, wtype):
         data, sc = synth.q8_0(22, M, K), None
     elif wtype == T_Q4_1:
         data, sc = synth.q4_1(22, M, K), None
+    elif wtype == T_Q5_K:
+        data, sc = synth.q5_k(22, M, K), None
     else:
         data, sc = synth.q6_k(22, M, K), None
     for B in (1, 3, 8, 16):
