@@ -174,7 +174,7 @@ def time_each(fn, n: int, warmup: int, stream) -> list[float]:
 
 
 def extra_leg(steps: int, warmup: int) -> dict:
-    """c0 GGUF Q4_0 GEMV B=1, Q4_1 down GEMV B=8, c2 Q6_K head + argmax + walk at B=8, c3 GDN block
+    """c0 GGUF Q4_0 GEMV B=1, Q4_1 down and Q5_K ssm_out GEMVs at B=8, c2 Q6_K head + argmax + walk at B=8, c3 GDN block
     at B=8: average launch time over back-to-back launches (rotating enough
     copies that each launch streams from HBM), GB/s from the algorithmic bytes."""
     import torch
@@ -211,6 +211,19 @@ def extra_leg(steps: int, warmup: int) -> dict:
     out["q4_1_down_5120x17408_b8"] = {"ms": ms, "GB_s": q41_bytes / (ms * 1e-3) / 1e9,
                                       "frac_of_peak": q41_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
                                       "bytes": q41_bytes, "launches": "Q4_1 GEMV on f16 x (one launch)"}
+    del Ws
+
+    # Q5_K (the real model's ssm_out), 5120 x 6144 at B=8; 16 copies x 21.6 MB > MALL.
+    M5, K5, B5 = 5120, 6144, 8
+    Ws = [gpu.Weight(ctx, gpu.T_Q5_K, synth.q5_k(0, M5, K5, key=c), None, K5, M5) for c in range(16)]
+    xh = torch.from_numpy(synth.activations(0, B5, K5)).cuda().half()
+    y = torch.empty(B5, M5, device="cuda")
+    ms = time_launches(lambda i: gpu.gemvb_f16(ctx, Ws[i % len(Ws)], xh, y, B5, stream=stream), steps, warmup,
+                       stream)
+    q5_bytes = M5 * (K5 // 256) * 176 + B5 * K5 * 2 + B5 * M5 * 4
+    out["q5_k_ssm_out_5120x6144_b8"] = {"ms": ms, "GB_s": q5_bytes / (ms * 1e-3) / 1e9,
+                                        "frac_of_peak": q5_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
+                                        "bytes": q5_bytes, "launches": "Q5_K GEMV on f16 x (one launch)"}
     del Ws
 
     # c2: 638 MB head (> MALL), B=8, drafts = argmax w.p. 0.6

@@ -145,6 +145,7 @@ int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *sc
     case CWEN_T_Q4_0RSI: qbytes = nblk * 32; sbytes = nblk * 4; nside = 2; break;
     case CWEN_T_Q6_K: qbytes = (size_t)(ne0 / 256) * ne1 * 210; break;
     case CWEN_T_Q4_1: qbytes = nblk * 20; break;
+    case CWEN_T_Q5_K: qbytes = (size_t)(ne0 / 256) * ne1 * 176; break;
     default: qbytes = nblk * 34; break;  // Q8_0
   }
 

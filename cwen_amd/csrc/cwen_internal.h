@@ -19,7 +19,7 @@ constexpr int Q4_ROWS = 16;
 // K must be a whole number of super-tiles.
 constexpr int Q4_K_ALIGN = Q4_ST_K;
 
-enum { GEMV_Q4 = 0, GEMV_Q6K = 1, GEMV_Q8 = 2, GEMV_Q41 = 3 };
+enum { GEMV_Q4 = 0, GEMV_Q6K = 1, GEMV_Q8 = 2, GEMV_Q41 = 3, GEMV_Q5K = 4 };
 
 struct cwen_ctx {
   int device;
@@ -46,7 +46,7 @@ struct GemvGrid {
 struct cwen_weight {
   cwen_ctx *ctx;
   int type;                 // CWEN_T_*
-  int fmt;                  // GEMV_Q4 / GEMV_Q6K / GEMV_Q8 / GEMV_Q41
+  int fmt;                  // GEMV_Q4 / GEMV_Q6K / GEMV_Q8 / GEMV_Q41 / GEMV_Q5K
   int ne0, ne1;             // K, M
   int nside;                // 2 for an interleaved pair, else 1
   int nrg, nst;             // 16-row groups, 512-wide K super-tiles

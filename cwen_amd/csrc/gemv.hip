@@ -87,6 +87,19 @@ template <> struct Fmt<GEMV_Q41> {
   static constexpr uint32_t ST_BYTES = 5120, SC_OFS = 4096;
   static constexpr int TV = 1;
 };
+// Q5_K: the low 4 bits in the Q4_0 nibble layout, then per lane one dword
+// of fifth bits per tile (kQ5HiPos), then per lane the 4 sub-blocks'
+// (d*sc, -dmin*m) f16 pairs.
+template <> struct Fmt<GEMV_Q5K> {
+  static constexpr uint32_t ST_BYTES = 6144, HI_OFS = 4096, SC_OFS = 5120;
+  static constexpr int TV = 1;
+};
+// Q5_K fifth bit of weight e of K run m sits at bit kQ5HiPos[e] + m of the
+// tile's dword, so that the unpack's shifts (h >> m for elements 0-3,
+// h >> (8 + m) for 4-5, h << (8 - m) for 6-7) bring it next to the nibble:
+// to value 16 (bit 4 / 20) of a plain element, 256 (bit 8 / 24) of an
+// element read as 16 * n.
+__constant__ int kQ5HiPos[8] = {4, 20, 8, 24, 12, 28, 0, 16};
 
 // (q & mask) | magic in one VOP3 op.  gfx9 VOP3 takes no literal and reads at
 // most one scalar, so the mask comes from an SGPR and the magic from a VGPR.
@@ -99,6 +112,7 @@ __device__ __forceinline__ uint32_t and_or(uint32_t q, uint32_t mask_s, uint32_t
 struct Unpack {
   uint32_t lo, hi;     // SGPR masks 0x000F000F, 0x00F000F0
   uint32_t h0, h1;     // SGPR masks 0x00300030, 0x03000300 (Q6_K high bits)
+  uint32_t b4, b8;     // SGPR masks 0x00100010, 0x01000100 (Q5_K fifth bits)
   uint32_t magic;      // VGPR 0x64006400
 };
 // Materialise the constants once, opaque to the compiler, so the loop does
@@ -109,6 +123,8 @@ __device__ __forceinline__ Unpack unpack_consts() {
   asm volatile("s_mov_b32 %0, 0x00f000f0" : "=s"(u.hi));
   asm volatile("s_mov_b32 %0, 0x00300030" : "=s"(u.h0));
   asm volatile("s_mov_b32 %0, 0x03000300" : "=s"(u.h1));
+  asm volatile("s_mov_b32 %0, 0x00100010" : "=s"(u.b4));
+  asm volatile("s_mov_b32 %0, 0x01000100" : "=s"(u.b8));
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(u.magic));
   return u;
 }
@@ -144,6 +160,24 @@ __device__ __forceinline__ half8_t unpack8_q41(uint32_t q, const Unpack &u, half
   const uint32_t t1 = and_or(q, u.hi, u.magic);    // 1024 + 16 n1, 1024 + 16 n5
   const uint32_t t2 = and_or(q2, u.lo, u.magic);
   const uint32_t t3 = and_or(q2, u.hi, u.magic);
+  const half2_t n0 = __builtin_bit_cast(half2_t, t0) - h2c(1024.f);
+  const half2_t n1 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t1), h2c(0.0625f), h2c(-64.f));
+  const half2_t n2 = __builtin_bit_cast(half2_t, t2) - h2c(1024.f);
+  const half2_t n3 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t3), h2c(0.0625f), h2c(-64.f));
+  return pack8(__builtin_elementwise_fma(n0, dd, mm), __builtin_elementwise_fma(n1, dd, mm),
+               __builtin_elementwise_fma(n2, dd, mm), __builtin_elementwise_fma(n3, dd, mm));
+}
+
+// Q5_K (w = q*D + M, D = d*sc, M = -dmin*m, q = 5 bits): the nibble
+// extraction of unpack8_q4 with the fifth bit ORed in (ha = h >> m,
+// hb = h >> (8 + m), hc = h << (8 - m) for K run m), q exact, then one fma.
+__device__ __forceinline__ half8_t unpack8_q5(uint32_t q, uint32_t ha, uint32_t hb, uint32_t hc, const Unpack &u,
+                                              half2_t dd, half2_t mm) {
+  const uint32_t q2 = q >> 8;
+  const uint32_t t0 = and_or(ha, u.b4, and_or(q, u.lo, u.magic));    // 1024 + q0, 1024 + q4
+  const uint32_t t1 = and_or(ha, u.b8, and_or(q, u.hi, u.magic));    // 1024 + 16 q1, 1024 + 16 q5
+  const uint32_t t2 = and_or(hb, u.b4, and_or(q2, u.lo, u.magic));
+  const uint32_t t3 = and_or(hc, u.b8, and_or(q2, u.hi, u.magic));
   const half2_t n0 = __builtin_bit_cast(half2_t, t0) - h2c(1024.f);
   const half2_t n1 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t1), h2c(0.0625f), h2c(-64.f));
   const half2_t n2 = __builtin_bit_cast(half2_t, t2) - h2c(1024.f);
@@ -336,7 +370,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     const int rgc = rgs[r] < p.nrg ? rgs[r] : p.nrg - 1;  // idle streams read a valid tile
     wofs[r] = (((uint32_t)rgc * p.nst + st0) * p.nsw + side) * F::ST_BYTES;
   }
-  const uint32_t lq = lane * 16, ls = F::SC_OFS + lane * (FMT == GEMV_Q41 ? 16 : 8);
+  constexpr bool DM = FMT == GEMV_Q41 || FMT == GEMV_Q5K;  // per-block (scale, offset) pairs
+  const uint32_t lq = lane * 16, ls = F::SC_OFS + lane * (DM ? 16 : 8);
 
   // Activation staging: this wave copies columns c = wave + WAVES*i; lane
   // copies f16 unit `lane` (K elements 8*lane .. 8*lane+7) of the column's
@@ -360,17 +395,23 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   uint4 xs[XL][XN ? 2 : 1];
   uint4 wq[TILES][NSET][TV];
   // Scales of a round: 4 f16 (one per tile), or for Q4_1 4 (d, m) pairs.
-  using ScT = std::conditional_t<FMT == GEMV_Q41, uint4, uint2>;
+  using ScT = std::conditional_t<DM, uint4, uint2>;
   ScT sc[NSET];
   auto sc_load = [&](uint32_t soff) __attribute__((always_inline)) -> ScT {
-    if constexpr (FMT == GEMV_Q41) return bload16(wr, ls, soff);
+    if constexpr (DM) return bload16(wr, ls, soff);
     else return bload8(wr, ls, soff);
+  };
+  uint4 h5[NSET];             // Q5_K: fifth bits of the round's 4 tiles (one dword each)
+  auto h5_load = [&](uint32_t soff) __attribute__((always_inline)) -> uint4 {
+    if constexpr (FMT == GEMV_Q5K) return bload16(wr, F::HI_OFS + lq, soff);
+    else return make_uint4(0u, 0u, 0u, 0u);
   };
   uint32_t dq[NSET];          // Q6_K: f16 d of the round's two super-blocks
   uint4 hq[2][NSET];          // Q6_K: high bits of tile pairs (0,1) and (2,3)
 #pragma unroll
   for (int q = 0; q < NSET; ++q) {
     sc[q] = sc_load(wofs[q]);
+    h5[q] = h5_load(wofs[q]);
     if constexpr (FMT == GEMV_Q6K) dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q], 0);
   }
   auto stage_load = [&](uint32_t soff) __attribute__((always_inline)) {
@@ -457,7 +498,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
           dd[q][u][1] = (half2_t){ds[1], ds[1]};
         }
       } else {
-        if constexpr (FMT == GEMV_Q41) {  // dd[q][u][0] = d, dd[q][u][1] = m
+        if constexpr (DM) {  // dd[q][u][0] = scale, dd[q][u][1] = offset
           const uint32_t w4[4] = {sc[q].x, sc[q].y, sc[q].z, sc[q].w};
 #pragma unroll
           for (int u = 0; u < TILES; ++u) {
@@ -472,9 +513,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
         }
       }
     }
+    uint4 h5c[NSET];  // Q5_K: this round's fifth bits (h5 is reloaded for the next)
 #pragma unroll
     for (int q = 0; q < NSET; ++q) {
+      h5c[q] = h5[q];
       sc[q] = sc_load(wofs[q] + nr * sstride);
+      if constexpr (FMT == GEMV_Q5K) h5[q] = h5_load(wofs[q] + nr * sstride);
       if constexpr (FMT == GEMV_Q6K)
         dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q] + nr * sstride, 0);
     }
@@ -490,6 +534,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
           b[q][1] = unpack8_q4(wq[j][q][0].y, uc, dd[q][j][0]);
           b[q][2] = unpack8_q4(wq[j][q][0].z, uc, dd[q][j][0]);
           b[q][3] = unpack8_q4(wq[j][q][0].w, uc, dd[q][j][0]);
+        } else if constexpr (FMT == GEMV_Q5K) {
+          const uint32_t h = j == 0 ? h5c[q].x : j == 1 ? h5c[q].y : j == 2 ? h5c[q].z : h5c[q].w;
+          const half2_t d5 = dd[q][j][0], m5 = dd[q][j][1];
+          b[q][0] = unpack8_q5(wq[j][q][0].x, h, h >> 8, h << 8, uc, d5, m5);
+          b[q][1] = unpack8_q5(wq[j][q][0].y, h >> 1, h >> 9, h << 7, uc, d5, m5);
+          b[q][2] = unpack8_q5(wq[j][q][0].z, h >> 2, h >> 10, h << 6, uc, d5, m5);
+          b[q][3] = unpack8_q5(wq[j][q][0].w, h >> 3, h >> 11, h << 5, uc, d5, m5);
         } else if constexpr (FMT == GEMV_Q41) {
           b[q][0] = unpack8_q41(wq[j][q][0].x, uc, dd[q][j][0], dd[q][j][1]);
           b[q][1] = unpack8_q41(wq[j][q][0].y, uc, dd[q][j][0], dd[q][j][1]);
@@ -811,6 +862,61 @@ __device__ inline int q6_value(const uint8_t *b, int j) {
 // Bit position of weight e's high pair in the run's dword (see unpack8_q6).
 __constant__ int kQ6HiPos[8] = {4, 20, 8, 24, 6, 22, 10, 26};
 
+// Q5_K (GGUF 176-byte super-blocks, run.c:1142-1156): lane l = 16g + n gets,
+// for each tile u, sub-block g of that tile for row n (32 weights, one
+// Q5_K sub-block): the low 4 bits in the Q4_0 nibble layout, the fifth bits
+// in one dword (kQ5HiPos), and (f16(d*sc), f16(-dmin*m)) of the sub-block.
+__global__ void repack_q5k_kernel(uint8_t *dst, const uint8_t *src, int M, int K, int nrg, int nst) {
+  const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t total = (size_t)nrg * nst * 64;
+  if (id >= total) return;
+  const int lane = (int)(id & 63);
+  const size_t t = id >> 6;
+  const int st = (int)(t % nst);
+  const int rg = (int)(t / nst);
+  const int n = lane & 15, g = lane >> 4;
+  const int row = rg * Q4_ROWS + n;
+  const int nsb = K / 256;
+  using F = Fmt<GEMV_Q5K>;
+  uint8_t *stile = dst + ((size_t)rg * nst + st) * F::ST_BYTES;
+  uint32_t hw[TILES], dm[TILES];
+  for (int u = 0; u < TILES; ++u) {
+    const int k0 = st * Q4_ST_K + u * Q4_TILE_K + g * 32;   // first K of the lane's sub-block
+    const uint8_t *b = (row < M) ? src + ((size_t)row * nsb + k0 / 256) * 176 : nullptr;
+    const int sb = (k0 & 255) / 32, jj = sb / 2, hs = sb & 1;
+    uint32_t lo[4] = {0, 0, 0, 0};
+    hw[u] = 0;
+    dm[u] = 0;   // rows past M: zero weights
+    if (b) {
+      const uint8_t *scales = b + 4, *qh = b + 16, *ql = b + 48 + 32 * jj;
+      for (int m = 0; m < 4; ++m)
+        for (int e = 0; e < 8; ++e) {
+          const int l = 8 * m + e;   // weight l of the sub-block
+          const uint32_t nib = hs ? (ql[l] >> 4) : (ql[l] & 15u);
+          const uint32_t h5 = (qh[l] >> (2 * jj + hs)) & 1u;
+          lo[m] |= nib << (4 * kNibPos[e]);
+          hw[u] |= h5 << (kQ5HiPos[e] + m);
+        }
+      // run.c:426-429 get_scale_min_k4
+      int sc, mn;
+      if (sb < 4) {
+        sc = scales[sb] & 63;
+        mn = scales[sb + 4] & 63;
+      } else {
+        sc = (scales[sb + 4] & 0xF) | ((scales[sb - 4] >> 6) << 4);
+        mn = (scales[sb + 4] >> 4) | ((scales[sb] >> 6) << 4);
+      }
+      const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(b[0] | (b[1] << 8)));
+      const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(b[2] | (b[3] << 8)));
+      const _Float16 D = (_Float16)(d * (float)sc), Mo = (_Float16)(-(dmin * (float)mn));
+      dm[u] = (uint32_t)__builtin_bit_cast(uint16_t, D) | ((uint32_t)__builtin_bit_cast(uint16_t, Mo) << 16);
+    }
+    *(uint4 *)(stile + u * 1024 + lane * 16) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  }
+  *(uint4 *)(stile + F::HI_OFS + lane * 16) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  *(uint4 *)(stile + F::SC_OFS + lane * 16) = make_uint4(dm[0], dm[1], dm[2], dm[3]);
+}
+
 __global__ void repack_q6k_kernel(uint8_t *dst, const uint8_t *src, int M, int K, int nrg, int nst) {
   const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   const size_t total = (size_t)nrg * nst * 64;
@@ -977,13 +1083,15 @@ int gemv_fmt_of(int type) {
     case CWEN_T_Q6_K: return GEMV_Q6K;
     case CWEN_T_Q8_0: return GEMV_Q8;
     case CWEN_T_Q4_1: return GEMV_Q41;
+    case CWEN_T_Q5_K: return GEMV_Q5K;
     default: return -1;
   }
 }
 
 size_t gemv_st_bytes(int fmt) {
   return fmt == GEMV_Q4 ? Fmt<GEMV_Q4>::ST_BYTES : fmt == GEMV_Q6K ? Fmt<GEMV_Q6K>::ST_BYTES
-       : fmt == GEMV_Q41  ? Fmt<GEMV_Q41>::ST_BYTES : Fmt<GEMV_Q8>::ST_BYTES;
+       : fmt == GEMV_Q41  ? Fmt<GEMV_Q41>::ST_BYTES : fmt == GEMV_Q5K ? Fmt<GEMV_Q5K>::ST_BYTES
+                          : Fmt<GEMV_Q8>::ST_BYTES;
 }
 
 int gemv_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStream_t st) {
@@ -995,6 +1103,9 @@ int gemv_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStr
                        w->type, w->ne1, w->ne0, w->nrg, w->nst, w->nside, 0, -1);
   else if (w->fmt == GEMV_Q6K)
     hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, w->ne1,
+                       w->ne0, w->nrg, w->nst);
+  else if (w->fmt == GEMV_Q5K)
+    hipLaunchKernelGGL(repack_q5k_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, w->ne1,
                        w->ne0, w->nrg, w->nst);
   else
     hipLaunchKernelGGL(repack_q8_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, w->ne1,
@@ -1151,6 +1262,8 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
     rc = launch_fmt<GEMV_Q8>(p, nrt, R, nsides, epi, st);
   } else if (w->fmt == GEMV_Q41) {
     rc = launch_fmt<GEMV_Q41>(p, nrt, R, nsides, epi, st);
+  } else if (w->fmt == GEMV_Q5K) {
+    rc = launch_fmt<GEMV_Q5K>(p, nrt, R, nsides, epi, st);
   }
   if (rc) return rc;
   CWEN_HIP_TRY(hipGetLastError());

@@ -18,7 +18,7 @@ CWEN_OK = 0
 CWEN_ERANGE = -6
 ERRORS = {-1: "EINVAL", -2: "EHIP", -3: "ENOMEM", -4: "ETYPE", -5: "ESCRATCH", -6: "ERANGE"}
 
-T_F32, T_Q4_0, T_Q4_1, T_Q8_0, T_Q6_K, T_Q4_0RS, T_Q4_0RSI = 0, 2, 3, 8, 14, 101, 102
+T_F32, T_Q4_0, T_Q4_1, T_Q8_0, T_Q5_K, T_Q6_K, T_Q4_0RS, T_Q4_0RSI = 0, 2, 3, 8, 13, 14, 101, 102
 BMAX = 16
 
 # (name, restype, argtypes) of every exported entry point.

@@ -48,6 +48,9 @@ extern "C" {
 #define CWEN_T_Q4_1     3    /* GGUF 20-byte blocks {f16 d; f16 m; u8 qs[16]},
                                 w = n*d + m (run.c:111, 571-588, 1026-1099)     */
 #define CWEN_T_Q8_0     8    /* GGUF 34-byte blocks {f16 d; i8 qs[32]}          */
+#define CWEN_T_Q5_K    13    /* GGUF 176-byte super-blocks of 256 {f16 d, dmin;
+                                u8 scales[12]; u8 qh[32]; u8 qs[128]}
+                                (run.c:113-115, 426-429, 1100-1158)              */
 #define CWEN_T_Q6_K    14    /* GGUF 210-byte super-blocks of 256                */
 #define CWEN_T_Q4_0RS  101   /* CWENR split: qs[ne1][nb][16] + f16 sc[ne1][nb]   */
 #define CWEN_T_Q4_0RSI 102   /* CWENR interleaved pair: qs[ne1][nb][A16|B16],

@@ -171,7 +171,7 @@ def test_argument_errors(env):
     with pytest.raises(gpu.CwenError):
         gpu.Weight(ctx, T_RS, qs2, sc2, 96, M)             # K not a multiple of 512
     with pytest.raises(gpu.CwenError):
-        gpu.Weight(ctx, 13, qs, sc, K, M)                  # Q5_K is not a supported type
+        gpu.Weight(ctx, 1, qs, sc, K, M)                   # F16 is not a supported type
 
 
 @pytest.mark.slow
@@ -249,3 +249,23 @@ def test_q4_1_parity(env, oracle, M, K):
             full = got
     one = _run(env, W, X[9:10])
     assert np.array_equal(one[0].view(np.uint32), full[9].view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K", [(16, 512), (100, 1024), (5120, 6144)])
+def test_q5_k_parity(env, oracle, M, K):
+    """Q5_K (the real model's ssm_out type, here at its 5120 x 6144 shape):
+    the low nibbles in the Q4_0 layout, the fifth bits ORed in by the unpack,
+    (d*sc, -dmin*m) per sub-block rounded to f16 at upload.  Within TOL of
+    the oracle's dot_q5_K; a column is bit-identical alone and in a block."""
+    torch, gpu, ctx = env
+    blk = synth.q5_k(110, M, K)
+    W = gpu.Weight(ctx, gpu.T_Q5_K, blk, None, K, M)
+    X = synth.activations(110, 16, K)
+    full = None
+    for B in (1, 5, 8, 16):
+        got = _run(env, W, X[:B])
+        assert rel_err(got, oracle.gemvb(gpu.T_Q5_K, blk, None, K, M, X[:B])) <= TOL, B
+        if B == 16:
+            full = got
+    one = _run(env, W, X[4:5])
+    assert np.array_equal(one[0].view(np.uint32), full[4].view(np.uint32))
