@@ -137,12 +137,14 @@ def rsi_side(qs: np.ndarray, sc: np.ndarray, M: int, K: int, side: int) -> tuple
 
 
 # ---------------------------------------------------------------- whole model
-def model_tensors(cfg: dict, seed: int = 0):
+def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False):
     """Seeded random-init tensors of the hybrid decoder, in the reference's
     layouts: yields (layer, tensor id, type, data, scales, ne0, ne1); layer -1
     for the global tensors.  Q4_0 matrices are CWENR (RS, or RSI for the
     gate/up and k/v pairs), the head Q6_K, the embedding Q4_0RS; norms, conv
-    taps and gate parameters F32."""
+    taps and gate parameters F32.  real_types: the GGUF types the real
+    model mixes in -- ffn_down of every other layer in Q4_1, every ssm_out
+    in Q5_K."""
     from . import gpu as G
     H, I, V = cfg["d_model"], cfg["d_ffn"], cfg["vocab"]
     nkh, nvh = cfg["gdn_nkh"], cfg["gdn_nvh"]
@@ -165,15 +167,21 @@ def model_tensors(cfg: dict, seed: int = 0):
         yield l, G.POST_NORM, G.T_F32, norm_w(k0 + 2, H), None, H, 1
         qs, sc = q4_rsi(seed, I, H, key=k0 + 3)
         yield l, G.FFN_GATE_UP, G.T_Q4_0RSI, qs, sc, H, I
-        qs, sc = q4_rs(seed, H, I, key=k0 + 4)
-        yield l, G.FFN_DOWN, G.T_Q4_0RS, qs, sc, I, H
+        if real_types and l % 2 == 0:
+            yield l, G.FFN_DOWN, G.T_Q4_1, q4_1(seed, H, I, key=k0 + 4), None, I, H
+        else:
+            qs, sc = q4_rs(seed, H, I, key=k0 + 4)
+            yield l, G.FFN_DOWN, G.T_Q4_0RS, qs, sc, I, H
         if not full:
             for tid, M, key in ((G.ATTN_QKV, C, 5), (G.ATTN_GATE, Zh, 6), (G.SSM_ALPHA, nvh, 7),
                                 (G.SSM_BETA, nvh, 8)):
                 qs, sc = q4_rs(seed, M, H, key=k0 + key)
                 yield l, tid, G.T_Q4_0RS, qs, sc, H, M
-            qs, sc = q4_rs(seed, H, Zh, key=k0 + 9)
-            yield l, G.SSM_OUT, G.T_Q4_0RS, qs, sc, Zh, H
+            if real_types:
+                yield l, G.SSM_OUT, G.T_Q5_K, q5_k(seed, H, Zh, key=k0 + 9), None, Zh, H
+            else:
+                qs, sc = q4_rs(seed, H, Zh, key=k0 + 9)
+                yield l, G.SSM_OUT, G.T_Q4_0RS, qs, sc, Zh, H
             g = rng(seed, 21, k0)
             yield l, G.SSM_A, G.T_F32, (-np.exp(g.uniform(-1, 1, nvh))).astype(f32), None, nvh, 1
             yield l, G.SSM_DT, G.T_F32, (0.5 * g.standard_normal(nvh)).astype(f32), None, nvh, 1

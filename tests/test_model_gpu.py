@@ -101,6 +101,41 @@ def test_forward_parity_across_key_chunks(env, oracle):
         assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
 
 
+def test_real_model_types(env, oracle):
+    """The real model's mix of GGUF types: Q4_1 ffn_down in every other layer
+    and Q5_K ssm_out in every GDN layer (the producers of the split RMSNorm's
+    operand are then Q4_1 / Q5_K GEMVs).  Forward parity vs the oracle with
+    the same tolerance, a block equal to single positions bit for bit, and
+    speculative decode equal to serial decode."""
+    gpu, ctx, _, _ = env
+    tensors = list(synth.model_tensors(CFG, seed=3, real_types=True))
+    assert {t[2] for t in tensors} >= {gpu.T_Q4_1, gpu.T_Q5_K}
+    m = gpu.Model(ctx, **CFG)
+    for t in tensors:
+        m.set(*t)
+    toks = synth.prompt_tokens(4, 24, CFG["vocab"])
+    ref, tol = _oracle_logits(oracle, tensors, toks)
+    got = []
+    for b0, B in ((0, 8), (8, 16)):
+        m.forward(toks[b0:b0 + B])
+        got.append(m.logits(B))
+    got = np.concatenate(got)
+    for p in range(len(toks)):
+        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
+    m.reset()
+    singles = []
+    for p in range(8):
+        m.forward(toks[p:p + 1])
+        singles.append(m.logits(1)[0])
+    assert np.array_equal(np.stack(singles).view(np.uint32), got[:8].view(np.uint32))
+    prompt = synth.prompt_tokens(5, 48, CFG["vocab"], period=13, noise=0.05)
+    m.reset()
+    serial = m.generate_serial(prompt, 40)
+    spec, st = m.generate_spec(prompt, 40, n_key=2)
+    assert np.array_equal(spec, serial)
+    m.free()
+
+
 @pytest.mark.parametrize("B", [4, 8, 16])
 def test_block_equals_serial_bitwise(env, B):
     """Every block size takes the same path (the producer writes the f16
