@@ -147,7 +147,8 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
 // ... up to the block's last position (the partials are per chunk, so the
 // mapping does not change the arithmetic).
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-constexpr int QROW = HD + 4, KROW = HD + 4, VROW = TC + 4, PROW = TC + 4;
+constexpr int KROW = HD + 4, VROW = TC + 4, PROW = TC + 4;
+constexpr int QT_WAVE = 2;   // 16-query tiles per wave held in registers (nq <= 4 * 2 * 16)
 constexpr int KV_FLOATS = TC * KROW > HD * VROW ? TC * KROW : HD * VROW;
 
 __device__ __forceinline__ float max16(float m) {
@@ -164,29 +165,25 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
   const int pbase = *p.last + 1;
   const int tlast = min(pbase + p.B - 1, p.max_ctx - 1);  // last position of the block
   if ((int)blockIdx.x * TC > tlast) return;
-  float *Qs = sm;                              // [MT*16][QROW], rows >= nq zero
-  float *KV = Qs + MT * 16 * QROW;             // K [TC][KROW], then V^T [HD][VROW]
+  float *KV = sm;                              // K [TC][KROW], then V^T [HD][VROW]
   float *Ps = KV + KV_FLOATS;                  // [MT*16][PROW]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
   const float scale = 1.f / sqrtf((float)HD);
-  // Global -> LDS copies keep QB (queries) or KV_L (key/value rows) loads
-  // per thread in flight before the first store.
-  constexpr int QB = 8;
-  for (int e0 = 0; e0 < MT * 16 * (HD / 4); e0 += 256 * QB) {  // query (b, m) -> head hkv*kvm + m
-    float4 t[QB];
+  // The score phase's queries stay in registers: wave w holds 16-query
+  // tiles w and w + 4, lane (lr, lg) the HD/4 dims lg*HD/4 .. of query row
+  // lr of each (rows >= nq zero).  Keeping them out of LDS leaves room for
+  // several workgroups per CU.
+  float4 qreg[QT_WAVE][HD / 16];
 #pragma unroll
-    for (int u = 0; u < QB; ++u) {
-      const int e = e0 + tid + 256 * u, qi = e / (HD / 4), d4 = e % (HD / 4);
-      t[u] = (float4){0.f, 0.f, 0.f, 0.f};
-      if (qi < nq) t[u] = *(const float4 *)(p.q + ((size_t)(qi / kvm) * p.NH + hkv * kvm + qi % kvm) * HD + d4 * 4);
-    }
+  for (int t = 0; t < QT_WAVE; ++t) {
+    const int qi = (wave + 4 * t) * 16 + lr;
 #pragma unroll
-    for (int u = 0; u < QB; ++u) {
-      const int e = e0 + tid + 256 * u;
-      if (e < MT * 16 * (HD / 4)) *(float4 *)(Qs + (e / (HD / 4)) * QROW + (e % (HD / 4)) * 4) = t[u];
-    }
+    for (int k = 0; k < HD / 16; ++k)
+      qreg[t][k] = qi < nq ? *(const float4 *)(p.q + ((size_t)(qi / kvm) * p.NH + hkv * kvm + qi % kvm) * HD +
+                                              lg * (HD / 4) + 4 * k)
+                           : (float4){0.f, 0.f, 0.f, 0.f};
   }
   constexpr int KV_L = TC * (HD / 4) / 256;    // float4 of a chunk's K (or V) rows per thread
   for (int c = blockIdx.x; c * TC <= tlast; c += gridDim.x) {
@@ -205,13 +202,15 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
     for (int u = 0; u < KV_L; ++u) *(float4 *)(KV + (wave + 4 * u) * KROW + lane * 4) = kv[u];
     __syncthreads();
     // scores and the chunk softmax, one 16-query tile per wave
-    for (int mt = wave; mt < MT; mt += 4) {
+#pragma unroll
+    for (int t = 0; t < QT_WAVE; ++t) {
+      const int mt = wave + 4 * t;
+      if (mt >= MT) break;
       f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-      const float *qa = Qs + (mt * 16 + lr) * QROW + lg * (HD / 4);
       const float *k0 = KV + lr * KROW + lg * (HD / 4), *k1 = k0 + 16 * KROW;
-#pragma unroll 4
+#pragma unroll
       for (int k = 0; k < HD / 4; k += 4) {
-        const float4 a = *(const float4 *)(qa + k), b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
+        const float4 a = qreg[t][k / 4], b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b0.x, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b1.x, s1, 0, 0, 0);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b0.y, s0, 0, 0, 0);
@@ -382,7 +381,8 @@ int attention_launch(const float *qfull, int qfs, const float *kx, const float *
   hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
   const int nwg = p.nchunk < ATTN_CHUNK_WGS ? p.nchunk : ATTN_CHUNK_WGS;
   const int MT = (nq + 15) / 16;
-  const size_t lds = ((size_t)MT * 16 * (QROW + PROW) + KV_FLOATS) * sizeof(float);
+  if (MT > 4 * QT_WAVE) return CWEN_EINVAL;   // query tiles beyond the waves' registers
+  const size_t lds = ((size_t)MT * 16 * PROW + KV_FLOATS) * sizeof(float);
   if (lds > 160 * 1024) return CWEN_EINVAL;
   int rc;
   if ((rc = attention_init())) return rc;
