@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
 // mapping does not change the arithmetic).
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int KROW = HD + 4, VROW = TC + 4, PROW = TC + 4;
-constexpr int QT_WAVE = 2;   // 16-query tiles per wave held in registers (nq <= 4 * 2 * 16)
+constexpr int QT_MAX = 2;    // 16-query tiles per wave held in registers (nq <= 4 * 2 * 16)
 constexpr int KV_FLOATS = TC * KROW > HD * VROW ? TC * KROW : HD * VROW;
 
 __device__ __forceinline__ float max16(float m) {
@@ -156,6 +156,8 @@ __device__ __forceinline__ float max16(float m) {
   m = fmaxf(m, dpp<0x141>(m)); return fmaxf(m, dpp<0x140>(m));
 }
 
+// QT: 16-query tiles per wave (1 when the block has at most 4 tiles).
+template <int QT>
 __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
   extern __shared__ __align__(16) float sm[];
   const int hkv = blockIdx.y;
@@ -175,9 +177,9 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
   // tiles w and w + 4, lane (lr, lg) the HD/4 dims lg*HD/4 .. of query row
   // lr of each (rows >= nq zero).  Keeping them out of LDS leaves room for
   // several workgroups per CU.
-  float4 qreg[QT_WAVE][HD / 16];
+  float4 qreg[QT][HD / 16];
 #pragma unroll
-  for (int t = 0; t < QT_WAVE; ++t) {
+  for (int t = 0; t < QT; ++t) {
     const int qi = (wave + 4 * t) * 16 + lr;
 #pragma unroll
     for (int k = 0; k < HD / 16; ++k)
@@ -203,22 +205,53 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
     __syncthreads();
     // scores and the chunk softmax, one 16-query tile per wave
 #pragma unroll
-    for (int t = 0; t < QT_WAVE; ++t) {
+    for (int t = 0; t < QT; ++t) {
       const int mt = wave + 4 * t;
       if (mt >= MT) break;
+      // QT == 1: four independent accumulators per 16 keys (the lane
+      // group's K run split in halves), summed at the end in a fixed order,
+      // for shorter MFMA dependency chains; QT == 2 keeps two (registers).
       f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
       const float *k0 = KV + lr * KROW + lg * (HD / 4), *k1 = k0 + 16 * KROW;
+      if constexpr (QT == 2) {
 #pragma unroll
-      for (int k = 0; k < HD / 4; k += 4) {
+        for (int k = 0; k < HD / 4; k += 4) {
+          const float4 a = qreg[t][k / 4], b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
+          s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b0.x, s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b1.x, s1, 0, 0, 0);
+          s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b0.y, s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b1.y, s1, 0, 0, 0);
+          s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b0.z, s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b1.z, s1, 0, 0, 0);
+          s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b0.w, s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b1.w, s1, 0, 0, 0);
+        }
+      } else {
+      f32x4_t u0 = {0.f, 0.f, 0.f, 0.f}, u1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < HD / 8; k += 4) {
         const float4 a = qreg[t][k / 4], b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
+        const float4 c = qreg[t][(k + HD / 8) / 4], e0 = *(const float4 *)(k0 + k + HD / 8),
+                     e1 = *(const float4 *)(k1 + k + HD / 8);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b0.x, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b1.x, s1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.x, e0.x, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.x, e1.x, u1, 0, 0, 0);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b0.y, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b1.y, s1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.y, e0.y, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.y, e1.y, u1, 0, 0, 0);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b0.z, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b1.z, s1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.z, e0.z, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.z, e1.z, u1, 0, 0, 0);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b0.w, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b1.w, s1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.w, e0.w, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.w, e1.w, u1, 0, 0, 0);
+      }
+      s0 += u0;
+      s1 += u1;
       }
       // s0[r], s1[r]: query row mt*16 + 4*lg + r, keys lr and 16 + lr
 #pragma unroll
@@ -350,7 +383,9 @@ size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B) {
 int attention_init() {
   static bool done = false;
   if (!done) {
-    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     160 * 1024));
+    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      160 * 1024));
     done = true;
   }
@@ -381,12 +416,13 @@ int attention_launch(const float *qfull, int qfs, const float *kx, const float *
   hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
   const int nwg = p.nchunk < ATTN_CHUNK_WGS ? p.nchunk : ATTN_CHUNK_WGS;
   const int MT = (nq + 15) / 16;
-  if (MT > 4 * QT_WAVE) return CWEN_EINVAL;   // query tiles beyond the waves' registers
+  if (MT > 4 * QT_MAX) return CWEN_EINVAL;   // query tiles beyond the waves' registers
   const size_t lds = ((size_t)MT * 16 * PROW + KV_FLOATS) * sizeof(float);
   if (lds > 160 * 1024) return CWEN_EINVAL;
   int rc;
   if ((rc = attention_init())) return rc;
-  hipLaunchKernelGGL(attn_chunk_kernel, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);
+  if (MT <= 4) hipLaunchKernelGGL(attn_chunk_kernel<1>, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);
+  else hipLaunchKernelGGL(attn_chunk_kernel<2>, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);
   hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)B, (unsigned)NH), dim3(HD), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
