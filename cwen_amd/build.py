@@ -66,10 +66,10 @@ def build_gpu(verbose: bool = False) -> Path:
 
 def build_host(verbose: bool = False) -> Path:
     """The C host drivers (cwen_amd/host), linked against libcwen_gpu.so."""
-    src = PKG / "host" / "cwen_host.c"
+    srcs = [PKG / "host" / "cwen_host.c", PKG / "host" / "cwen_gguf.c"]
     tmp = HOST_LIB.with_suffix(".so.tmp")
     _run(["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", "-fPIC", "-shared", f"-I{ROOT / 'include'}",
-          str(src), f"-L{PKG}", "-lcwen_gpu", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])
+          *map(str, srcs), f"-L{PKG}", "-lcwen_gpu", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])
     os.replace(tmp, HOST_LIB)
     if verbose:
         print(f"built {HOST_LIB}")

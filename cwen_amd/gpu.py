@@ -65,6 +65,14 @@ HOST_SIGNATURES = [
     ("cwen_prefill", _I, [_VP, _VP, _I, C.POINTER(_I)]),
     ("cwen_generate_serial", _I, [_VP, _VP, _I, _I, _VP, _VP]),
     ("cwen_generate_spec", _I, [_VP, _VP, _I, _I, _VP, _VP, _VP]),
+    ("cwen_gguf_open", _I, [C.c_char_p, C.POINTER(_VP)]),
+    ("cwen_gguf_close", None, [_VP]),
+    ("cwen_gguf_error", C.c_char_p, []),
+    ("cwen_gguf_count", _I, [_VP]),
+    ("cwen_gguf_tensor", _I, [_VP, _I, C.POINTER(C.c_char_p), C.POINTER(_I), C.POINTER(_I), C.POINTER(_I),
+                              C.POINTER(_VP)]),
+    ("cwen_gguf_find", _I, [_VP, C.c_char_p]),
+    ("cwen_model_load_gguf", _I, [_VP, _VP, _VP]),
 ]
 
 
@@ -316,6 +324,41 @@ class SpecStats(C.Structure):
                 ("prefill_s", C.c_double), ("decode_s", C.c_double)]
 
 
+class GGUF:
+    """A GGUF file mapped by the host library (cwen_gguf_*); no GPU needed."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        rc = host_lib().cwen_gguf_open(str(path).encode(), C.byref(h))
+        if rc != CWEN_OK:
+            raise CwenError(f"cwen_gguf_open ({host_lib().cwen_gguf_error().decode()})", rc)
+        self.h = h
+
+    def __len__(self) -> int:
+        return host_lib().cwen_gguf_count(self.h)
+
+    def tensor(self, i: int) -> tuple[str, int, int, int, int]:
+        """(name, GGUF type, ne0, ne1, data address)."""
+        name, t, a, b, d = C.c_char_p(), _I(), _I(), _I(), C.c_void_p()
+        check("cwen_gguf_tensor", host_lib().cwen_gguf_tensor(self.h, i, C.byref(name), C.byref(t), C.byref(a),
+                                                              C.byref(b), C.byref(d)))
+        return name.value.decode(), t.value, a.value, b.value, d.value
+
+    def find(self, name: str) -> int:
+        return host_lib().cwen_gguf_find(self.h, name.encode())
+
+    def close(self) -> None:
+        if self.h:
+            host_lib().cwen_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Model:
     """The block-verify model on one device (cwen_model_* of the C ABI)."""
 
@@ -382,6 +425,12 @@ class Model:
         if n < 0:
             raise CwenError("cwen_generate_spec", n)
         return out[:n], st
+
+    def load_gguf(self, g: "GGUF") -> None:
+        """Upload the verify path's tensors from a GGUF file (cwen_model_load_gguf)."""
+        rc = host_lib().cwen_model_load_gguf(self.h, C.byref(self.cfg), g.h)
+        if rc != CWEN_OK:
+            raise CwenError(f"cwen_model_load_gguf ({host_lib().cwen_gguf_error().decode()})", rc)
 
     def free(self) -> None:
         if self.h:

@@ -54,6 +54,28 @@ int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_g
 int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen, const cwen_spec_cfg *cfg,
                        int *out, cwen_spec_stats *stats);
 
+/* ---- GGUF weights (cwen_gguf.c) ----
+ * load_gguf (run.c:3188-3301): map a GGUF v2/v3 file read-only and read its
+ * tensor table with the reference's bounds checks.  Malformed input returns
+ * CWEN_EINVAL; cwen_gguf_error names the reason. */
+typedef struct cwen_gguf cwen_gguf;
+int cwen_gguf_open(const char *path, cwen_gguf **out);
+void cwen_gguf_close(cwen_gguf *g);
+const char *cwen_gguf_error(void);
+/* Tensor count; tensor i's name, GGUF type id, ne0, ne1 and data pointer
+ * (inside the mapping; any out pointer may be NULL); index of a name or -1
+ * (run.c find_tensor). */
+int cwen_gguf_count(const cwen_gguf *g);
+int cwen_gguf_tensor(const cwen_gguf *g, int i, const char **name, int *type, int *ne0, int *ne1,
+                     const void **data);
+int cwen_gguf_find(const cwen_gguf *g, const char *name);
+/* rebind_layers_from_tens (run.c:3366-3406): upload every tensor the verify
+ * path uses, by the reference's names, with its shape pins, into model m
+ * created with cfg.  ffn_gate/ffn_up and attn_k/attn_v (GGUF Q4_0) are
+ * interleaved on the host into the device's pair form; output.weight falls
+ * back to token_embd.weight (tied).  The embedding must be Q4_0. */
+int cwen_model_load_gguf(cwen_model *m, const cwen_model_cfg *cfg, const cwen_gguf *g);
+
 #ifdef __cplusplus
 }
 #endif

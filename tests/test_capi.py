@@ -10,12 +10,15 @@ ROOT = Path(__file__).resolve().parent.parent
 DECL = re.compile(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(cwen_\w+)\s*\(", re.M)
 
 
-def declared():
+def declared(headers=None):
     names = set()
-    for h in (ROOT / "include").glob("*.h"):
+    for h in headers or (ROOT / "include").glob("*.h"):
         text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
         names |= set(DECL.findall(text))
     return sorted(names)
+
+
+HOST_H = [ROOT / "cwen_amd" / "host" / "cwen_host.h"]
 
 
 def test_header_declares_entry_points():
@@ -37,6 +40,19 @@ def test_python_binding_covers_header():
     from cwen_amd import gpu
     bound = {name for name, _, _ in gpu.SIGNATURES}
     assert set(declared()) <= bound, set(declared()) - bound
+
+
+def test_host_library_exports_and_bindings():
+    """libcwen_host.so (host drivers, GGUF reader) exports what cwen_host.h
+    declares, and the Python binding covers it."""
+    from cwen_amd import gpu
+    if not gpu.HOST_LIB_PATH.exists():
+        pytest.fail("libcwen_host.so is not built (python -m cwen_amd.build)")
+    L = gpu.host_lib()
+    names = declared(HOST_H)
+    assert "cwen_gguf_open" in names and "cwen_model_load_gguf" in names
+    assert not [n for n in names if not hasattr(L, n)]
+    assert set(names) <= {name for name, _, _ in gpu.HOST_SIGNATURES}
 
 
 def test_version_string():

@@ -136,6 +136,39 @@ def test_real_model_types(env, oracle):
     m.free()
 
 
+def test_gguf_load_equals_set(env, tmp_path):
+    """cwen_model_load_gguf on a GGUF file written from the synthetic model
+    (the reference's tensor names, GGUF Q4_0 matrices with gate/up and k/v as
+    separate tensors, F32 vectors, the Q6_K head) gives the model set tensor
+    by tensor: argmaxes and logits bit for bit.  A file missing a tensor the
+    reference requires is refused, naming it."""
+    gpu, ctx, m, tensors = env
+    from gguf_writer import gguf_bytes, model_gguf_tensors
+    gt = model_gguf_tensors(tensors, CFG)
+    p = tmp_path / "model.gguf"
+    p.write_bytes(gguf_bytes(gt))
+    g = gpu.GGUF(p)
+    mg = gpu.Model(ctx, **CFG)
+    mg.load_gguf(g)
+    toks = synth.prompt_tokens(2, 10, CFG["vocab"])
+    m.reset()
+    a, la = m.forward(toks), m.logits(10)
+    b, lb = mg.forward(toks), mg.logits(10)
+    assert np.array_equal(a, b)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    mg.free()
+    g.close()
+    p2 = tmp_path / "missing.gguf"
+    p2.write_bytes(gguf_bytes([t for t in gt if t[0] != "blk.1.ffn_down.weight"]))
+    g2 = gpu.GGUF(p2)
+    mg2 = gpu.Model(ctx, **CFG)
+    with pytest.raises(gpu.CwenError) as e:
+        mg2.load_gguf(g2)
+    assert "missing blk.1.ffn_down.weight" in str(e.value)
+    mg2.free()
+    g2.close()
+
+
 @pytest.mark.parametrize("B", [4, 8, 16])
 def test_block_equals_serial_bitwise(env, B):
     """Every block size takes the same path (the producer writes the f16
