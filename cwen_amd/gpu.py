@@ -72,6 +72,10 @@ HOST_SIGNATURES = [
     ("cwen_gguf_tensor", _I, [_VP, _I, C.POINTER(C.c_char_p), C.POINTER(_I), C.POINTER(_I), C.POINTER(_I),
                               C.POINTER(_VP)]),
     ("cwen_gguf_find", _I, [_VP, C.c_char_p]),
+    ("cwen_gguf_tensor_scales", _I, [_VP, _I, C.POINTER(_VP), C.POINTER(_I)]),
+    ("cwen_cwenr_path", _I, [C.c_char_p, C.c_char_p, C.c_size_t]),
+    ("cwen_gguf_apply_cwenr", _I, [_VP, C.c_char_p, C.c_char_p]),
+    ("cwen_f32_to_f16", C.c_uint16, [C.c_float]),
     ("cwen_model_load_gguf", _I, [_VP, _VP, _VP]),
 ]
 
@@ -346,6 +350,31 @@ class GGUF:
 
     def find(self, name: str) -> int:
         return host_lib().cwen_gguf_find(self.h, name.encode())
+
+    def scales(self, i: int) -> tuple[int | None, int]:
+        """(f16 scale address, pair side) of a tensor a sidecar rebound."""
+        sc, side = C.c_void_p(), _I()
+        check("cwen_gguf_tensor_scales", host_lib().cwen_gguf_tensor_scales(self.h, i, C.byref(sc), C.byref(side)))
+        return sc.value, side.value
+
+    def apply_cwenr(self, path, src_gguf=None) -> int:
+        """Rebind the Q4_0 tensors a CWENR sidecar holds; the number rebound
+        (0: no file, or no entry applies)."""
+        rc = host_lib().cwen_gguf_apply_cwenr(self.h, str(path).encode(),
+                                              None if src_gguf is None else str(src_gguf).encode())
+        if rc < 0:
+            raise CwenError(f"cwen_gguf_apply_cwenr ({host_lib().cwen_gguf_error().decode()})", rc)
+        return rc
+
+    @staticmethod
+    def cwenr_path(gguf_path) -> str:
+        buf = C.create_string_buffer(4096)
+        check("cwen_cwenr_path", host_lib().cwen_cwenr_path(str(gguf_path).encode(), buf, len(buf)))
+        return buf.value.decode()
+
+    @staticmethod
+    def last_error() -> str:
+        return host_lib().cwen_gguf_error().decode()
 
     def close(self) -> None:
         if self.h:

@@ -15,6 +15,13 @@
  * device model takes gate/up and k/v as interleaved pairs (CWENR v4 RSI), so
  * two GGUF Q4_0 tensors are interleaved on the host first, as the
  * reference's offline repack does (tools/repack_q4.py).
+ *
+ * The CWENR sidecar reader follows load_cwenr (run.c:3467-3643): a sidecar
+ * stamped with its source GGUF's size in 4 KiB pages is dropped when the
+ * GGUF no longer has that size; v3/v4 entries rebind a GGUF Q4_0 tensor of
+ * the same name and shape to a split (RS) or interleaved (RSI) view of the
+ * sidecar; v2's packed 20-byte blocks are split on the host, the f32 scale
+ * rounded to f16 to nearest even.  Entries that cannot apply are skipped.
  */
 #define _GNU_SOURCE
 #include "cwen_host.h"
@@ -36,6 +43,8 @@ typedef struct {
   int type, ne0, ne1;
   uint64_t off;
   const void *data;
+  const void *scales;  /* CWENR RS / RSI: the f16 scales */
+  int side;            /* CWENR RSI: 0 = first (A), 1 = second (B) of the pair */
 } gguf_tensor;
 
 struct cwen_gguf {
@@ -43,6 +52,9 @@ struct cwen_gguf {
   size_t len;
   int n;
   gguf_tensor *t;
+  void *rmap;   /* a v3/v4 CWENR sidecar the tensors point into */
+  size_t rlen;
+  void *split;  /* v2: qs and f16 scales split on the host */
 };
 
 static char g_err[192];
@@ -136,6 +148,8 @@ static uint64_t row_bytes(int type, int ne0) {
 void cwen_gguf_close(cwen_gguf *g) {
   if (!g) return;
   if (g->map && g->map != MAP_FAILED) munmap(g->map, g->len);
+  if (g->rmap) munmap(g->rmap, g->rlen);
+  free(g->split);
   free(g->t);
   free(g);
 }
@@ -283,12 +297,238 @@ int cwen_gguf_find(const cwen_gguf *g, const char *name) {
   return -1;
 }
 
+int cwen_gguf_tensor_scales(const cwen_gguf *g, int i, const void **scales, int *side) {
+  if (!g || i < 0 || i >= g->n) return CWEN_EINVAL;
+  if (scales) *scales = g->t[i].scales;
+  if (side) *side = g->t[i].side;
+  return CWEN_OK;
+}
+
+/* ------------------------------------------------------------ CWENR sidecar */
+
+enum { R_HEAD = 32, R_ENT = 128, R_MAX = 1024, R_IL_A = 1, R_IL_B = 2 };
+#define R_STAMP_TAG 0x4e455743u /* "CWEN" little-endian */
+
+int cwen_cwenr_path(const char *gguf, char *out, size_t cap) {
+  if (!gguf || !out || !cap) return CWEN_EINVAL;
+  const char *env = getenv("CWEN_REPACK");
+  int k;
+  if (env && env[0]) {
+    k = snprintf(out, cap, "%s", env);
+  } else {
+    const size_t n = strlen(gguf);
+    if (n > 5 && !strcmp(gguf + n - 5, ".gguf"))
+      k = snprintf(out, cap, "%.*s.cwenr", (int)(n - 5), gguf);
+    else
+      k = snprintf(out, cap, "%s.cwenr", gguf);
+  }
+  return (k < 0 || (size_t)k >= cap) ? CWEN_EINVAL : CWEN_OK;
+}
+
+/* IEEE binary32 -> binary16, round to nearest even; NaN becomes a quiet NaN
+ * with the sign kept, overflow becomes infinity, and results below the
+ * smallest subnormal's half become signed zero. */
+static uint16_t f32_to_f16_rne(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (a > 0x7f800000u ? 0x0200u : 0));
+  const int e = (int)(a >> 23) - 127;                    /* unbiased exponent */
+  if (e < -25) return (uint16_t)sign;                    /* |x| < 2^-25 */
+  const uint32_t mant = (a & 0x7fffffu) | 0x800000u;    /* 24 significant bits */
+  /* the result's unit in the last place is 2^(e-10) for normals, 2^-24 below
+   * 2^-14: drop `sh` low bits of the 24-bit significand */
+  const int sh = e < -14 ? 13 + (-14 - e) : 13;
+  uint32_t r = mant >> sh;
+  const uint32_t rem = mant & ((1u << sh) - 1u), half = 1u << (sh - 1);
+  if (rem > half || (rem == half && (r & 1u))) r++;
+  if (e < -14) return (uint16_t)(sign | r);              /* subnormal, or the smallest normal */
+  /* normal: r holds the hidden bit; a carry out of 11 bits bumps the exponent */
+  uint32_t he = (uint32_t)(e + 15);
+  if (r >> 11) {
+    r >>= 1;
+    he++;
+  }
+  if (he >= 31u) return (uint16_t)(sign | 0x7c00u);
+  return (uint16_t)(sign | (he << 10) | (r & 0x3ffu));
+}
+
+uint16_t cwen_f32_to_f16(float x) { return f32_to_f16_rne(x); }
+
+typedef struct {
+  int t;             /* tensor index */
+  int32_t ne0, ne1;
+  uint64_t a, b;     /* v3/v4: qs and scale offsets; v2: offset and byte count */
+  uint32_t flags;
+} r_entry;
+
+/* One directory entry and the GGUF Q4_0 tensor of the same name and shape
+ * it applies to, or -1 (run.c:3472-3485). */
+static int r_match(const cwen_gguf *g, const uint8_t *dir, uint32_t i, r_entry *e) {
+  const uint8_t *p = dir + R_HEAD + (size_t)i * R_ENT;
+  char name[G_NAME];
+  memcpy(name, p, G_NAME);
+  name[G_NAME - 1] = 0;
+  memcpy(&e->ne0, p + 96, 4);
+  memcpy(&e->ne1, p + 100, 4);
+  memcpy(&e->a, p + 104, 8);
+  memcpy(&e->b, p + 112, 8);
+  memcpy(&e->flags, p + 120, 4);
+  e->t = cwen_gguf_find(g, name);
+  if (e->t < 0) return -1;
+  const gguf_tensor *t = &g->t[e->t];
+  if (t->type != CWEN_T_Q4_0 || t->ne0 != e->ne0 || t->ne1 != e->ne1) return -1;
+  return e->t;
+}
+
+int cwen_gguf_apply_cwenr(cwen_gguf *g, const char *path, const char *src_gguf) {
+  if (!g || !path) return fail("null argument");
+  if (g->rmap || g->split) return fail("a sidecar is already applied");
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0) {
+    snprintf(g_err, sizeof g_err, "no sidecar");
+    return 0;  /* optional */
+  }
+  struct stat st;
+  if (fstat(fd, &st) || st.st_size < R_HEAD) {
+    close(fd);
+    return fail("cwenr: unusable (too small)");
+  }
+  const size_t len = (size_t)st.st_size;
+  void *map = mmap(NULL, len, PROT_READ, MAP_PRIVATE, fd, 0);
+  close(fd);
+  if (map == MAP_FAILED) return fail("cwenr: mmap failed");
+  const uint8_t *p = (const uint8_t *)map;
+  int rc = CWEN_OK;
+  if (memcmp(p, "CWENR001", 8)) {
+    rc = fail("cwenr: bad magic");
+    goto drop;
+  }
+  {  /* staleness gate: a stamped sidecar must match its source's size */
+    uint32_t tag, src_pages;
+    memcpy(&tag, p + 24, 4);
+    memcpy(&src_pages, p + 28, 4);
+    if (tag == R_STAMP_TAG) {
+      struct stat gs;
+      const uint64_t want = (src_gguf && stat(src_gguf, &gs) == 0) ? ((uint64_t)gs.st_size + 4095) / 4096 : 0;
+      if ((uint64_t)src_pages != want) {
+        rc = fail("cwenr: stale sidecar (its source GGUF changed since the repack)");
+        goto drop;
+      }
+    }
+  }
+  uint32_t ver, n;
+  uint64_t base;
+  memcpy(&ver, p + 8, 4);
+  memcpy(&n, p + 12, 4);
+  memcpy(&base, p + 16, 8);
+  if ((ver != 2 && ver != 3 && ver != 4) || n > R_MAX || base >= len || R_HEAD + (size_t)n * R_ENT > len) {
+    char m[64];
+    snprintf(m, sizeof m, "cwenr: bad header ver=%u n=%u", ver, n);
+    rc = fail(m);
+    goto drop;
+  }
+  const size_t rem = len - (size_t)base;
+  int bound = 0;
+  if (ver >= 3) {
+    for (uint32_t i = 0; i < n; i++) {
+      r_entry e;
+      if (r_match(g, p, i, &e) < 0) continue;
+      const int il = e.flags == R_IL_A || e.flags == R_IL_B;
+      const size_t nblk = (size_t)(e.ne0 / 32) * (size_t)e.ne1;
+      const size_t qsb = nblk * (il ? 32u : 16u), scb = nblk * (il ? 4u : 2u);
+      if (e.a > rem || e.b > rem || qsb > rem - e.a || scb > rem - e.b) continue;  /* out of the file */
+      gguf_tensor *t = &g->t[e.t];
+      t->data = p + base + e.a;
+      t->scales = p + base + e.b;
+      t->type = il ? CWEN_T_Q4_0RSI : CWEN_T_Q4_0RS;
+      t->side = e.flags == R_IL_B;
+      bound++;
+    }
+    if (!bound) goto none;
+    g->rmap = map;
+    g->rlen = len;
+  } else {
+    /* v2: packed {u8 qs[16]; f32 d} blocks, split into qs and f16 scales */
+    r_entry *es = (r_entry *)calloc(n ? n : 1, sizeof *es);
+    if (!es) {
+      rc = CWEN_ENOMEM;
+      goto drop;
+    }
+    size_t total = 0;
+    int k = 0;
+    for (uint32_t i = 0; i < n; i++) {
+      r_entry e;
+      if (r_match(g, p, i, &e) < 0) continue;
+      const size_t nblk = (size_t)(e.ne0 / 32) * (size_t)e.ne1;
+      if (e.a > rem || e.b > rem - e.a || e.b != nblk * 20u) continue;  /* out of the file, or mis-sized */
+      es[k++] = e;
+      total += nblk;
+    }
+    if (!k) {
+      free(es);
+      goto none;
+    }
+    uint8_t *arena = (uint8_t *)malloc(total * 18u);
+    if (!arena) {
+      free(es);
+      rc = CWEN_ENOMEM;
+      goto drop;
+    }
+    uint8_t *qd = arena;
+    uint16_t *sd = (uint16_t *)(arena + total * 16u);
+    for (int j = 0; j < k; j++) {
+      gguf_tensor *t = &g->t[es[j].t];
+      if (t->type != CWEN_T_Q4_0) continue;  /* a repeated name binds once */
+      const size_t nblk = (size_t)(es[j].ne0 / 32) * (size_t)es[j].ne1;
+      const uint8_t *src = p + base + es[j].a;
+      for (size_t b = 0; b < nblk; b++) {
+        float d;
+        memcpy(qd + b * 16, src + b * 20, 16);
+        memcpy(&d, src + b * 20 + 16, 4);
+        sd[b] = f32_to_f16_rne(d);
+      }
+      t->data = qd;
+      t->scales = sd;
+      t->type = CWEN_T_Q4_0RS;
+      t->side = 0;
+      qd += nblk * 16u;
+      sd += nblk;
+      bound++;
+    }
+    free(es);
+    g->split = arena;
+    munmap(map, len);
+  }
+  g_err[0] = 0;
+  return bound;
+none:
+  snprintf(g_err, sizeof g_err, "cwenr: no usable entries");
+  munmap(map, len);
+  return 0;
+drop:
+  munmap(map, len);
+  return rc;
+}
+
 /* ------------------------------------------------------------------ binder */
 
 /* Matrix types the device GEMV computes (the reference's matmul_type_ok,
  * run.c:1311-1318, minus its drafter-only T_Q8S). */
+static int q4_family(int ty) { return ty == CWEN_T_Q4_0 || ty == CWEN_T_Q4_0RS || ty == CWEN_T_Q4_0RSI; }
 static int mat_type_ok(int ty) {
-  return ty == CWEN_T_Q4_0 || ty == CWEN_T_Q4_1 || ty == CWEN_T_Q8_0 || ty == CWEN_T_Q5_K || ty == CWEN_T_Q6_K;
+  return q4_family(ty) || ty == CWEN_T_Q4_1 || ty == CWEN_T_Q8_0 || ty == CWEN_T_Q5_K || ty == CWEN_T_Q6_K;
+}
+
+/* Block i (row-major over rows, then K) of a Q4_0 tensor in any of its three
+ * layouts: the f16 scale bits and the 16 nibble bytes. */
+static const uint8_t *q4_block(const gguf_tensor *t, size_t i, uint16_t *d) {
+  const uint8_t *q = (const uint8_t *)t->data, *sc = (const uint8_t *)t->scales;
+  switch (t->type) {
+    case CWEN_T_Q4_0: memcpy(d, q + i * 18, 2); return q + i * 18 + 2;
+    case CWEN_T_Q4_0RS: memcpy(d, sc + i * 2, 2); return q + i * 16;
+    default: memcpy(d, sc + (2 * i + t->side) * 2, 2); return q + i * 32 + 16 * t->side;
+  }
 }
 
 static const gguf_tensor *need(const cwen_gguf *g, const char *name, int *rc) {
@@ -337,32 +577,38 @@ static const gguf_tensor *vec(const cwen_gguf *g, const char *name, int n, int *
 static int set_vec(cwen_model *m, int layer, int id, const gguf_tensor *t, int n) {
   return cwen_model_set(m, layer, id, CWEN_T_F32, t->data, NULL, n, 1);
 }
+/* A matrix as the device takes it: GGUF types and a sidecar's split (RS)
+ * view as they are; one side of an interleaved (RSI) view split out first. */
 static int set_mat(cwen_model *m, int layer, int id, const gguf_tensor *t) {
-  return cwen_model_set(m, layer, id, t->type, t->data, NULL, t->ne0, t->ne1);
+  if (t->type != CWEN_T_Q4_0RSI) return cwen_model_set(m, layer, id, t->type, t->data, t->scales, t->ne0, t->ne1);
+  const size_t nblk = (size_t)(t->ne0 / 32) * t->ne1;
+  uint8_t *qs = (uint8_t *)malloc(nblk * 18);
+  if (!qs) return CWEN_ENOMEM;
+  uint16_t *sc = (uint16_t *)(qs + nblk * 16);
+  for (size_t i = 0; i < nblk; i++) memcpy(qs + i * 16, q4_block(t, i, &sc[i]), 16);
+  const int rc = cwen_model_set(m, layer, id, CWEN_T_Q4_0RS, qs, sc, t->ne0, t->ne1);
+  free(qs);
+  return rc;
 }
 
-/* Two GGUF Q4_0 matrices of one shape as a CWENR interleaved pair:
- * qs[row][block][a 16 | b 16], f16 sc[row][block][a | b]. */
+/* Two Q4_0 matrices of one shape as an interleaved pair,
+ * qs[row][block][a 16 | b 16], f16 sc[row][block][a | b]: a sidecar's pair
+ * as it is, any other combination of layouts interleaved on the host. */
 static int set_pair(cwen_model *m, int layer, int id, const gguf_tensor *a, const gguf_tensor *b) {
-  if (a->type != CWEN_T_Q4_0 || b->type != CWEN_T_Q4_0) return fail("pair halves must be Q4_0");
+  if (!q4_family(a->type) || !q4_family(b->type)) return fail("pair halves must be Q4_0");
+  if (a->type == CWEN_T_Q4_0RSI && b->type == CWEN_T_Q4_0RSI && a->data == b->data && a->scales == b->scales &&
+      a->side == 0 && b->side == 1)
+    return cwen_model_set(m, layer, id, CWEN_T_Q4_0RSI, a->data, a->scales, a->ne0, a->ne1);
   const size_t nblk = (size_t)(a->ne0 / 32) * a->ne1;
-  uint8_t *qs = (uint8_t *)malloc(nblk * 32);
-  uint16_t *sc = (uint16_t *)malloc(nblk * 4);
-  if (!qs || !sc) {
-    free(qs);
-    free(sc);
-    return CWEN_ENOMEM;
-  }
-  const uint8_t *pa = (const uint8_t *)a->data, *pb = (const uint8_t *)b->data;
+  uint8_t *qs = (uint8_t *)malloc(nblk * 36);
+  if (!qs) return CWEN_ENOMEM;
+  uint16_t *sc = (uint16_t *)(qs + nblk * 32);
   for (size_t i = 0; i < nblk; i++) {
-    memcpy(&sc[2 * i], pa + i * 18, 2);
-    memcpy(&sc[2 * i + 1], pb + i * 18, 2);
-    memcpy(qs + i * 32, pa + i * 18 + 2, 16);
-    memcpy(qs + i * 32 + 16, pb + i * 18 + 2, 16);
+    memcpy(qs + i * 32, q4_block(a, i, &sc[2 * i]), 16);
+    memcpy(qs + i * 32 + 16, q4_block(b, i, &sc[2 * i + 1]), 16);
   }
   const int rc = cwen_model_set(m, layer, id, CWEN_T_Q4_0RSI, qs, sc, a->ne0, a->ne1);
   free(qs);
-  free(sc);
   return rc;
 }
 
@@ -383,7 +629,7 @@ int cwen_model_load_gguf(cwen_model *m, const cwen_model_cfg *c, const cwen_gguf
   const int Qo = c->n_head * c->head_dim, Ko = c->n_kv_head * c->head_dim;
   const gguf_tensor *t, *u;
   NEED(t, need(g, "token_embd.weight", &rc));
-  if (t->type != CWEN_T_Q4_0) return fail("token_embd.weight: the device embedding takes Q4_0");
+  if (!q4_family(t->type)) return fail("token_embd.weight: the device embedding takes Q4_0");
   if (t->ne0 != H || t->ne1 != V) return fail("token_embd.weight: shape");
   TRY(set_mat(m, -1, CWEN_TOK_EMBD, t));
   NEED(u, vec(g, "output_norm.weight", H, &rc));

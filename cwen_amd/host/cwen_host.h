@@ -69,11 +69,34 @@ int cwen_gguf_count(const cwen_gguf *g);
 int cwen_gguf_tensor(const cwen_gguf *g, int i, const char **name, int *type, int *ne0, int *ne1,
                      const void **data);
 int cwen_gguf_find(const cwen_gguf *g, const char *name);
+/* Tensor i's f16 scales and pair side once a CWENR sidecar rebound it
+ * (type CWEN_T_Q4_0RS / CWEN_T_Q4_0RSI); NULL and 0 for GGUF types. */
+int cwen_gguf_tensor_scales(const cwen_gguf *g, int i, const void **scales, int *side);
+
+/* ---- CWENR sidecar (cwen_gguf.c) ----
+ * cwenr_path_for (run.c:3310-3325): $CWEN_REPACK if set, else the GGUF
+ * path with ".gguf" replaced by (or, without it, followed by) ".cwenr".
+ * CWEN_EINVAL when the result does not fit in cap bytes. */
+int cwen_cwenr_path(const char *gguf, char *out, size_t cap);
+/* load_cwenr (run.c:3486-3643): map the sidecar at path and rebind the Q4_0
+ * tensors of g it holds (same name and shape) to its split (v3, v4 solo) or
+ * interleaved (v4 pairs) views; v2's packed blocks are split on the host.
+ * Returns the number of tensors rebound (>= 1); 0 when there is no file or
+ * no entry applies; CWEN_EINVAL for a bad magic or header, or a stamped
+ * sidecar whose source size (src_gguf's, in 4 KiB pages) no longer matches.
+ * Below 1, g is unchanged and the reason is in cwen_gguf_error.  The views
+ * live until cwen_gguf_close. */
+int cwen_gguf_apply_cwenr(cwen_gguf *g, const char *path, const char *src_gguf);
+/* IEEE f32 -> f16 bits, rounded to nearest even (the v2 scale split,
+ * run.c:443-470). */
+uint16_t cwen_f32_to_f16(float x);
 /* rebind_layers_from_tens (run.c:3366-3406): upload every tensor the verify
  * path uses, by the reference's names, with its shape pins, into model m
  * created with cfg.  ffn_gate/ffn_up and attn_k/attn_v (GGUF Q4_0) are
  * interleaved on the host into the device's pair form; output.weight falls
- * back to token_embd.weight (tied).  The embedding must be Q4_0. */
+ * back to token_embd.weight (tied).  The embedding must be Q4_0.  Tensors a
+ * sidecar rebound are uploaded from its views (an interleaved pair as it
+ * is). */
 int cwen_model_load_gguf(cwen_model *m, const cwen_model_cfg *cfg, const cwen_gguf *g);
 
 #ifdef __cplusplus

@@ -1,4 +1,5 @@
-"""Minimal GGUF v2/v3 writer for tests (test infrastructure only), and the
+"""Minimal GGUF v2/v3 and CWENR sidecar writers for tests (test
+infrastructure only; the sidecar layout of tools/repack_q4.py:1-27, 197-262), and the
 conversion of the synthetic model's CWENR tensors to the GGUF tensors the
 reference binds (run.c:3366-3406 names; GGUF Q4_0 blocks for the matrices
 the reference's offline repack turns into CWENR RS/RSI)."""
@@ -67,3 +68,68 @@ def model_gguf_tensors(tensors, cfg: dict):
         else:
             out.append((nm, wtype, (ne0, ne1), np.ascontiguousarray(data).tobytes()))
     return out
+
+
+CWENR_TAG = 0x4E455743  # "CWEN"
+PAIRS = ((".ffn_gate.weight", ".ffn_up.weight"), (".attn_k.weight", ".attn_v.weight"))
+
+
+def cwenr_entry(name: str, ne0: int, ne1: int, a: int, b: int, flags: int = 0) -> bytes:
+    """One 128-byte directory entry: name[96], ne0, ne1, two u64 offsets, flags, pad."""
+    nb = name.encode()
+    assert len(nb) < 96
+    return nb.ljust(96, b"\0") + struct.pack("<iiQQII", ne0, ne1, a, b, flags, 0)
+
+
+def cwenr_bytes(entries, payload: bytes, version: int = 4, src_pages: int | None = None,
+                data_base: int | None = None) -> bytes:
+    """Header (magic, version, count, data_base, stamp), the entries, the
+    payload at data_base (by default the next 64-byte boundary)."""
+    n = len(entries)
+    base = (32 + 128 * n + 63) // 64 * 64 if data_base is None else data_base
+    stamp = struct.pack("<II", CWENR_TAG, src_pages) if src_pages is not None else b"\0" * 8
+    head = b"CWENR001" + struct.pack("<IIQ", version, n, base) + stamp + b"".join(entries)
+    return head.ljust(base, b"\0") + payload
+
+
+def cwenr_from_gguf(gt, version: int = 4, src_pages: int | None = None) -> bytes:
+    """The sidecar of the GGUF Q4_0 tensors in gt ((name, type, dims, raw)):
+    v4 interleaves the gate/up and k/v pairs and splits the rest, v3 splits
+    every tensor into qs + f16 scales, v2 packs {qs[16], f32 d} blocks."""
+    q4 = {name: (dims, raw) for name, typ, dims, raw in gt if typ == 2}
+    entries, payload = [], bytearray()
+
+    def put(blob: bytes) -> int:
+        payload.extend(b"\0" * (-len(payload) % 64))
+        off = len(payload)
+        payload.extend(blob)
+        return off
+
+    def blocks(raw):
+        return np.frombuffer(raw, np.uint8).reshape(-1, 18)
+
+    used = set()
+    for name in sorted(q4):
+        if name in used:
+            continue
+        dims, raw = q4[name]
+        ne0, ne1 = dims[0], dims[1] if len(dims) > 1 else 1
+        partner = next((name[:-len(a)] + b for a, b in PAIRS if name.endswith(a)), None) if version == 4 else None
+        if partner in q4:
+            ba, bb = blocks(raw), blocks(q4[partner][1])
+            qs = np.concatenate([ba[:, 2:], bb[:, 2:]], axis=1).tobytes()
+            sc = np.concatenate([ba[:, :2], bb[:, :2]], axis=1).tobytes()
+            a, b = put(qs), put(sc)
+            entries += [cwenr_entry(name, ne0, ne1, a, b, 1), cwenr_entry(partner, ne0, ne1, a, b, 2)]
+            used |= {name, partner}
+            continue
+        bl = blocks(raw)
+        if version == 2:
+            d = bl[:, :2].copy().view(np.float16).astype(np.float32)
+            packed = np.concatenate([bl[:, 2:], d.view(np.uint8).reshape(-1, 4)], axis=1).tobytes()
+            entries.append(cwenr_entry(name, ne0, ne1, put(packed), len(packed)))
+        else:
+            a, b = put(bl[:, 2:].tobytes()), put(bl[:, :2].tobytes())
+            entries.append(cwenr_entry(name, ne0, ne1, a, b))
+        used.add(name)
+    return cwenr_bytes(entries, bytes(payload), version, src_pages)

@@ -169,6 +169,35 @@ def test_gguf_load_equals_set(env, tmp_path):
     g2.close()
 
 
+@pytest.mark.parametrize("version", [4, 3, 2])
+def test_cwenr_load_equals_set(env, tmp_path, version):
+    """A GGUF file with a CWENR sidecar of its Q4_0 tensors (v4: gate/up and
+    k/v interleaved pairs uploaded as they are; v3: split halves interleaved
+    on the host; v2: packed blocks split on the host) loads into the model
+    set tensor by tensor: argmaxes and logits bit for bit."""
+    gpu, ctx, m, tensors = env
+    from gguf_writer import cwenr_from_gguf, gguf_bytes, model_gguf_tensors
+    gt = model_gguf_tensors(tensors, CFG)
+    p = tmp_path / "model.gguf"
+    p.write_bytes(gguf_bytes(gt))
+    s = tmp_path / "model.cwenr"
+    s.write_bytes(cwenr_from_gguf(gt, version, src_pages=(p.stat().st_size + 4095) // 4096))
+    g = gpu.GGUF(p)
+    n_q4 = sum(1 for t in gt if t[1] == gpu.T_Q4_0)
+    assert g.apply_cwenr(gpu.GGUF.cwenr_path(p), p) == n_q4
+    assert g.tensor(g.find("token_embd.weight"))[1] == gpu.T_Q4_0RS
+    mg = gpu.Model(ctx, **CFG)
+    mg.load_gguf(g)
+    toks = synth.prompt_tokens(3, 10, CFG["vocab"])
+    m.reset()
+    a, la = m.forward(toks), m.logits(10)
+    b, lb = mg.forward(toks), mg.logits(10)
+    assert np.array_equal(a, b)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    mg.free()
+    g.close()
+
+
 @pytest.mark.parametrize("B", [4, 8, 16])
 def test_block_equals_serial_bitwise(env, B):
     """Every block size takes the same path (the producer writes the f16
