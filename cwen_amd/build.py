@@ -66,7 +66,7 @@ def build_gpu(verbose: bool = False) -> Path:
 
 def build_host(verbose: bool = False) -> Path:
     """The C host drivers (cwen_amd/host), linked against libcwen_gpu.so."""
-    srcs = [PKG / "host" / "cwen_host.c", PKG / "host" / "cwen_gguf.c"]
+    srcs = [PKG / "host" / "cwen_host.c", PKG / "host" / "cwen_gguf.c", PKG / "host" / "cwen_serve.c"]
     tmp = HOST_LIB.with_suffix(".so.tmp")
     _run(["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", "-fPIC", "-shared", f"-I{ROOT / 'include'}",
           *map(str, srcs), f"-L{PKG}", "-lcwen_gpu", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])

@@ -16,7 +16,7 @@ HOST_LIB_PATH = Path(__file__).resolve().parent / "libcwen_host.so"
 
 CWEN_OK = 0
 CWEN_ERANGE = -6
-ERRORS = {-1: "EINVAL", -2: "EHIP", -3: "ENOMEM", -4: "ETYPE", -5: "ESCRATCH", -6: "ERANGE"}
+ERRORS = {-1: "EINVAL", -2: "EHIP", -3: "ENOMEM", -4: "ETYPE", -5: "ESCRATCH", -6: "ERANGE", -7: "EIO"}
 
 T_F32, T_Q4_0, T_Q4_1, T_Q8_0, T_Q5_K, T_Q6_K, T_Q4_0RS, T_Q4_0RSI = 0, 2, 3, 8, 13, 14, 101, 102
 BMAX = 16
@@ -77,6 +77,8 @@ HOST_SIGNATURES = [
     ("cwen_gguf_apply_cwenr", _I, [_VP, C.c_char_p, C.c_char_p]),
     ("cwen_f32_to_f16", C.c_uint16, [C.c_float]),
     ("cwen_model_load_gguf", _I, [_VP, _VP, _VP]),
+    ("cwen_read_frame", _I, [_I, _VP, _I, _I, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
+    ("cwen_serve", _I, [_VP, _VP, _I, _I, _VP, C.POINTER(_I)]),
 ]
 
 
@@ -328,6 +330,18 @@ class SpecStats(C.Structure):
                 ("prefill_s", C.c_double), ("decode_s", C.c_double)]
 
 
+def read_frame(fd: int, max_ctx: int, vocab: int) -> tuple[int, np.ndarray | None, int]:
+    """One request frame from fd (cwen_read_frame): (1, prompt, n_gen) for a
+    valid frame, (0, None, 0) for a rejected one, (2, None, 0) at the end of
+    the stream."""
+    toks = np.zeros(max_ctx, np.int32)
+    n_p, n_g = C.c_uint32(), C.c_uint32()
+    r = host_lib().cwen_read_frame(fd, toks.ctypes.data, max_ctx, vocab, C.byref(n_p), C.byref(n_g))
+    if r < 0:
+        raise CwenError("cwen_read_frame", r)
+    return (1, toks[:n_p.value].copy(), n_g.value) if r == 1 else (r, None, 0)
+
+
 class GGUF:
     """A GGUF file mapped by the host library (cwen_gguf_*); no GPU needed."""
 
@@ -454,6 +468,14 @@ class Model:
         if n < 0:
             raise CwenError("cwen_generate_spec", n)
         return out[:n], st
+
+    def serve(self, fd_in: int, fd_out: int, spec: SpecCfg | None = None) -> int:
+        """Answer request frames from fd_in on fd_out until the stream ends
+        (cwen_serve); the number of valid frames answered."""
+        n = _I()
+        check("cwen_serve", host_lib().cwen_serve(self.h, C.byref(self.cfg), fd_in, fd_out,
+                                                  None if spec is None else C.byref(spec), C.byref(n)))
+        return n.value
 
     def load_gguf(self, g: "GGUF") -> None:
         """Upload the verify path's tensors from a GGUF file (cwen_model_load_gguf)."""

@@ -99,6 +99,30 @@ uint16_t cwen_f32_to_f16(float x);
  * is). */
 int cwen_model_load_gguf(cwen_model *m, const cwen_model_cfg *cfg, const cwen_gguf *g);
 
+/* ---- binary-frame server (cwen_serve.c) ---- */
+#define CWEN_EIO (-7) /* a reply could not be written */
+#define CWEN_FRAME_REJECTED 0
+#define CWEN_FRAME_OK 1
+#define CWEN_FRAME_END 2
+/* server_read_frame (run.c:4212-4232): read one request
+ * <u32 n_prompt><u32 n_gen><n_prompt x i32> from fd, unbuffered.  Returns
+ * CWEN_FRAME_OK for a valid frame (counts stored, tokens filled),
+ * CWEN_FRAME_REJECTED for a rejected one (a count outside [1, max_ctx]: its
+ * payload drained; a token outside [0, vocab)), CWEN_FRAME_END at the end of
+ * the stream (0xffffffff in a header word, or a frame cut short; the
+ * reference's -1), CWEN_EINVAL for bad arguments.  tokens holds max_ctx ids. */
+int cwen_read_frame(int fd, int *tokens, int max_ctx, int vocab, uint32_t *n_prompt, uint32_t *n_gen);
+/* server_loop (run.c:5063-5078): answer every frame read from fd_in on
+ * fd_out -- a rejected frame with the u32 0, a valid one with
+ * <u32 n_out><n_out x i32> from a fresh decode of its prompt: greedy serial
+ * decode when spec is NULL, else block-verify speculation with spec's knobs
+ * (the same tokens).  cfg is the model's.  Returns CWEN_OK at the end of the
+ * stream, CWEN_EIO when a reply cannot be written, or a decode's negative
+ * status; *n_served (may be NULL) counts the valid frames answered.  The
+ * descriptors stay open. */
+int cwen_serve(cwen_model *m, const cwen_model_cfg *cfg, int fd_in, int fd_out, const cwen_spec_cfg *spec,
+               int *n_served);
+
 #ifdef __cplusplus
 }
 #endif

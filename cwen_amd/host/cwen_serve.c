@@ -1,0 +1,114 @@
+/* cwen_serve.c -- the reference's binary-frame server over the cwen_gpu C ABI.
+ *
+ * Requests are <u32 n_prompt><u32 n_gen><n_prompt x i32>, little-endian;
+ * 0xffffffff in a header word, or a stream that ends inside a frame, closes
+ * the server (run.c:4177-4232).  A frame with a count outside [1, max_ctx]
+ * is rejected after its declared payload is drained, so the next header
+ * stays aligned; a frame with a token id outside [0, vocab) is rejected
+ * after its payload is read.  A rejected frame is answered with the u32 0,
+ * a valid one with <u32 n_out><n_out x i32> from a fresh decode of its
+ * prompt (server_loop, run.c:5063-5078).
+ */
+#define _GNU_SOURCE
+#include "cwen_host.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <unistd.h>
+
+static uint32_t rd_u32(FILE *f) {
+  uint32_t v = 0;
+  return fread(&v, 4, 1, f) == 1 ? v : 0xffffffffu;
+}
+
+/* Read and drop n words; a short read leaves the stream at its end, which
+ * the next header read reports. */
+static void drain(FILE *f, uint64_t n) {
+  uint32_t buf[1024];
+  while (n) {
+    const size_t take = n > 1024 ? 1024 : (size_t)n;
+    if (fread(buf, 4, take, f) != take) return;
+    n -= take;
+  }
+}
+
+static int read_frame(FILE *in, int *tokens, int max_ctx, int vocab, uint32_t *np, uint32_t *ng) {
+  const uint32_t n_prompt = rd_u32(in), n_gen = rd_u32(in);
+  if (n_prompt == 0xffffffffu || n_gen == 0xffffffffu) return CWEN_FRAME_END;
+  if (!n_prompt || n_prompt > (uint32_t)max_ctx || !n_gen || n_gen > (uint32_t)max_ctx) {
+    fprintf(stderr, "cwen server: bad frame %u %u\n", n_prompt, n_gen);
+    drain(in, n_prompt);
+    return CWEN_FRAME_REJECTED;
+  }
+  if (fread(tokens, 4, n_prompt, in) != n_prompt) return CWEN_FRAME_END;
+  for (uint32_t i = 0; i < n_prompt; i++)
+    if (tokens[i] < 0 || tokens[i] >= vocab) {
+      fprintf(stderr, "cwen server: token %d out of range [0,%d)\n", tokens[i], vocab);
+      return CWEN_FRAME_REJECTED;
+    }
+  *np = n_prompt;
+  *ng = n_gen;
+  return CWEN_FRAME_OK;
+}
+
+/* Buffered stdio over a duplicate of fd, so the caller's descriptor stays
+ * open after fclose. */
+static FILE *open_dup(int fd, const char *mode) {
+  const int d = dup(fd);
+  if (d < 0) return NULL;
+  FILE *f = fdopen(d, mode);
+  if (!f) close(d);
+  return f;
+}
+
+int cwen_read_frame(int fd, int *tokens, int max_ctx, int vocab, uint32_t *n_prompt, uint32_t *n_gen) {
+  if (!tokens || !n_prompt || !n_gen || max_ctx < 1 || vocab < 1) return CWEN_EINVAL;
+  /* unbuffered, so nothing past this frame is taken from fd */
+  FILE *in = open_dup(fd, "rb");
+  if (!in) return CWEN_EINVAL;
+  setvbuf(in, NULL, _IONBF, 0);
+  const int r = read_frame(in, tokens, max_ctx, vocab, n_prompt, n_gen);
+  fclose(in);
+  return r;
+}
+
+static int put_reply(FILE *out, const int *tok, uint32_t n) {
+  if (fwrite(&n, 4, 1, out) != 1 || (n && fwrite(tok, 4, n, out) != n) || fflush(out)) {
+    fprintf(stderr, "cwen server: reply write failed\n");
+    return CWEN_EIO;
+  }
+  return CWEN_OK;
+}
+
+int cwen_serve(cwen_model *m, const cwen_model_cfg *cfg, int fd_in, int fd_out, const cwen_spec_cfg *spec,
+               int *n_served) {
+  if (!m || !cfg || cfg->max_ctx < 1) return CWEN_EINVAL;
+  int *tokens = (int *)malloc((size_t)cfg->max_ctx * sizeof(int));
+  int *out = (int *)malloc((size_t)cfg->max_ctx * sizeof(int));
+  FILE *in = open_dup(fd_in, "rb"), *wr = open_dup(fd_out, "wb");
+  int rc = (!tokens || !out) ? CWEN_ENOMEM : (!in || !wr) ? CWEN_EINVAL : CWEN_OK;
+  int served = 0;
+  while (!rc) {
+    uint32_t np = 0, ng = 0;
+    const int r = read_frame(in, tokens, cfg->max_ctx, cfg->vocab, &np, &ng);
+    if (r == CWEN_FRAME_END) break;  /* a clean close */
+    if (r == CWEN_FRAME_REJECTED) {
+      rc = put_reply(wr, NULL, 0);
+      continue;
+    }
+    const int n = spec ? cwen_generate_spec(m, tokens, (int)np, (int)ng, spec, out, NULL)
+                       : cwen_generate_serial(m, tokens, (int)np, (int)ng, out, NULL);
+    if (n < 0) {
+      rc = n;
+      break;
+    }
+    rc = put_reply(wr, out, (uint32_t)n);
+    served++;
+  }
+  if (in) fclose(in);
+  if (wr) fclose(wr);
+  free(tokens);
+  free(out);
+  if (n_served) *n_served = served;
+  return rc;
+}

@@ -198,6 +198,47 @@ def test_cwenr_load_equals_set(env, tmp_path, version):
     g.close()
 
 
+def test_serve_answers_frames_like_generate(env):
+    """The frame server (cwen_serve, run.c:5063-5078) over pipes: each valid
+    frame is answered with the tokens cwen_generate_serial gives for it, from
+    a fresh decode, in serial and in speculative mode alike; a frame with an
+    out-of-range token is answered with 0 and the stream continues."""
+    import os
+    import struct
+    gpu, ctx, m, _ = env
+    prompts = [synth.prompt_tokens(5, 48, CFG["vocab"], period=13, noise=0.05),
+               synth.prompt_tokens(6, 7, CFG["vocab"]), synth.prompt_tokens(7, 33, CFG["vocab"], period=5)]
+    n_gen = [30, 12, 25]
+    want = []
+    for p, g in zip(prompts, n_gen):
+        want.append(m.generate_serial(p, g).tolist())
+    req = b""
+    for i, (p, g) in enumerate(zip(prompts, n_gen)):
+        req += struct.pack("<II", len(p), g) + np.asarray(p, "<i4").tobytes()
+        if i == 0:
+            req += struct.pack("<IIi", 1, 4, CFG["vocab"])           # rejected: token out of range
+    for spec in (None, gpu.SpecCfg(2, 8, 2, 8, 0)):
+        ri, wi = os.pipe()
+        ro, wo = os.pipe()
+        os.write(wi, req)
+        os.close(wi)
+        try:
+            assert m.serve(ri, wo, spec) == 3
+            os.close(wo)
+            raw = b""
+            while chunk := os.read(ro, 65536):
+                raw += chunk
+        finally:
+            os.close(ri)
+            os.close(ro)
+        got, at = [], 0
+        while at < len(raw):
+            (n,) = struct.unpack_from("<I", raw, at)
+            got.append(list(struct.unpack_from(f"<{n}i", raw, at + 4)))
+            at += 4 + 4 * n
+        assert got == [want[0], [], want[1], want[2]], spec
+
+
 @pytest.mark.parametrize("B", [4, 8, 16])
 def test_block_equals_serial_bitwise(env, B):
     """Every block size takes the same path (the producer writes the f16
