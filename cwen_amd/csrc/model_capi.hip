@@ -73,6 +73,23 @@ struct cwen_model {
   _Float16 *hh = nullptr;        // FFN hidden f16 [BMAX][I]
   float *logits = nullptr;       // [BMAX][V]
   int *hres = nullptr;           // pinned host copy of res
+  // MTP nextn drafter (blk.N after the N decoder layers; its decoder block
+  // is L[n_layers]).  Its KV stream starts at slot 1: slot s lives at index
+  // s - 1, *mctl is the last index filled.  Every block commits its
+  // positions into the stream after the target's head, pairing position
+  // p's token with the target's final residual at p - 1 (hprev holds the
+  // previous block's last committed row).
+  cwen_weight *mtp_eh = nullptr;                       // nextn.eh_proj [H][2H]
+  float *mtp_enorm = nullptr, *mtp_hnorm = nullptr, *mtp_shn = nullptr;
+  int mtp_hpos = -1;                                   // hprev holds position mtp_hpos (host copy)
+  int *mctl = nullptr;                                 // [0] last filled index of the MTP stream
+  int *mres = nullptr;                                 // per draft step t: [4t] k, [4t+1] token, [4t+2] argmax
+  int *hmres = nullptr;                                // pinned host copy of mres
+  float *hprev = nullptr;                              // [H] target residual of position mtp_hpos
+  float *hin = nullptr, *e2 = nullptr, *X2 = nullptr;  // [BMAX][H]
+  _Float16 *cat = nullptr, *xh2 = nullptr;             // [BMAX][2H], [BMAX][H]
+  float *ssq2 = nullptr;                               // [CWEN_MAX_PARTS][BMAX]
+  float *mlogits = nullptr;                            // [BMAX][V] logits of the draft steps
 };
 
 namespace {
@@ -155,6 +172,150 @@ enum { MODE_FWD = 0, MODE_FWD_HEAD = 1, MODE_VERIFY = 2 };
 // One block over the tokens in m->toks: positions ctl[0]+1 .. ctl[0]+B, then
 // the device commit.  MODE_FWD_HEAD adds the head and per-position argmax,
 // MODE_VERIFY the head and the walk over drafts toks[1..B-1] (kept = k + 1).
+// The nextn input of one row (mtp_step, run.c:3099-3102): the embedding e
+// and the predecessor hidden h = rmsnorm(hsrc, wpre) (the target's
+// output_norm, or the MTP block's own shared_head_norm while drafting), each
+// RMS-normalised with its own weight, as the f16 operand [e' | h'] of
+// eh_proj.  One workgroup per row.
+__global__ __launch_bounds__(256) void mtp_cat_kernel(const float *e, const float *hsrc, int hs, const float *wpre,
+                                                      const float *enorm, const float *hnorm, int H, float eps,
+                                                      _Float16 *cat, int *rflag) {
+  __shared__ float red[3][8];
+  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float *er = e + (size_t)r * H, *hr = hsrc + (size_t)r * hs;
+  float se = 0.f, sh = 0.f;
+  for (int i = tid; i < H; i += 256) {
+    se += er[i] * er[i];
+    sh += hr[i] * hr[i];
+  }
+  for (int o = 32; o; o >>= 1) {
+    se += __shfl_xor(se, o);
+    sh += __shfl_xor(sh, o);
+  }
+  if (lane == 0) { red[0][wv] = se; red[1][wv] = sh; }
+  __syncthreads();
+  se = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+  sh = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  const float re = 1.f / sqrtf(se / H + eps), rh = 1.f / sqrtf(sh / H + eps);
+  float s1 = 0.f;
+  for (int i = tid; i < H; i += 256) {
+    const float h1 = hr[i] * rh * wpre[i];
+    s1 += h1 * h1;
+  }
+  for (int o = 32; o; o >>= 1) s1 += __shfl_xor(s1, o);
+  if (lane == 0) red[2][wv] = s1;
+  __syncthreads();
+  s1 = red[2][0] + red[2][1] + red[2][2] + red[2][3];
+  const float r1 = 1.f / sqrtf(s1 / H + eps);
+  _Float16 *out = cat + (size_t)r * 2 * H;
+  bool bad = false;
+  for (int i = tid; i < H; i += 256) {
+    const _Float16 a = (_Float16)(er[i] * re * enorm[i]);
+    const _Float16 b = (_Float16)(hr[i] * rh * wpre[i] * r1 * hnorm[i]);
+    out[i] = a;
+    out[H + i] = b;
+    bad |= f16_bad(a) | f16_bad(b);
+  }
+  if (bad) raise_flag(rflag);
+}
+
+// *p = v, or *p += v (add): the MTP stream's fill mark, set on the device so
+// that it stays ordered with the launches around it.
+__global__ void mtp_ctl_kernel(int *p, int v, int add) { p[0] = add ? p[0] + v : v; }
+
+// hprev = row `walk ? walk[0] : n - 1` of X (the last committed position).
+__global__ void mtp_park_kernel(const float *X, int H, const int *walk, int n, float *hprev) {
+  const int row = walk ? walk[0] : n - 1;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x)
+    hprev[i] = X[(size_t)row * H + i];
+}
+
+int mtp_ready(const cwen_model *m) {
+  const Layer &y = m->L[m->cfg.n_layers];
+  return m->mtp_eh && m->mtp_enorm && m->mtp_hnorm && m->mtp_shn && m->mctl && y.attn_norm && y.post_norm &&
+         y.ffn_gu && y.ffn_down && y.parts == 3u && y.wo && y.q_norm && y.k_norm;
+}
+
+// One pass of B rows through the nextn block (mtp_step, run.c:3099-3133):
+// tokens toks[0..B-1], predecessor hiddens rows of hsrc (stride hs) under
+// norm weight wpre; the block's attention appends at *mctl + 1 ...  With
+// head_t >= 0 (B = 1) the shared head scores the result into mlogits row
+// head_t and its argmax lands in mres[4 * head_t + 1].
+int mtp_pass(cwen_model *m, int B, const int *toks, const float *hsrc, int hs, const float *wpre, int head_t,
+             hipStream_t st) {
+  const cwen_model_cfg &c = m->cfg;
+  cwen_ctx *ctx = m->ctx;
+  const int H = c.d_model;
+  Layer &y = m->L[c.n_layers];
+  int *const rflag = m->ctl + 5;
+  int rc;
+  if ((rc = embed_launch(m->emb_qs, m->emb_sc, m->emb_type, toks, B, H, m->e2, H, m->ssq2, st))) return rc;
+  hipLaunchKernelGGL(mtp_cat_kernel, dim3(B), dim3(256), 0, st, m->e2, hsrc, hs, wpre, m->mtp_enorm, m->mtp_hnorm,
+                     H, c.rms_eps, m->cat, rflag);
+  CWEN_HIP_TRY(hipGetLastError());
+  GemvOut o0 = {m->X2, nullptr, m->xh2, H, 0};
+  o0.ssq = m->ssq2;
+  o0.nwh = y.attn_norm;
+  o0.rflag = rflag;
+  if ((rc = gemv_launch(ctx, m->mtp_eh, 1, 0, GEMV_EPI_STORE, m->cat, o0, B, st))) return rc;
+  const Rows r = rows_of(c);
+  const GemvPost n1 = {m->ssq2, gemv_row_tiles(m->mtp_eh), c.rms_eps};
+  GemvOut o1 = {m->att, nullptr, nullptr, r.att, 0};
+  if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, m->xh2, o1, B, st, nullptr, &n1))) return rc;
+  if ((rc = attention_launch(m->att, r.att, m->att + r.Qo2, m->att + r.Qo2 + r.Ko, r.att, y.q_norm, y.k_norm,
+                             m->qbuf, y.K, y.V, m->mctl, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
+                             c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st, rflag)))
+    return rc;
+  GemvOut o5 = {m->X2, nullptr, m->xh2, H, 1};
+  o5.ssq = m->ssq2;
+  o5.nwh = y.post_norm;
+  o5.rflag = rflag;
+  if ((rc = gemv_launch(ctx, y.wo, 1, 0, GEMV_EPI_STORE, m->yh, o5, B, st))) return rc;
+  const GemvPost n2 = {m->ssq2, gemv_row_tiles(y.wo), c.rms_eps};
+  GemvOut f1 = {nullptr, nullptr, m->hh, 0, 0};
+  f1.rflag = rflag;
+  GemvOut f2 = {m->X2, nullptr, m->xh2, H, 1};
+  f2.ssq = m->ssq2;
+  f2.rflag = rflag;
+  f2.nwh = m->mtp_shn;
+  if ((rc = gemv_launch(ctx, y.ffn_gu, 2, 0, GEMV_EPI_SWIGLU, m->xh2, f1, B, st, nullptr, &n2)) ||
+      (rc = gemv_launch(ctx, y.ffn_down, 1, 0, GEMV_EPI_STORE, m->hh, f2, B, st)))
+    return rc;
+  if (head_t < 0) return CWEN_OK;
+  const GemvPost nh = {m->ssq2, gemv_row_tiles(y.ffn_down), c.rms_eps};
+  GemvOut o = {m->mlogits + (size_t)head_t * c.vocab, nullptr, nullptr, c.vocab, 0,
+               {ctx->amax_keys, ctx->amax_cnt, m->toks, 0, m->mres + 4 * head_t}};
+  return gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, m->xh2, o, 1, st, nullptr, &nh);
+}
+
+// mtp_commit (run.c:3150-3163) for the B positions of a block starting at
+// position P = m->pos + 1: position 0 is only parked (it has no
+// predecessor), every other position p is stepped with its token and the
+// target residual of p - 1.  Rows past the verify walk write MTP slots past
+// the commit, which later blocks and drafts rewrite before any read; the
+// parked hidden is the walk's last kept row.
+int mtp_commit_pass(cwen_model *m, int B, int mode, hipStream_t st) {
+  const int H = m->cfg.d_model, P = m->pos;
+  const int s0 = P < 0 ? 1 : 0, Bm = B - s0;
+  if (Bm > 0) {
+    float *dst = m->hin;
+    if (!s0) {
+      CWEN_HIP_TRY(hipMemcpyAsync(dst, m->hprev, (size_t)H * sizeof(float), hipMemcpyDeviceToDevice, st));
+      dst += H;
+    }
+    if (B > 1)
+      CWEN_HIP_TRY(hipMemcpyAsync(dst, m->X, (size_t)(B - 1) * H * sizeof(float), hipMemcpyDeviceToDevice, st));
+    hipLaunchKernelGGL(mtp_ctl_kernel, dim3(1), dim3(1), 0, st, m->mctl, P + s0 - 1, 0);
+    CWEN_HIP_TRY(hipGetLastError());
+    int rc = mtp_pass(m, Bm, m->toks + s0, m->hin, H, m->out_norm, -1, st);
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(mtp_park_kernel, dim3((H + 255) / 256), dim3(256), 0, st, m->X, H,
+                     mode == MODE_VERIFY ? m->res + 1 : nullptr, B, m->hprev);
+  CWEN_HIP_TRY(hipGetLastError());
+  return CWEN_OK;
+}
+
 int block(cwen_model *m, int B, int mode, hipStream_t st) {
   const cwen_model_cfg &c = m->cfg;
   cwen_ctx *ctx = m->ctx;
@@ -226,6 +387,7 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
                  {ctx->amax_keys, ctx->amax_cnt, m->toks + 1, E, m->res + 1}};
     if ((rc = gemv_launch(ctx, m->head, 1, 0, GEMV_EPI_ARGMAX, m->xh, o, B, st, nullptr, &nh))) return rc;
   }
+  if (mtp_ready(m) && (rc = mtp_commit_pass(m, B, mode, st))) return rc;
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, m->ctl, mode == MODE_VERIFY ? m->res + 1 : nullptr, B,
                      B, CWEN_BMAX + 1, m->res);
   CWEN_HIP_TRY(hipGetLastError());
@@ -250,7 +412,8 @@ int run_block(cwen_model *m, const int *toks, int B, int mode, hipStream_t st) {
   memcpy(m->htok, toks, (size_t)B * sizeof(int));
   CWEN_HIP_TRY(hipMemcpyAsync(m->toks, m->htok, (size_t)B * sizeof(int), hipMemcpyHostToDevice, st));
   CWEN_HIP_TRY(hipEventRecord(m->tok_ev, st));
-  if (!m->use_graphs) return block(m, B, mode, st);
+  // the MTP commit's launch shape depends on the position: eager
+  if (!m->use_graphs || mtp_ready(m)) return block(m, B, mode, st);
   hipGraphExec_t &ge = m->gexec[mode][B - 1];
   if (!ge) {
     hipGraph_t g = nullptr;
@@ -277,6 +440,29 @@ void commit(cwen_model *m, int n, int B) {
   for (int l = 0; l < m->cfg.n_layers; ++l)
     if (m->L[l].linear) gdn_commit_host(m->L[l].gdn, n, B);
   m->pos += n;
+  if (mtp_ready(m)) m->mtp_hpos = m->pos;
+}
+
+// The MTP block's buffers, on the first MTP tensor set.
+int mtp_alloc(cwen_model *m) {
+  if (m->mctl) return CWEN_OK;
+  const cwen_model_cfg &c = m->cfg;
+  const int H = c.d_model, BM = CWEN_BMAX;
+  const Rows R = rows_of(c);
+  Layer &y = m->L[c.n_layers];
+  y.linear = 0;
+  const size_t kv = (size_t)c.max_ctx * R.Ko;
+  int rc = (dmalloc(&y.K, kv) || dmalloc(&y.V, kv) || dmalloc(&m->mres, 4 * BM) || dmalloc(&m->hprev, H) ||
+            dmalloc(&m->hin, (size_t)BM * H) || dmalloc(&m->e2, (size_t)BM * H) || dmalloc(&m->X2, (size_t)BM * H) ||
+            dmalloc(&m->cat, (size_t)BM * 2 * H) || dmalloc(&m->xh2, (size_t)BM * H) ||
+            dmalloc(&m->ssq2, (size_t)CWEN_MAX_PARTS * BM) || dmalloc(&m->mlogits, (size_t)BM * c.vocab))
+               ? CWEN_ENOMEM
+               : CWEN_OK;
+  if (!rc) rc = gemv_alloc_q4(m->ctx, H, R.att, &y.att_in);
+  if (!rc && hipHostMalloc((void **)&m->hmres, 4 * BM * sizeof(int), hipHostMallocDefault) != hipSuccess)
+    rc = CWEN_ENOMEM;
+  if (!rc) rc = dmalloc(&m->mctl, 2);  // last: marks the buffers complete
+  return rc;
 }
 
 int ready(const cwen_model *m) {
@@ -426,7 +612,7 @@ int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out
   m->ctx = ctx;
   m->cfg = *cfg;
   const cwen_model_cfg &c = m->cfg;
-  m->L = new (std::nothrow) Layer[c.n_layers];
+  m->L = new (std::nothrow) Layer[c.n_layers + 1];  // + the MTP block
   if (!m->L) { delete m; return CWEN_ENOMEM; }
   const int H = c.d_model, I = c.d_ffn, BM = CWEN_BMAX;
   const Rows R = rows_of(c);
@@ -484,7 +670,7 @@ int cwen_model_free(cwen_model *m) {
   drop_graphs(m);
   if (m->cap) (void)hipStreamDestroy(m->cap);
   if (m->tok_ev) (void)hipEventDestroy(m->tok_ev);
-  for (int l = 0; m->L && l < m->cfg.n_layers; ++l) {
+  for (int l = 0; m->L && l <= m->cfg.n_layers; ++l) {
     Layer &y = m->L[l];
     for (float *p : {y.attn_norm, y.post_norm, y.ssm_a, y.ssm_dt, y.ssm_conv, y.ssm_norm, y.q_norm, y.k_norm, y.K,
                      y.V})
@@ -499,6 +685,12 @@ int cwen_model_free(cwen_model *m) {
                   (void *)m->qbuf,
                   (void *)m->apart, (void *)m->yh, (void *)m->hh, (void *)m->logits})
     if (p) (void)hipFree(p);
+  for (void *p : {(void *)m->mtp_enorm, (void *)m->mtp_hnorm, (void *)m->mtp_shn, (void *)m->mctl, (void *)m->mres,
+                  (void *)m->hprev, (void *)m->hin, (void *)m->e2, (void *)m->X2, (void *)m->cat, (void *)m->xh2,
+                  (void *)m->ssq2, (void *)m->mlogits})
+    if (p) (void)hipFree(p);
+  if (m->mtp_eh) cwen_weight_free(m->mtp_eh);
+  if (m->hmres) (void)hipHostFree(m->hmres);
   if (m->head) cwen_weight_free(m->head);
   if (m->hres) (void)hipHostFree(m->hres);
   if (m->htok) (void)hipHostFree(m->htok);
@@ -535,7 +727,21 @@ int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data,
   }
   if (id == CWEN_OUTPUT_NORM) return (f32 && ne0 == H) ? upload_f32(data, H, &m->out_norm) : CWEN_EINVAL;
   if (id == CWEN_OUTPUT) return f32 ? CWEN_ETYPE : upload_w(m, type, data, scales, ne0, ne1, H, c.vocab, &m->head);
-  if (layer < 0 || layer >= c.n_layers) return CWEN_EINVAL;
+  if (id >= CWEN_NEXTN_EH_PROJ && id <= CWEN_NEXTN_SHEAD_NORM) {
+    int rc = mtp_alloc(m);
+    if (rc) return rc;
+    switch (id) {
+      case CWEN_NEXTN_EH_PROJ: return upload_w(m, type, data, scales, ne0, ne1, 2 * H, H, &m->mtp_eh);
+      case CWEN_NEXTN_ENORM: return (f32 && ne0 == H) ? upload_f32(data, H, &m->mtp_enorm) : CWEN_EINVAL;
+      case CWEN_NEXTN_HNORM: return (f32 && ne0 == H) ? upload_f32(data, H, &m->mtp_hnorm) : CWEN_EINVAL;
+      default: return (f32 && ne0 == H) ? upload_f32(data, H, &m->mtp_shn) : CWEN_EINVAL;
+    }
+  }
+  if (layer < 0 || layer > c.n_layers) return CWEN_EINVAL;
+  if (layer == c.n_layers) {
+    int rc = mtp_alloc(m);
+    if (rc) return rc;
+  }
   Layer &y = m->L[layer];
   switch (id) {
     case CWEN_ATTN_NORM: return (f32 && ne0 == H) ? upload_f32(data, H, &y.attn_norm) : CWEN_EINVAL;
@@ -661,6 +867,7 @@ int cwen_model_reset(cwen_model *m) {
   const int ctl0[6] = {-1, 0, 0, 0, 0, 0};  // clears the range flag too
   CWEN_HIP_TRY(hipMemcpy(m->ctl, ctl0, sizeof(ctl0), hipMemcpyHostToDevice));
   m->pos = -1;
+  m->mtp_hpos = -1;
   return CWEN_OK;
 }
 
@@ -697,6 +904,47 @@ int cwen_model_verify(cwen_model *m, const int *blk, int B, int *k_out, int *bon
   if (k_out) *k_out = k;
   if (bonus_out) *bonus_out = m->hres[2];
   return m->hres[0] ? CWEN_ERANGE : CWEN_OK;
+}
+
+int cwen_model_has_mtp(const cwen_model *m) { return m ? mtp_ready(m) : CWEN_EINVAL; }
+
+int cwen_model_mtp_draft(cwen_model *m, int pend, int n, int *drafts, void *stream) {
+  if (!m || !drafts || n < 0 || n > CWEN_BMAX - 1 || pend < 0 || pend >= m->cfg.vocab) return CWEN_EINVAL;
+  if (!mtp_ready(m) || !ready(m) || m->pos < 0 || m->mtp_hpos != m->pos || n == 0) return 0;
+  if (m->pos + n >= m->cfg.max_ctx) n = m->cfg.max_ctx - 1 - m->pos;
+  if (n <= 0) return 0;
+  hipStream_t st = (hipStream_t)stream;
+  const cwen_model_cfg &c = m->cfg;
+  CWEN_HIP_TRY(hipSetDevice(m->ctx->device));
+  CWEN_HIP_TRY(hipEventSynchronize(m->tok_ev));
+  m->htok[0] = pend;
+  CWEN_HIP_TRY(hipMemcpyAsync(m->toks, m->htok, sizeof(int), hipMemcpyHostToDevice, st));
+  CWEN_HIP_TRY(hipEventRecord(m->tok_ev, st));
+  // slots pos+1 .. pos+n, at indices pos .. pos+n-1
+  hipLaunchKernelGGL(mtp_ctl_kernel, dim3(1), dim3(1), 0, st, m->mctl, m->pos - 1, 0);
+  CWEN_HIP_TRY(hipGetLastError());
+  for (int t = 0; t < n; ++t) {
+    const int *tok = t ? m->mres + 4 * (t - 1) + 1 : m->toks;
+    const int rc = t ? mtp_pass(m, 1, tok, m->X2, c.d_model, m->mtp_shn, t, st)
+                     : mtp_pass(m, 1, tok, m->hprev, c.d_model, m->out_norm, t, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(mtp_ctl_kernel, dim3(1), dim3(1), 0, st, m->mctl, 1, 1);
+    CWEN_HIP_TRY(hipGetLastError());
+  }
+  CWEN_HIP_TRY(hipMemcpyAsync(m->hmres, m->mres, (size_t)4 * n * sizeof(int), hipMemcpyDeviceToHost, st));
+  CWEN_HIP_TRY(hipStreamSynchronize(st));
+  for (int t = 0; t < n; ++t) {
+    drafts[t] = m->hmres[4 * t + 1];
+    if (drafts[t] < 0 || drafts[t] >= c.vocab) return CWEN_EHIP;
+  }
+  return n;
+}
+
+int cwen_model_mtp_logits(cwen_model *m, float *host, int rows) {
+  if (!m || !host || rows < 1 || rows > CWEN_BMAX || !m->mlogits) return CWEN_EINVAL;
+  CWEN_HIP_TRY(hipDeviceSynchronize());
+  CWEN_HIP_TRY(hipMemcpy(host, m->mlogits, (size_t)rows * m->cfg.vocab * sizeof(float), hipMemcpyDeviceToHost));
+  return CWEN_OK;
 }
 
 int cwen_model_logits(cwen_model *m, float *host, int rows) {

@@ -56,6 +56,9 @@ SIGNATURES = [
     ("cwen_model_forward", _I, [_VP, _VP, _I, _I, _VP, _VP]),
     ("cwen_model_verify", _I, [_VP, _VP, _I, C.POINTER(_I), C.POINTER(_I), _VP]),
     ("cwen_model_logits", _I, [_VP, _VP, _I]),
+    ("cwen_model_has_mtp", _I, [_VP]),
+    ("cwen_model_mtp_draft", _I, [_VP, _I, _I, _VP, _VP]),
+    ("cwen_model_mtp_logits", _I, [_VP, _VP, _I]),
 ]
 
 # libcwen_host.so (include/.. cwen_amd/host/cwen_host.h)
@@ -316,12 +319,12 @@ class ModelCfg(C.Structure):
 
 (TOK_EMBD, OUTPUT_NORM, OUTPUT, ATTN_NORM, POST_NORM, FFN_GATE_UP, FFN_DOWN, ATTN_QKV, ATTN_GATE, SSM_ALPHA,
  SSM_BETA, SSM_A, SSM_DT, SSM_CONV, SSM_NORM, SSM_OUT, ATTN_Q, ATTN_KV, ATTN_OUTPUT, ATTN_Q_NORM,
- ATTN_K_NORM) = range(21)
+ ATTN_K_NORM, NEXTN_EH_PROJ, NEXTN_ENORM, NEXTN_HNORM, NEXTN_SHEAD_NORM) = range(25)
 
 
 class SpecCfg(C.Structure):
     _fields_ = [("n_key", C.c_int), ("max_draft", C.c_int), ("min_draft", C.c_int), ("cooldown", C.c_int),
-                ("max_cycles", C.c_int)]
+                ("max_cycles", C.c_int), ("mtp", C.c_int)]
 
 
 class SpecStats(C.Structure):
@@ -448,6 +451,22 @@ class Model:
         check("cwen_model_logits", lib().cwen_model_logits(self.h, out.ctypes.data, rows))
         return out
 
+    def has_mtp(self) -> bool:
+        return lib().cwen_model_has_mtp(self.h) == 1
+
+    def mtp_draft(self, pend: int, n: int) -> np.ndarray:
+        """Up to n greedy drafts of the MTP block after the last filled position."""
+        out = np.zeros(max(n, 1), dtype=np.int32)
+        k = lib().cwen_model_mtp_draft(self.h, int(pend), n, out.ctypes.data, None)
+        if k < 0:
+            raise CwenError("cwen_model_mtp_draft", k)
+        return out[:k]
+
+    def mtp_logits(self, rows: int) -> np.ndarray:
+        out = np.empty((rows, self.cfg.vocab), dtype=np.float32)
+        check("cwen_model_mtp_logits", lib().cwen_model_mtp_logits(self.h, out.ctypes.data, rows))
+        return out
+
     def generate_serial(self, prompt, n_gen: int, with_stats: bool = False):
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.zeros(n_gen, dtype=np.int32)
@@ -458,10 +477,10 @@ class Model:
         return (out[:n], st) if with_stats else out[:n]
 
     def generate_spec(self, prompt, n_gen: int, n_key: int = 16, max_draft: int = 8, min_draft: int = 2,
-                      cooldown: int = 8, max_cycles: int = 0) -> tuple[np.ndarray, SpecStats]:
+                      cooldown: int = 8, max_cycles: int = 0, mtp: int = 1) -> tuple[np.ndarray, SpecStats]:
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.zeros(n_gen, dtype=np.int32)
-        cfg = SpecCfg(n_key, max_draft, min_draft, cooldown, max_cycles)
+        cfg = SpecCfg(n_key, max_draft, min_draft, cooldown, max_cycles, mtp)
         st = SpecStats()
         n = host_lib().cwen_generate_spec(self.h, p.ctypes.data, p.size, n_gen, C.byref(cfg), out.ctypes.data,
                                           C.byref(st))

@@ -20,6 +20,7 @@ void cwen_spec_default(cwen_spec_cfg *cfg) {
   cfg->min_draft = 2;
   cfg->cooldown = 8;
   cfg->max_cycles = 0;
+  cfg->mtp = 1;
 }
 
 /* run.c:4533-4549 */
@@ -108,6 +109,7 @@ int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen
     out[g++] = pend;
   }
   const int cap_hard = cfg.max_draft;
+  const int use_mtp = cfg.mtp && cwen_model_has_mtp(m) == 1;
   int E_cap = cap_hard;
   int blk[CWEN_BMAX];
   while (g > 0 && g < n_gen) {
@@ -120,7 +122,12 @@ int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen
     } else {
       const int room = cap - 1 - (pos + 1);        /* block slots must stay in range */
       const int lim = E_cap < room ? E_cap : room;
-      E = cwen_ngram_draft(hist, hn, blk + 1, cfg.n_key, lim);
+      if (use_mtp) {
+        E = cwen_model_mtp_draft(m, hist[hn - 1], lim, blk + 1, NULL);
+        if (E < 0) { free(hist); return E; }
+      } else {
+        E = cwen_ngram_draft(hist, hn, blk + 1, cfg.n_key, lim);
+      }
       if (E && E < cfg.min_draft) E = 0;
     }
     blk[0] = hist[hn - 1];                         /* pend */

@@ -22,6 +22,8 @@ typedef struct {
   int min_draft;   /* a proposal shorter than this is dropped (2) */
   int cooldown;    /* plain steps after 3 short walks (8)      */
   int max_cycles;  /* stop after this many verify cycles (0: no limit) */
+  int mtp;         /* draft with the model's MTP block when it has one,
+                      else the n-gram drafter (1; run.c CWEN_MTP)      */
 } cwen_spec_cfg;
 
 typedef struct {
@@ -49,8 +51,10 @@ int cwen_prefill(cwen_model *m, const int *prompt, int n_prompt, int *next);
 int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_gen, int *out,
                          cwen_spec_stats *stats);
 
-/* generate_tokens_spec (run.c:4882-5025) with the n-gram drafter: the same
- * token stream as cwen_generate_serial, produced by block-verify cycles. */
+/* generate_tokens_spec (run.c:4882-5025): the same token stream as
+ * cwen_generate_serial, produced by block-verify cycles; the drafts come
+ * from the model's MTP block (cwen_model_mtp_draft) when cfg->mtp is set and
+ * the model has one, else from the n-gram drafter. */
 int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen, const cwen_spec_cfg *cfg,
                        int *out, cwen_spec_stats *stats);
 

@@ -137,14 +137,15 @@ def rsi_side(qs: np.ndarray, sc: np.ndarray, M: int, K: int, side: int) -> tuple
 
 
 # ---------------------------------------------------------------- whole model
-def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False):
+def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool = False):
     """Seeded random-init tensors of the hybrid decoder, in the reference's
     layouts: yields (layer, tensor id, type, data, scales, ne0, ne1); layer -1
     for the global tensors.  Q4_0 matrices are CWENR (RS, or RSI for the
     gate/up and k/v pairs), the head Q6_K, the embedding Q4_0RS; norms, conv
     taps and gate parameters F32.  real_types: the GGUF types the real
     model mixes in -- ffn_down of every other layer in Q4_1, every ssm_out
-    in Q5_K."""
+    in Q5_K.  mtp: also the MTP nextn drafter -- a full-attention block at
+    layer n_layers and the nextn eh_proj (Q4_0RS, [H][2H]) and norms."""
     from . import gpu as G
     H, I, V = cfg["d_model"], cfg["d_ffn"], cfg["vocab"]
     nkh, nvh = cfg["gdn_nkh"], cfg["gdn_nvh"]
@@ -160,9 +161,9 @@ def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False):
     yield -1, G.TOK_EMBD, G.T_Q4_0RS, qs, sc, H, V
     yield -1, G.OUTPUT_NORM, G.T_F32, norm_w(1, H), None, H, 1
     yield -1, G.OUTPUT, G.T_Q6_K, q6_k(seed, V, H, key=1001), None, H, V
-    for l in range(cfg["n_layers"]):
+
+    def layer(l, full, real_types):
         k0 = 100 * (l + 1)
-        full = l % cfg["full_interval"] == cfg["full_interval"] - 1
         yield l, G.ATTN_NORM, G.T_F32, norm_w(k0 + 1, H), None, H, 1
         yield l, G.POST_NORM, G.T_F32, norm_w(k0 + 2, H), None, H, 1
         qs, sc = q4_rsi(seed, I, H, key=k0 + 3)
@@ -196,6 +197,16 @@ def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False):
             yield l, G.ATTN_OUTPUT, G.T_Q4_0RS, qs, sc, Qo, H
             yield l, G.ATTN_Q_NORM, G.T_F32, norm_w(k0 + 14, cfg["head_dim"]), None, cfg["head_dim"], 1
             yield l, G.ATTN_K_NORM, G.T_F32, norm_w(k0 + 15, cfg["head_dim"]), None, cfg["head_dim"], 1
+
+    for l in range(cfg["n_layers"]):
+        yield from layer(l, l % cfg["full_interval"] == cfg["full_interval"] - 1, real_types)
+    if mtp:
+        NL = cfg["n_layers"]
+        yield from layer(NL, True, False)
+        qs, sc = q4_rs(seed, H, 2 * H, key=90001)
+        yield -1, G.NEXTN_EH_PROJ, G.T_Q4_0RS, qs, sc, 2 * H, H
+        for tid, key in ((G.NEXTN_ENORM, 90002), (G.NEXTN_HNORM, 90003), (G.NEXTN_SHEAD_NORM, 90004)):
+            yield -1, tid, G.T_F32, norm_w(key, H), None, H, 1
 
 
 def prompt_tokens(seed: int, n: int, V: int, period: int = 37, noise: float = 0.1) -> np.ndarray:

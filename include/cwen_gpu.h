@@ -222,7 +222,15 @@ enum {
   CWEN_ATTN_KV,          /* attn_k + attn_v        Q4_0RSI pair [NKV*HD][H]       */
   CWEN_ATTN_OUTPUT,      /* attn_output            [H][NH*HD]                     */
   CWEN_ATTN_Q_NORM,      /* attn_q_norm            F32 [HD]                       */
-  CWEN_ATTN_K_NORM       /* attn_k_norm            F32 [HD]                       */
+  CWEN_ATTN_K_NORM,      /* attn_k_norm            F32 [HD]                       */
+  /* MTP nextn drafter (run.c:3087-3187, the GGUF's blk.N, N = n_layers):
+   * these four at layer -1; its decoder block is layer n_layers, set with
+   * the full-attention ids above (attn_norm, post_norm, ffn pair and down,
+   * attn_q, the k/v pair, attn_output, q/k norms). */
+  CWEN_NEXTN_EH_PROJ,    /* nextn.eh_proj          [H][2H] (input [e' | h'])      */
+  CWEN_NEXTN_ENORM,      /* nextn.enorm            F32 [H]                        */
+  CWEN_NEXTN_HNORM,      /* nextn.hnorm            F32 [H]                        */
+  CWEN_NEXTN_SHEAD_NORM  /* nextn.shared_head_norm F32 [H]                        */
 };
 
 int cwen_model_create(cwen_ctx *ctx, const cwen_model_cfg *cfg, cwen_model **out);
@@ -264,6 +272,21 @@ int cwen_model_forward(cwen_model *m, const int *toks, int B, int want_argmax, i
 int cwen_model_verify(cwen_model *m, const int *blk, int B, int *k, int *bonus, void *stream);
 /* Copy the f32 logits of the last head pass (rows 0..rows-1) to HOST. */
 int cwen_model_logits(cwen_model *m, float *host, int rows);
+
+/* MTP nextn drafter.  1 when every MTP tensor is set.  From then on each
+ * forward / verify block also commits its kept positions into the drafter's
+ * own KV stream on the device (mtp_commit, run.c:3150-3163). */
+int cwen_model_has_mtp(const cwen_model *m);
+/* mtp_draft (run.c:3170-3187): up to n (<= CWEN_BMAX - 1) greedy drafts after
+ * the last filled position, starting from the pending token pend, each step
+ * the nextn block on the previous step's own output plus the shared head,
+ * chained on the device; one synchronisation at the end.  Returns the count
+ * (fewer near the end of the context; 0 without an MTP block or before the
+ * first block), or a negative status.  The slots drafted are speculative:
+ * the next block's commit rewrites them. */
+int cwen_model_mtp_draft(cwen_model *m, int pend, int n, int *drafts, void *stream);
+/* Copy the f32 logits of the last draft's steps (rows 0..rows-1) to HOST. */
+int cwen_model_mtp_logits(cwen_model *m, float *host, int rows);
 
 /* ---- f16 activation operands ----
  * The kernels read activations as IEEE half, row-major [B][K] with row stride

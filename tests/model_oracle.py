@@ -1,7 +1,8 @@
 """Serial forward pass of the hybrid decoder composed from the oracle's C
 restatements (test infrastructure).  Mirrors forward_ex / layer_linear /
 layer_full / mlp of the reference (run.c:2594-2645, 2325-2358, 2412-2458,
-2205-2321) one position at a time."""
+2205-2321) one position at a time, and, when the tensors hold an MTP block,
+its nextn stream: mtp_step / mtp_commit / mtp_draft (run.c:3099-3187)."""
 import numpy as np
 
 T_F32, T_Q4_0RS, T_Q4_0RSI, T_Q6_K = 0, 101, 102, 14
@@ -21,6 +22,8 @@ class OracleModel:
             self.t[(layer, tid)] = (wtype, data, sc, ne0, ne1)
         c = cfg
         self.C = (2 * c["gdn_nkh"] + c["gdn_nvh"]) * 128
+        from cwen_amd import gpu as G
+        self.has_mtp = (-1, G.NEXTN_EH_PROJ) in self.t
         self.reset()
 
     def reset(self):
@@ -36,6 +39,10 @@ class OracleModel:
             else:
                 self.S[l] = np.zeros((c["gdn_nvh"], 128, 128), np.float32)
                 self.hist[l] = np.zeros((self.C, 3), np.float32)
+        NL = c["n_layers"]
+        self.K[NL] = np.zeros((c["max_ctx"], c["n_kv_head"], c["head_dim"]), np.float32)
+        self.V[NL] = np.zeros_like(self.K[NL])
+        self.hprev, self.hpos = None, -1
 
     def mv(self, layer, tid, x, side=0):
         wtype, data, sc, ne0, ne1 = self.t[(layer, tid)]
@@ -68,21 +75,71 @@ class OracleModel:
                                              c["gdn_nkh"], c["gdn_nvh"], 128)
                 x = (x + self.mv(l, G.SSM_OUT, o)).astype(np.float32)
             else:
-                NH, NKV, HD = c["n_head"], c["n_kv_head"], c["head_dim"]
-                qf = self.mv(l, G.ATTN_Q, xb).reshape(NH, 2, HD)
-                q, gate = qf[:, 0].copy(), qf[:, 1].copy()
-                k = self.mv(l, G.ATTN_KV, xb, 0).reshape(NKV, HD)
-                v = self.mv(l, G.ATTN_KV, xb, 1).reshape(NKV, HD)
-                qn, kn = self.f32(l, G.ATTN_Q_NORM), self.f32(l, G.ATTN_K_NORM)
-                q = np.stack([O.rmsnorm(q[h], qn) for h in range(NH)])
-                k = np.stack([O.rmsnorm(k[h], kn) for h in range(NKV)])
-                q = O.rope(q, pos, c["n_rot_pairs"], c["n_rot"], c["rope_theta"])
-                k = O.rope(k, pos, c["n_rot_pairs"], c["n_rot"], c["rope_theta"])
-                self.K[l][pos], self.V[l][pos] = k, v
-                att = O.attention(self.K[l][:pos + 1], self.V[l][:pos + 1], 0, pos, q, gate)
-                x = (x + self.mv(l, G.ATTN_OUTPUT, att.reshape(-1))).astype(np.float32)
-            xb = O.rmsnorm(x, self.f32(l, G.POST_NORM))
-            h = O.silu_mul(self.mv(l, G.FFN_GATE_UP, xb, 0), self.mv(l, G.FFN_GATE_UP, xb, 1))
-            x = (x + self.mv(l, G.FFN_DOWN, h)).astype(np.float32)
+                x = self.full_attn(l, x, xb, pos, 0)
+            x = self.mlp(l, x)
+        self.mtp_commit(pos, int(tok), x)
         xb = O.rmsnorm(x, self.f32(-1, G.OUTPUT_NORM))
         return self.mv(-1, G.OUTPUT, xb)
+
+    def full_attn(self, l, x, xb, pos, t0):
+        """layer_full (run.c:2412-2458): x + the gated attention over slots t0..pos."""
+        from cwen_amd import gpu as G
+        O, c = self.O, self.c
+        NH, NKV, HD = c["n_head"], c["n_kv_head"], c["head_dim"]
+        qf = self.mv(l, G.ATTN_Q, xb).reshape(NH, 2, HD)
+        q, gate = qf[:, 0].copy(), qf[:, 1].copy()
+        k = self.mv(l, G.ATTN_KV, xb, 0).reshape(NKV, HD)
+        v = self.mv(l, G.ATTN_KV, xb, 1).reshape(NKV, HD)
+        qn, kn = self.f32(l, G.ATTN_Q_NORM), self.f32(l, G.ATTN_K_NORM)
+        q = np.stack([O.rmsnorm(q[h], qn) for h in range(NH)])
+        k = np.stack([O.rmsnorm(k[h], kn) for h in range(NKV)])
+        q = O.rope(q, pos, c["n_rot_pairs"], c["n_rot"], c["rope_theta"])
+        k = O.rope(k, pos, c["n_rot_pairs"], c["n_rot"], c["rope_theta"])
+        self.K[l][pos], self.V[l][pos] = k, v
+        att = O.attention(self.K[l][:pos + 1], self.V[l][:pos + 1], t0, pos, q, gate)
+        return (x + self.mv(l, G.ATTN_OUTPUT, att.reshape(-1))).astype(np.float32)
+
+    def mlp(self, l, x):
+        from cwen_amd import gpu as G
+        O = self.O
+        xb = O.rmsnorm(x, self.f32(l, G.POST_NORM))
+        h = O.silu_mul(self.mv(l, G.FFN_GATE_UP, xb, 0), self.mv(l, G.FFN_GATE_UP, xb, 1))
+        return (x + self.mv(l, G.FFN_DOWN, h)).astype(np.float32)
+
+    def mtp_step(self, tok: int, pos: int, h: np.ndarray) -> np.ndarray:
+        """mtp_step (run.c:3099-3133): the nextn block at stream slot pos on
+        token tok and predecessor hidden h; returns the shared-head-normed
+        hidden.  The stream's attention covers slots 1..pos."""
+        from cwen_amd import gpu as G
+        O, NL = self.O, self.c["n_layers"]
+        wtype, qs, sc, H, _ = self.t[(-1, G.TOK_EMBD)]
+        e = O.embed(wtype, qs, sc, int(tok), H)
+        cat = np.concatenate([O.rmsnorm(e, self.f32(-1, G.NEXTN_ENORM)), O.rmsnorm(h, self.f32(-1, G.NEXTN_HNORM))])
+        x = self.mv(-1, G.NEXTN_EH_PROJ, cat.astype(np.float32))
+        x = self.full_attn(NL, x, O.rmsnorm(x, self.f32(NL, G.ATTN_NORM)), pos, 1)
+        x = self.mlp(NL, x)
+        return O.rmsnorm(x, self.f32(-1, G.NEXTN_SHEAD_NORM))
+
+    def mtp_commit(self, pos: int, tok: int, x_pre: np.ndarray) -> None:
+        """mtp_commit (run.c:3150-3163): step the committed position (from
+        slot 1 on) against the parked hidden of pos - 1, then park
+        rmsnorm(x_pre, output_norm)."""
+        from cwen_amd import gpu as G
+        if not self.has_mtp:
+            return
+        if pos >= 1 and self.hpos == pos - 1:
+            self.mtp_step(tok, pos, self.hprev)
+        self.hprev = self.O.rmsnorm(x_pre, self.f32(-1, G.OUTPUT_NORM))
+        self.hpos = pos
+
+    def mtp_draft_logits(self, pend: int, pos: int, inputs) -> np.ndarray:
+        """mtp_draft (run.c:3170-3187) from the hidden parked at pos, with the
+        step inputs given (pend, then the previous drafts): each step's head
+        logits."""
+        from cwen_amd import gpu as G
+        assert self.hpos == pos
+        h, out = self.hprev, []
+        for t, tok in enumerate([pend] + list(inputs)):
+            h = self.mtp_step(int(tok), pos + 1 + t, h)
+            out.append(self.mv(-1, G.OUTPUT, h))
+        return np.stack(out)

@@ -217,7 +217,7 @@ def test_serve_answers_frames_like_generate(env):
         req += struct.pack("<II", len(p), g) + np.asarray(p, "<i4").tobytes()
         if i == 0:
             req += struct.pack("<IIi", 1, 4, CFG["vocab"])           # rejected: token out of range
-    for spec in (None, gpu.SpecCfg(2, 8, 2, 8, 0)):
+    for spec in (None, gpu.SpecCfg(2, 8, 2, 8, 0, 1)):
         ri, wi = os.pipe()
         ro, wo = os.pipe()
         os.write(wi, req)
