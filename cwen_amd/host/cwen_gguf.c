@@ -704,6 +704,55 @@ int cwen_model_load_gguf(cwen_model *m, const cwen_model_cfg *c, const cwen_gguf
     }
 #undef NM
   }
+  /* The MTP nextn block blk.N, N = n_layers (run.c:3409-3464): bound when
+   * its eh_proj is present, and then every part with its shape pinned. */
+  snprintf(n, sizeof n, "blk.%d.nextn.eh_proj.weight", c->n_layers);
+  if (cwen_gguf_find(g, n) >= 0) {
+    const int l = c->n_layers;
+    NEED(t, mat(g, n, 2 * H, H, &rc));
+    TRY(set_mat(m, -1, CWEN_NEXTN_EH_PROJ, t));
+    static const struct { const char *suf; int id; } norms[] = {
+        {"nextn.enorm.weight", CWEN_NEXTN_ENORM}, {"nextn.hnorm.weight", CWEN_NEXTN_HNORM},
+        {"nextn.shared_head_norm.weight", CWEN_NEXTN_SHEAD_NORM}};
+    for (int k = 0; k < 3; k++) {
+      snprintf(n, sizeof n, "blk.%d.%s", l, norms[k].suf);
+      NEED(u, vec(g, n, H, &rc));
+      TRY(set_vec(m, -1, norms[k].id, u, H));
+    }
+#define NM(buf, suf) snprintf(buf, sizeof buf, "blk.%d.%s", l, suf)
+    NM(n, "attn_norm.weight");
+    NEED(u, vec(g, n, H, &rc));
+    TRY(set_vec(m, l, CWEN_ATTN_NORM, u, H));
+    NM(n, "post_attention_norm.weight");
+    NEED(u, vec(g, n, H, &rc));
+    TRY(set_vec(m, l, CWEN_POST_NORM, u, H));
+    NM(n, "ffn_gate.weight");
+    NM(n2, "ffn_up.weight");
+    NEED(t, mat(g, n, H, I, &rc));
+    NEED(u, mat(g, n2, H, I, &rc));
+    TRY(set_pair(m, l, CWEN_FFN_GATE_UP, t, u));
+    NM(n, "ffn_down.weight");
+    NEED(t, mat(g, n, I, H, &rc));
+    TRY(set_mat(m, l, CWEN_FFN_DOWN, t));
+    NM(n, "attn_q.weight");
+    NEED(t, mat(g, n, H, 2 * Qo, &rc));
+    TRY(set_mat(m, l, CWEN_ATTN_Q, t));
+    NM(n, "attn_k.weight");
+    NM(n2, "attn_v.weight");
+    NEED(t, mat(g, n, H, Ko, &rc));
+    NEED(u, mat(g, n2, H, Ko, &rc));
+    TRY(set_pair(m, l, CWEN_ATTN_KV, t, u));
+    NM(n, "attn_output.weight");
+    NEED(t, mat(g, n, Qo, H, &rc));
+    TRY(set_mat(m, l, CWEN_ATTN_OUTPUT, t));
+    NM(n, "attn_q_norm.weight");
+    NEED(u, vec(g, n, c->head_dim, &rc));
+    TRY(set_vec(m, l, CWEN_ATTN_Q_NORM, u, c->head_dim));
+    NM(n, "attn_k_norm.weight");
+    NEED(u, vec(g, n, c->head_dim, &rc));
+    TRY(set_vec(m, l, CWEN_ATTN_K_NORM, u, c->head_dim));
+#undef NM
+  }
   g_err[0] = 0;
   return CWEN_OK;
 }

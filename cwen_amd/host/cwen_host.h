@@ -100,7 +100,8 @@ uint16_t cwen_f32_to_f16(float x);
  * interleaved on the host into the device's pair form; output.weight falls
  * back to token_embd.weight (tied).  The embedding must be Q4_0.  Tensors a
  * sidecar rebound are uploaded from its views (an interleaved pair as it
- * is). */
+ * is).  When blk.<n_layers>.nextn.eh_proj.weight is present the MTP nextn
+ * block is bound too, every part required (run.c:3409-3464). */
 int cwen_model_load_gguf(cwen_model *m, const cwen_model_cfg *cfg, const cwen_gguf *g);
 
 /* ---- binary-frame server (cwen_serve.c) ---- */

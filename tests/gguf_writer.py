@@ -49,7 +49,11 @@ def model_gguf_tensors(tensors, cfg: dict):
             G.ATTN_Q: "attn_q.weight", G.ATTN_OUTPUT: "attn_output.weight",
             G.ATTN_Q_NORM: "attn_q_norm.weight", G.ATTN_K_NORM: "attn_k_norm.weight"}
     pairs = {G.FFN_GATE_UP: ("ffn_gate.weight", "ffn_up.weight"), G.ATTN_KV: ("attn_k.weight", "attn_v.weight")}
-    glob = {G.TOK_EMBD: "token_embd.weight", G.OUTPUT_NORM: "output_norm.weight", G.OUTPUT: "output.weight"}
+    NL = cfg["n_layers"]
+    glob = {G.TOK_EMBD: "token_embd.weight", G.OUTPUT_NORM: "output_norm.weight", G.OUTPUT: "output.weight",
+            G.NEXTN_EH_PROJ: f"blk.{NL}.nextn.eh_proj.weight", G.NEXTN_ENORM: f"blk.{NL}.nextn.enorm.weight",
+            G.NEXTN_HNORM: f"blk.{NL}.nextn.hnorm.weight",
+            G.NEXTN_SHEAD_NORM: f"blk.{NL}.nextn.shared_head_norm.weight"}
     C = (2 * cfg["gdn_nkh"] + cfg["gdn_nvh"]) * 128
     out = []
     for layer, tid, wtype, data, sc, ne0, ne1 in tensors:

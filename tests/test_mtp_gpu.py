@@ -127,6 +127,40 @@ def test_spec_with_mtp_equals_serial(env):
     assert np.array_equal(ng, serial)
 
 
+def test_gguf_with_nextn_block_equals_set(env, tmp_path):
+    """A GGUF file holding blk.N.nextn.* and blk.N's block (N = n_layers)
+    loads the drafter: drafts and their logits equal the set model's, bit for
+    bit; without its shared_head_norm the load is refused, naming it."""
+    gpu, ctx, m, tensors = env
+    from gguf_writer import gguf_bytes, model_gguf_tensors
+    gt = model_gguf_tensors(tensors, CFG)
+    p = tmp_path / "mtp.gguf"
+    p.write_bytes(gguf_bytes(gt))
+    g = gpu.GGUF(p)
+    mg = gpu.Model(ctx, **CFG)
+    mg.load_gguf(g)
+    assert mg.has_mtp()
+    toks = synth.prompt_tokens(15, 12, CFG["vocab"])
+    m.reset()
+    pend = int(m.forward(toks)[-1])
+    assert int(mg.forward(toks)[-1]) == pend
+    a, b = m.mtp_draft(pend, 4), mg.mtp_draft(pend, 4)
+    assert np.array_equal(a, b)
+    assert np.array_equal(m.mtp_logits(4).view(np.uint32), mg.mtp_logits(4).view(np.uint32))
+    mg.free()
+    g.close()
+    NL = CFG["n_layers"]
+    p2 = tmp_path / "partial.gguf"
+    p2.write_bytes(gguf_bytes([t for t in gt if t[0] != f"blk.{NL}.nextn.shared_head_norm.weight"]))
+    g2 = gpu.GGUF(p2)
+    mg2 = gpu.Model(ctx, **CFG)
+    with pytest.raises(gpu.CwenError) as e:
+        mg2.load_gguf(g2)
+    assert f"missing blk.{NL}.nextn.shared_head_norm.weight" in str(e.value)
+    mg2.free()
+    g2.close()
+
+
 def test_no_mtp_block_drafts_nothing(env):
     gpu, ctx, _, _ = env
     tensors = list(synth.model_tensors(CFG, seed=0))
