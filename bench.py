@@ -317,6 +317,41 @@ def c4_leg(n_prompt: int, cycles: int) -> dict:
                     "so n-gram drafts are accepted far more often than on a trained model"}
 
 
+def mtp_leg(n_prompt: int, n_gen: int) -> dict:
+    """The MTP nextn drafter on the 27B-shape model (device-generated trunk,
+    seeded host-generated nextn block): the cost of one draft of 7 steps,
+    of a serial step carrying the drafter's commit pass, and a speculative
+    decode drafting with it (its output must equal the serial decode's)."""
+    import time
+    from cwen_amd import gpu, synth
+    ctx = gpu.Context(0)
+    m = gpu.Model(ctx, **C4_CFG)
+    m.synth(0)
+    for t in synth.mtp_tensors(C4_CFG, 1):
+        m.set(*t)
+    assert m.has_mtp()
+    prompt = synth.prompt_tokens(0, n_prompt, C4_CFG["vocab"], period=61, noise=0.02)
+    serial, st2 = m.generate_serial(prompt, n_gen, with_stats=True)
+    pend = int(serial[-1])
+    m.mtp_draft(pend, 7)
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        m.mtp_draft(pend, 7)
+    draft_ms = (time.perf_counter() - t0) / reps * 1e3
+    spec, st = m.generate_spec(prompt, n_gen, max_draft=7, mtp=1)
+    m.free()
+    return {"prompt_tokens": n_prompt, "tokens": int(len(spec)),
+            "draft7_ms": round(draft_ms, 3), "draft_step_ms": round(draft_ms / 7, 3),
+            "ms_per_serial_step_with_commit": round(st2.decode_s / max(st2.cycles, 1) * 1e3, 3),
+            "spec_ms_per_cycle": round(st.decode_s / max(st.cycles, 1) * 1e3, 3),
+            "spec_tok_s": round(len(spec) / st.decode_s, 1),
+            "serial_tok_s": round(len(serial) / st2.decode_s, 1),
+            "mean_accepted_drafts": round(st.kept / max(st.drafted, 1), 3),
+            "spec_equals_serial": bool(np.array_equal(spec, serial)),
+            "note": "random-init nextn block: its drafts are rarely accepted; the timings are the cost side"}
+
+
 def cpu_child(B: int, reps: int) -> None:
     """CPU baseline leg: the reference engine's own mlp_blk kernels (gemvb x3 +
     silu_mul, run.c:2677-2681), compiled from its run.c (oracle/_ref); the
@@ -391,6 +426,7 @@ def main() -> int:
     ap.add_argument("--no-c4", action="store_true", help="skip the full-model speculative decode")
     ap.add_argument("--c4-prompt", type=int, default=4096)
     ap.add_argument("--c4-cycles", type=int, default=256)
+    ap.add_argument("--mtp", action="store_true", help="also time the MTP nextn drafter on the 27B shape")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a 256 MiB device copy (for FETCH_SIZE/WRITE_SIZE calibration)")
     ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
@@ -411,6 +447,7 @@ def main() -> int:
     res = gpu_leg(args.steps, args.warmup, Bs)
     extra = None if args.no_extra else extra_leg(args.steps, args.warmup)
     c4 = None if args.no_c4 else c4_leg(args.c4_prompt, args.c4_cycles)
+    mtp = mtp_leg(args.c4_prompt, 64) if args.mtp else None
     traffic = load_traffic()
     h = res[8]
     b1, _ = ffn_bytes(8)
@@ -454,6 +491,8 @@ def main() -> int:
         "other_configs": extra,
         "c4_full_model_spec_b8": c4,
     }
+    if mtp is not None:
+        line["c4_mtp_drafter"] = mtp
     print(json.dumps(line))
     return 0
 

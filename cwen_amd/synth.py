@@ -137,7 +137,7 @@ def rsi_side(qs: np.ndarray, sc: np.ndarray, M: int, K: int, side: int) -> tuple
 
 
 # ---------------------------------------------------------------- whole model
-def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool = False):
+def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool = False, only_layer=None):
     """Seeded random-init tensors of the hybrid decoder, in the reference's
     layouts: yields (layer, tensor id, type, data, scales, ne0, ne1); layer -1
     for the global tensors.  Q4_0 matrices are CWENR (RS, or RSI for the
@@ -145,7 +145,9 @@ def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool 
     taps and gate parameters F32.  real_types: the GGUF types the real
     model mixes in -- ffn_down of every other layer in Q4_1, every ssm_out
     in Q5_K.  mtp: also the MTP nextn drafter -- a full-attention block at
-    layer n_layers and the nextn eh_proj (Q4_0RS, [H][2H]) and norms."""
+    layer n_layers and the nextn eh_proj (Q4_0RS, [H][2H]) and norms.
+    only_layer: that layer's tensors alone, as a full-attention layer (the
+    other tensors are not generated)."""
     from . import gpu as G
     H, I, V = cfg["d_model"], cfg["d_ffn"], cfg["vocab"]
     nkh, nvh = cfg["gdn_nkh"], cfg["gdn_nvh"]
@@ -156,11 +158,6 @@ def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool 
 
     def norm_w(key, n):
         return (1 + 0.1 * rng(seed, 20, key).standard_normal(n)).astype(f32)
-
-    qs, sc = q4_rs(seed, V, H, key=1000)
-    yield -1, G.TOK_EMBD, G.T_Q4_0RS, qs, sc, H, V
-    yield -1, G.OUTPUT_NORM, G.T_F32, norm_w(1, H), None, H, 1
-    yield -1, G.OUTPUT, G.T_Q6_K, q6_k(seed, V, H, key=1001), None, H, V
 
     def layer(l, full, real_types):
         k0 = 100 * (l + 1)
@@ -198,15 +195,32 @@ def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool 
             yield l, G.ATTN_Q_NORM, G.T_F32, norm_w(k0 + 14, cfg["head_dim"]), None, cfg["head_dim"], 1
             yield l, G.ATTN_K_NORM, G.T_F32, norm_w(k0 + 15, cfg["head_dim"]), None, cfg["head_dim"], 1
 
+    if only_layer is not None:
+        yield from layer(only_layer, True, False)
+        return
+    qs, sc = q4_rs(seed, V, H, key=1000)
+    yield -1, G.TOK_EMBD, G.T_Q4_0RS, qs, sc, H, V
+    yield -1, G.OUTPUT_NORM, G.T_F32, norm_w(1, H), None, H, 1
+    yield -1, G.OUTPUT, G.T_Q6_K, q6_k(seed, V, H, key=1001), None, H, V
+
     for l in range(cfg["n_layers"]):
         yield from layer(l, l % cfg["full_interval"] == cfg["full_interval"] - 1, real_types)
     if mtp:
-        NL = cfg["n_layers"]
-        yield from layer(NL, True, False)
-        qs, sc = q4_rs(seed, H, 2 * H, key=90001)
-        yield -1, G.NEXTN_EH_PROJ, G.T_Q4_0RS, qs, sc, 2 * H, H
-        for tid, key in ((G.NEXTN_ENORM, 90002), (G.NEXTN_HNORM, 90003), (G.NEXTN_SHEAD_NORM, 90004)):
-            yield -1, tid, G.T_F32, norm_w(key, H), None, H, 1
+        yield from mtp_tensors(cfg, seed)
+
+
+def mtp_tensors(cfg: dict, seed: int = 0):
+    """The MTP nextn drafter's tensors alone (model_tensors(mtp=True) ends
+    with them): the full-attention block at layer n_layers, eh_proj and the
+    three nextn norms."""
+    from . import gpu as G
+    H = cfg["d_model"]
+    NL = cfg["n_layers"]
+    yield from model_tensors(cfg, seed, only_layer=NL)
+    qs, sc = q4_rs(seed, H, 2 * H, key=90001)
+    yield -1, G.NEXTN_EH_PROJ, G.T_Q4_0RS, qs, sc, 2 * H, H
+    for tid, key in ((G.NEXTN_ENORM, 90002), (G.NEXTN_HNORM, 90003), (G.NEXTN_SHEAD_NORM, 90004)):
+        yield -1, tid, G.T_F32, (1 + 0.1 * rng(seed, 20, key).standard_normal(H)).astype(np.float32), None, H, 1
 
 
 def prompt_tokens(seed: int, n: int, V: int, period: int = 37, noise: float = 0.1) -> np.ndarray:
