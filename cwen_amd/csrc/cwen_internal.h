@@ -226,6 +226,9 @@ int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *tok
                  int *rflag = nullptr);
 size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B);
 int attention_init();
+// Largest query heads per KV head the attention kernels take at every block
+// size up to CWEN_BMAX (the block's queries of one KV head stay in registers).
+int attention_max_group();
 // `last` is a device int: the last filled cache slot before the block (the
 // block's positions are last+1 .. last+B).  The launch shape depends on
 // (B, NH, NKV, max_ctx) only, so a captured graph replays at any position.

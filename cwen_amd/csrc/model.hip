@@ -140,15 +140,17 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
 // In a product's k-th step lane group g (lanes 16g..16g+15) supplies
 // element g*run + k of the reduction dimension, so a lane reads 4 steps with
 // one 16-byte LDS read; the summation order is fixed and the same for every
-// query row, whatever B is.  Scores: one wave per 16-query tile (both 16-key
-// halves, so the chunk softmax stays in the wave).  P.V: V is staged
-// transposed; wave w takes head-dim tiles 4w..4w+3 of every query tile.  A
-// fixed grid of workgroups per kv head takes chunks blockIdx.x, + gridDim.x,
-// ... up to the block's last position (the partials are per chunk, so the
-// mapping does not change the arithmetic).
+// query row, whatever B is.  Scores: wave w takes 16-query tile w (both
+// 16-key halves, so the chunk softmax stays in the wave); a block with more
+// than 4 tiles runs 8-wave workgroups (NW = 8), so a wave never holds more
+// than one tile.  P.V: V is staged transposed; wave w takes head-dim tiles
+// (16/NW)w .. of every query tile.  Every output takes the same instruction
+// sequence for NW = 4 and 8.  A fixed grid of workgroups per kv head takes
+// chunks blockIdx.x, + gridDim.x, ... up to the block's last position (the
+// partials are per chunk, so the mapping does not change the arithmetic).
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int KROW = HD + 4, VROW = TC + 4, PROW = TC + 4;
-constexpr int QT_MAX = 2;    // 16-query tiles per wave held in registers (nq <= 4 * 2 * 16)
+constexpr int NW_MAX = 8;    // waves of the largest workgroup: 16-query tiles per block (nq <= 128)
 constexpr int KV_FLOATS = TC * KROW > HD * VROW ? TC * KROW : HD * VROW;
 
 __device__ __forceinline__ float max16(float m) {
@@ -156,9 +158,9 @@ __device__ __forceinline__ float max16(float m) {
   m = fmaxf(m, dpp<0x141>(m)); return fmaxf(m, dpp<0x140>(m));
 }
 
-// QT: 16-query tiles per wave (1 when the block has at most 4 tiles).
-template <int QT>
-__global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
+// NW: waves per workgroup (4, or 8 when the block has more than 4 query tiles).
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
   extern __shared__ __align__(16) float sm[];
   const int hkv = blockIdx.y;
   const int kvm = p.NH / p.NKV;
@@ -173,86 +175,67 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
   const float scale = 1.f / sqrtf((float)HD);
-  // The score phase's queries stay in registers: wave w holds 16-query
-  // tiles w and w + 4, lane (lr, lg) the HD/4 dims lg*HD/4 .. of query row
-  // lr of each (rows >= nq zero).  Keeping them out of LDS leaves room for
-  // several workgroups per CU.
-  float4 qreg[QT][HD / 16];
-#pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    const int qi = (wave + 4 * t) * 16 + lr;
+  // The score phase's queries stay in registers: wave w holds 16-query tile
+  // w, lane (lr, lg) the HD/4 dims lg*HD/4 .. of query row lr (rows >= nq
+  // zero).  Keeping them out of LDS leaves room for several workgroups per CU.
+  float4 qreg[HD / 16];
+  {
+    const int qi = wave * 16 + lr;
 #pragma unroll
     for (int k = 0; k < HD / 16; ++k)
-      qreg[t][k] = qi < nq ? *(const float4 *)(p.q + ((size_t)(qi / kvm) * p.NH + hkv * kvm + qi % kvm) * HD +
-                                              lg * (HD / 4) + 4 * k)
-                           : (float4){0.f, 0.f, 0.f, 0.f};
+      qreg[k] = qi < nq ? *(const float4 *)(p.q + ((size_t)(qi / kvm) * p.NH + hkv * kvm + qi % kvm) * HD +
+                                            lg * (HD / 4) + 4 * k)
+                        : (float4){0.f, 0.f, 0.f, 0.f};
   }
-  constexpr int KV_L = TC * (HD / 4) / 256;    // float4 of a chunk's K (or V) rows per thread
+  constexpr int KV_L = TC * (HD / 4) / (64 * NW);   // float4 of a chunk's K (or V) rows per thread
+  constexpr int DT = 16 / NW;                       // head-dim tiles of P.V per wave
   for (int c = blockIdx.x; c * TC <= tlast; c += gridDim.x) {
     const int t0 = c * TC;
     const int tn = min(TC, tlast + 1 - t0);     // keys of this chunk that exist
-    float4 kv[KV_L], vr[KV_L];                  // row t = wave + 4u, float4 d4 = lane
+    float4 kv[KV_L], vr[KV_L];                  // row t = wave + NW u, float4 d4 = lane
 #pragma unroll
     for (int u = 0; u < KV_L; ++u) {
-      const int t = wave + 4 * u;
+      const int t = wave + NW * u;
       const size_t at = ((size_t)(t0 + t) * p.NKV + hkv) * HD + lane * 4;
       kv[u] = t < tn ? *(const float4 *)(p.K + at) : (float4){0.f, 0.f, 0.f, 0.f};
       vr[u] = t < tn ? *(const float4 *)(p.V + at) : (float4){0.f, 0.f, 0.f, 0.f};  // held until P is done
     }
     __syncthreads();                            // previous chunk's reads of KV and Ps done
 #pragma unroll
-    for (int u = 0; u < KV_L; ++u) *(float4 *)(KV + (wave + 4 * u) * KROW + lane * 4) = kv[u];
+    for (int u = 0; u < KV_L; ++u) *(float4 *)(KV + (wave + NW * u) * KROW + lane * 4) = kv[u];
     __syncthreads();
     // scores and the chunk softmax, one 16-query tile per wave
-#pragma unroll
-    for (int t = 0; t < QT; ++t) {
-      const int mt = wave + 4 * t;
-      if (mt >= MT) break;
-      // QT == 1: four independent accumulators per 16 keys (the lane
-      // group's K run split in halves), summed at the end in a fixed order,
-      // for shorter MFMA dependency chains; QT == 2 keeps two (registers).
+    if (wave < MT) {
+      const int mt = wave;
+      // Four independent accumulators per 16 keys: s over the first half of
+      // the lane group's K run, u over the second, summed at the end.
       f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-      const float *k0 = KV + lr * KROW + lg * (HD / 4), *k1 = k0 + 16 * KROW;
-      if constexpr (QT == 2) {
-#pragma unroll
-        for (int k = 0; k < HD / 4; k += 4) {
-          const float4 a = qreg[t][k / 4], b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
-          s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b0.x, s0, 0, 0, 0);
-          s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b1.x, s1, 0, 0, 0);
-          s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b0.y, s0, 0, 0, 0);
-          s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b1.y, s1, 0, 0, 0);
-          s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b0.z, s0, 0, 0, 0);
-          s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b1.z, s1, 0, 0, 0);
-          s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b0.w, s0, 0, 0, 0);
-          s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b1.w, s1, 0, 0, 0);
-        }
-      } else {
       f32x4_t u0 = {0.f, 0.f, 0.f, 0.f}, u1 = {0.f, 0.f, 0.f, 0.f};
+      const float *k0 = KV + lr * KROW + lg * (HD / 4), *k1 = k0 + 16 * KROW;
 #pragma unroll
       for (int k = 0; k < HD / 8; k += 4) {
-        const float4 a = qreg[t][k / 4], b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
-        const float4 c = qreg[t][(k + HD / 8) / 4], e0 = *(const float4 *)(k0 + k + HD / 8),
+        const float4 a = qreg[k / 4], b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
+        const float4 cq = qreg[(k + HD / 8) / 4], e0 = *(const float4 *)(k0 + k + HD / 8),
                      e1 = *(const float4 *)(k1 + k + HD / 8);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b0.x, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b1.x, s1, 0, 0, 0);
-        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.x, e0.x, u0, 0, 0, 0);
-        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.x, e1.x, u1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.x, e0.x, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.x, e1.x, u1, 0, 0, 0);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b0.y, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b1.y, s1, 0, 0, 0);
-        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.y, e0.y, u0, 0, 0, 0);
-        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.y, e1.y, u1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.y, e0.y, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.y, e1.y, u1, 0, 0, 0);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b0.z, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b1.z, s1, 0, 0, 0);
-        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.z, e0.z, u0, 0, 0, 0);
-        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.z, e1.z, u1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.z, e0.z, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.z, e1.z, u1, 0, 0, 0);
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b0.w, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b1.w, s1, 0, 0, 0);
-        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.w, e0.w, u0, 0, 0, 0);
-        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c.w, e1.w, u1, 0, 0, 0);
+        u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.w, e0.w, u0, 0, 0, 0);
+        u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.w, e1.w, u1, 0, 0, 0);
       }
       s0 += u0;
       s1 += u1;
-      }
       // s0[r], s1[r]: query row mt*16 + 4*lg + r, keys lr and 16 + lr
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -276,20 +259,20 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnParams p) {
     __syncthreads();                            // K reads and P writes done
 #pragma unroll
     for (int u = 0; u < KV_L; ++u) {            // V^T[d][t]
-      const int t = wave + 4 * u;
+      const int t = wave + NW * u;
       KV[(lane * 4 + 0) * VROW + t] = vr[u].x;
       KV[(lane * 4 + 1) * VROW + t] = vr[u].y;
       KV[(lane * 4 + 2) * VROW + t] = vr[u].z;
       KV[(lane * 4 + 3) * VROW + t] = vr[u].w;
     }
     __syncthreads();
-    // P.V: head-dim tiles 4*wave .. 4*wave+3 of every query tile
+    // P.V: head-dim tiles DT*wave .. DT*wave + DT-1 of every query tile
     for (int mt = 0; mt < MT; ++mt) {
       const float *pa = Ps + (mt * 16 + lr) * PROW + lg * (TC / 4);
       const float4 pa0 = *(const float4 *)pa, pa1 = *(const float4 *)(pa + 4);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int nd = wave * 4 + q;
+      for (int q = 0; q < DT; ++q) {
+        const int nd = wave * DT + q;
         const float *vb = KV + (nd * 16 + lr) * VROW + lg * (TC / 4);
         const float4 vb0 = *(const float4 *)vb, vb1 = *(const float4 *)(vb + 4);
         f32x4_t o = {0.f, 0.f, 0.f, 0.f};
@@ -380,12 +363,14 @@ size_t attn_partial_floats(int NH, int NKV, int max_ctx, int B) {
 
 // Dynamic LDS above 64 KB (B = 16 blocks) needs the attribute; set once per
 // process before any launch (not inside a graph capture).
+int attention_max_group() { return NW_MAX * 16 / CWEN_BMAX; }
+
 int attention_init() {
   static bool done = false;
   if (!done) {
-    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      160 * 1024));
-    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      160 * 1024));
     done = true;
   }
@@ -413,16 +398,17 @@ int attention_launch(const float *qfull, int qfs, const float *kx, const float *
   p.pl = p.pm + (size_t)NKV * p.nchunk * nq;
   p.yh = yh;
   p.rflag = rflag;
-  hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
+  // Every check before the first launch: a block never stops half-way.
   const int nwg = p.nchunk < ATTN_CHUNK_WGS ? p.nchunk : ATTN_CHUNK_WGS;
   const int MT = (nq + 15) / 16;
-  if (MT > 4 * QT_MAX) return CWEN_EINVAL;   // query tiles beyond the waves' registers
+  if (NH % NKV || MT > NW_MAX) return CWEN_EINVAL;   // one 16-query tile per wave
   const size_t lds = ((size_t)MT * 16 * PROW + KV_FLOATS) * sizeof(float);
   if (lds > 160 * 1024) return CWEN_EINVAL;
   int rc;
   if ((rc = attention_init())) return rc;
-  if (MT <= 4) hipLaunchKernelGGL(attn_chunk_kernel<1>, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);
-  else hipLaunchKernelGGL(attn_chunk_kernel<2>, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);
+  hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
+  if (MT <= 4) hipLaunchKernelGGL(attn_chunk_kernel<4>, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);
+  else hipLaunchKernelGGL(attn_chunk_kernel<8>, dim3((unsigned)nwg, (unsigned)NKV), dim3(512), lds, st, p);
   hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)B, (unsigned)NH), dim3(HD), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;

@@ -123,6 +123,9 @@ int check_cfg(const cwen_model_cfg *c) {
   if (c->d_model % Q4_K_ALIGN || c->d_ffn % Q4_K_ALIGN) return CWEN_EINVAL;
   if (c->d_model > 8192) return CWEN_EINVAL;  // <= CWEN_MAX_PARTS row-tile partials of the residual's sum of squares
   if (c->head_dim != 256 || c->n_head <= 0 || c->n_kv_head <= 0 || c->n_head % c->n_kv_head) return CWEN_EINVAL;
+  // Attention takes every block size up to CWEN_BMAX: refused here rather than
+  // part-way through a block.
+  if (c->n_head / c->n_kv_head > attention_max_group()) return CWEN_EINVAL;
   if ((c->n_head * c->head_dim) % Q4_K_ALIGN) return CWEN_EINVAL;
   if (c->gdn_dk != 128 || c->gdn_nkh <= 0 || c->gdn_nvh % c->gdn_nkh || (c->gdn_nvh * 128) % Q4_K_ALIGN)
     return CWEN_EINVAL;
