@@ -20,6 +20,48 @@ constexpr size_t kScratchHalves = (size_t)CWEN_BMAX * CWEN_KMAX;
 constexpr size_t kPartialFloats = (size_t)8 << 20;   // 32 MiB of split-K partials
 constexpr int kCounters = 1 << 16;
 
+// Scratch of the allocation-free entry point, one copy per GPU, held until
+// the process ends: the f16 operand of X and the f16 hidden activations
+// ([CWEN_BMAX][CWEN_STATIC_KMAX] halves each), split-K partials and the
+// split-tile arrival counters, in that order.
+constexpr size_t kStaticHalves = (size_t)CWEN_BMAX * CWEN_STATIC_KMAX;
+constexpr size_t kStaticPartialFloats = (size_t)1 << 20;
+constexpr int kStaticCounters = 4096;
+constexpr size_t kStaticXhOfs = 0;
+constexpr size_t kStaticHhOfs = kStaticXhOfs + kStaticHalves * 2;
+constexpr size_t kStaticPartOfs = kStaticHhOfs + kStaticHalves * 2;
+constexpr size_t kStaticCntOfs = kStaticPartOfs + kStaticPartialFloats * 4;
+constexpr size_t kStaticBytes = kStaticCntOfs + (size_t)kStaticCounters * 4;
+static_assert(kStaticBytes == CWEN_STATIC_SCRATCH_BYTES, "static scratch size");
+__device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+// Device address of `scratch` on each GPU, looked up once per device with
+// that device current (each GPU holds its own copy at its own address).  In
+// host code the array's name is not a device address: only these are passed
+// to kernels.
+constexpr int kMaxDevices = 64;
+unsigned char *g_scratch_dev[kMaxDevices];
+
+__global__ void zero_ints_kernel(int *p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+// Look up this device's scratch address and clear its counters (first
+// context on the device only; `device` is current).
+int static_scratch_init(int device) {
+  if (device >= kMaxDevices) return CWEN_EINVAL;
+  if (g_scratch_dev[device]) return CWEN_OK;
+  unsigned char *ptr = nullptr;
+  CWEN_HIP_TRY(hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch)));
+  if (!ptr) return CWEN_EHIP;
+  hipLaunchKernelGGL(zero_ints_kernel, dim3(16), dim3(256), 0, nullptr, (int *)(ptr + kStaticCntOfs),
+                     kStaticCounters);
+  CWEN_HIP_TRY(hipGetLastError());
+  CWEN_HIP_TRY(hipDeviceSynchronize());
+  g_scratch_dev[device] = ptr;
+  return CWEN_OK;
+}
+
 }  // namespace
 
 int gemv_alloc_q4(cwen_ctx *ctx, int K, int M, cwen_weight **out) {
@@ -105,6 +147,11 @@ int cwen_ctx_create(int device, cwen_ctx **out) {
       hipDeviceSynchronize() != hipSuccess) {
     cwen_ctx_destroy(c);
     return CWEN_EHIP;
+  }
+  const int rs = static_scratch_init(device);
+  if (rs) {
+    cwen_ctx_destroy(c);
+    return rs;
   }
   *out = c;
   return CWEN_OK;
@@ -331,6 +378,35 @@ int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd,
   if ((rc = gemv_launch(ctx, Wgu, 2, 0, GEMV_EPI_SWIGLU, xh, o1, B, st, xh ? nullptr : &x))) return rc;
   GemvOut o2 = {Y, nullptr, nullptr, ys, 1};
   return gemv_launch(ctx, Wd, 1, 0, GEMV_EPI_STORE, ctx->hh, o2, B, st);
+}
+
+int cwen_mlp_block_noalloc(const cwen_weight *Wgu, const cwen_weight *Wd, const float *X, int xs, float *Y,
+                           int ys, int B, void *stream) {
+  if (!Wgu || !Wd || Wgu->ctx != Wd->ctx) return CWEN_EINVAL;
+  cwen_ctx *ctx = Wgu->ctx;
+  int rc;
+  if (Wgu->nside != 2 || Wd->nside != 1 || Wd->ne0 != Wgu->ne1 || Wd->ne1 != Wgu->ne0) return CWEN_EINVAL;
+  if ((rc = check_act(X, xs, Wgu->ne0, B)) || (rc = check_out(Y, ys, Wd->ne1, B))) return rc;
+  if (Wgu->ne0 > CWEN_STATIC_KMAX || Wgu->ne1 > CWEN_STATIC_KMAX) return CWEN_ESCRATCH;
+  if (ctx->device < 0 || ctx->device >= kMaxDevices || !g_scratch_dev[ctx->device]) return CWEN_EINVAL;
+  unsigned char *const base = g_scratch_dev[ctx->device];
+  const GemvScratch scr = {(float *)(base + kStaticPartOfs), kStaticPartialFloats, (int *)(base + kStaticCntOfs),
+                           kStaticCounters};
+  // Both launches' decompositions are checked before the first launch.
+  if (!gemv_grid_fits(Wgu->cfg[1], scr.partials_floats, scr.ncounters) ||
+      !gemv_grid_fits(Wd->cfg[0], scr.partials_floats, scr.ncounters))
+    return CWEN_ESCRATCH;
+  hipStream_t st = (hipStream_t)stream;
+  _Float16 *const xh = (_Float16 *)(base + kStaticXhOfs), *const hh = (_Float16 *)(base + kStaticHhOfs);
+  GemvF32 x = {X, xs};
+  const bool stage_f32 = B <= 4;  // the GEMV converts X while staging (cwen_mlp_block's rule)
+  if (!stage_f32 && (rc = act_to_f16(X, xs, xh, Wgu->ne0, B, st))) return rc;
+  GemvOut o1 = {nullptr, nullptr, hh, 0, 0};
+  if ((rc = gemv_launch(ctx, Wgu, 2, 0, GEMV_EPI_SWIGLU, stage_f32 ? nullptr : xh, o1, B, st,
+                        stage_f32 ? &x : nullptr, nullptr, &scr)))
+    return rc;
+  GemvOut o2 = {Y, nullptr, nullptr, ys, 1};
+  return gemv_launch(ctx, Wd, 1, 0, GEMV_EPI_STORE, hh, o2, B, st, nullptr, nullptr, &scr);
 }
 
 int cwen_head_verify(cwen_ctx *ctx, const cwen_weight *W, const float *X, int xs, int B,

@@ -29,7 +29,7 @@ struct cwen_ctx {
   _Float16 *hh;             // second f16 scratch (FFN hidden) [BMAX][KMAX]
   float *partials;          // split-K partial sums
   size_t partials_floats;
-  int *counters;            // per row-tile arrival counters, zero between launches
+  int *counters;            // per split-tile arrival counters, zero between launches
   int ncounters;
   unsigned long long *amax_keys;  // per-column argmax keys [CWEN_BMAX], zero between launches
   int *amax_cnt;            // argmax arrival counter, zero between launches
@@ -196,14 +196,26 @@ int gemv_alloc_q4(cwen_ctx *ctx, int K, int M, cwen_weight **out);
 int gemv_upload_part(cwen_weight *w, int type, const void *data, const void *scales, int M, int row_off,
                      int side_sel);
 void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w);
+// Split-K scratch of a launch: partial sums and per-split-tile arrival
+// counters (zero between launches; the last arriver of a tile resets its own).
+struct GemvScratch {
+  float *partials;
+  size_t partials_floats;
+  int *counters;
+  int ncounters;
+};
+// Whether a decomposition's split pieces fit the given scratch.
+bool gemv_grid_fits(const GemvGrid &g, size_t partials_floats, int ncounters);
 // Row tiles of a launch over w: the number of ssq partials it writes.
 int gemv_row_tiles(const cwen_weight *w);
 // post (f16 operand only): the operand is w * x with x not yet normalised;
 // each output column c is scaled by 1 / sqrt(sum_p post->ssq[p][c] / K +
 // post->eps), completing the RMSNorm (post->x, post->w unused).
+// scr (nullable) replaces the context's split-K scratch; a decomposition that
+// does not fit it returns CWEN_ESCRATCH before any launch.
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
                 const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvF32 *xf = nullptr,
-                const GemvPost *post = nullptr);
+                const GemvPost *post = nullptr, const GemvScratch *scr = nullptr);
 int act_to_f16(const float *x, int xs, _Float16 *xh, int K, int B, hipStream_t st);
 int argmax_walk_launch(const float *lg, long ls, int V, int B, const ArgmaxOut &a, hipStream_t st);
 

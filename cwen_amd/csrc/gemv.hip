@@ -339,7 +339,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   const int n = lane & 15, g = lane >> 4;
   const bool split = (int)blockIdx.x < p.nsplit;
   const int S = split ? p.S : 1;                   // pieces of this workgroup's row tile
-  const int rt = split ? p.tile0 + (int)blockIdx.x / p.S : (int)blockIdx.x - p.nsplit;
+  const int ti = split ? (int)blockIdx.x / p.S : 0;  // split tile: index of its partials and counter
+  const int rt = split ? p.tile0 + ti : (int)blockIdx.x - p.nsplit;
   const int sp = split ? (int)blockIdx.x % p.S : 0;
   const int st0 = sp * p.rps;
   const int nround = split ? min(p.nst - st0, p.rps) : p.nst;
@@ -606,7 +607,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     uint64_t *part = (uint64_t *)p.part;
 #pragma unroll
     for (int q = 0; q < NSET; ++q) {
-      const size_t base = ((((size_t)rt * WAVES + wave) * NSET + q) * S + sp) * 128 + lane * 2;
+      const size_t base = ((((size_t)ti * WAVES + wave) * NSET + q) * S + sp) * 128 + lane * 2;
       if (cols_on) {
         __hip_atomic_store(part + base, __builtin_bit_cast(uint64_t, (float2){res[q][0], res[q][1]}),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -617,7 +618,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // stores acknowledged
     __builtin_amdgcn_s_barrier();
     if (tid == 0)
-      s_last = __hip_atomic_fetch_add(p.cnt + rt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+      s_last = __hip_atomic_fetch_add(p.cnt + ti, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     if (!s_last) return;
@@ -632,7 +633,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
         uint64_t lo[NSET][KCH], hi[NSET][KCH];
 #pragma unroll
         for (int q = 0; q < NSET; ++q) {
-          const size_t base = ((((size_t)rt * WAVES + wave) * NSET + q) * S) * 128 + lane * 2;
+          const size_t base = ((((size_t)ti * WAVES + wave) * NSET + q) * S) * 128 + lane * 2;
 #pragma unroll
           for (int u = 0; u < KCH; ++u) {
             const size_t k = (size_t)min(k0 + u, S - 1);
@@ -651,7 +652,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
             }
       }
     }
-    if (tid == 0) __hip_atomic_store(p.cnt + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(p.cnt + ti, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   if (p.pss) {
@@ -1127,6 +1128,12 @@ int gemv_repack_part(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, i
   return CWEN_OK;
 }
 
+// Split-K scratch of a decomposition: WAVES x 256 partial floats per piece
+// (one row group per wave) and one arrival counter per split tile.
+bool gemv_grid_fits(const GemvGrid &g, size_t partials_floats, int ncounters) {
+  return g.nsplit == 0 || ((size_t)g.nsplit * WAVES * 256 <= partials_floats && g.nsplit / g.S <= ncounters);
+}
+
 namespace {
 // Estimated length of a launch (microseconds at the 27B FFN shape's rates).
 // Workgroup i runs on CU i mod ncu (dispatch fills every CU's first slot,
@@ -1162,7 +1169,6 @@ double grid_cost(int ncu, int nst, const GemvGrid &c, double extra) {
 // grid_cost) that spread them over the CUs: without that, the CUs that get
 // one whole tile more than the others would set the launch's length.
 GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
-  const size_t per_piece = (size_t)WAVES * 256;  // partial floats per tile and piece
   GemvGrid best = {ntile, 0, 1, nst, 0};
   if (ntile < ctx->ncu) {
     const int target = ctx->wg_per_cu * ctx->ncu;
@@ -1171,7 +1177,7 @@ GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
     int S = std::min(std::max(target / ntile, 1), std::max(nst / 2, 1));
     const int rps = (nst + S - 1) / S;
     S = (nst + rps - 1) / rps;
-    const bool fits = (size_t)ntile * S * per_piece <= ctx->partials_floats && ntile <= ctx->ncounters;
+    const bool fits = gemv_grid_fits(GemvGrid{ntile * S, ntile * S, S, rps, 0}, ctx->partials_floats, ctx->ncounters);
     if (S > 1 && fits) best = {ntile * S, ntile * S, S, rps, 0};
     return best;
   }
@@ -1180,8 +1186,8 @@ GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
   double best_cost = grid_cost(ctx->ncu, nst, best, 0.0);
   for (int s = 2; s <= nst / 2; ++s) {
     const int r = (nst + s - 1) / s, se = (nst + r - 1) / r;
-    if (se != s || (size_t)ntile * se * per_piece > ctx->partials_floats || ntile > ctx->ncounters) continue;
     const GemvGrid part = {rem * se + ntile - rem, rem * se, se, r, ntile - rem};
+    if (se != s || !gemv_grid_fits(part, ctx->partials_floats, ctx->ncounters)) continue;
     const double c = grid_cost(ctx->ncu, nst, part, kSplitEarly);
     if (c < best_cost) {
       best = part;
@@ -1209,7 +1215,7 @@ int gemv_row_tiles(const cwen_weight *w) { return (w->nrg + WAVES * w->rows - 1)
 
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
                 const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvF32 *xf,
-                const GemvPost *post) {
+                const GemvPost *post, const GemvScratch *scr) {
   if (post && (xf || !xh || !post->ssq || post->npart < 1 || post->npart > CWEN_MAX_PARTS)) return CWEN_EINVAL;
   if (xf && (xh || !xf->x || ((uintptr_t)xf->x & 15) || (xf->xs & 3) || (B > 1 && xf->xs < w->ne0)))
     return CWEN_EINVAL;
@@ -1233,13 +1239,14 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   p.eps = post ? post->eps : 0.f;
   p.K = w->ne0;
   p.B = B;
-  p.part = ctx->partials;
-  p.cnt = ctx->counters;
+  p.part = scr ? scr->partials : ctx->partials;
+  p.cnt = scr ? scr->counters : ctx->counters;
   p.out = out;
   const int R = w->rows;
   const int rpw = nsides == 2 ? WAVES / 2 : WAVES;  // row groups per row tile
   const int ntile = (w->nrg + rpw * R - 1) / (rpw * R);
   if (epi == GEMV_EPI_ARGMAX) cfg = {ntile, 0, 1, w->nst, 0};  // final row values in one workgroup
+  if (scr && !gemv_grid_fits(cfg, scr->partials_floats, scr->ncounters)) return CWEN_ESCRATCH;
   p.nsplit = cfg.nsplit;
   p.S = cfg.S;
   p.rps = cfg.rps;

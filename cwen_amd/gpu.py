@@ -35,6 +35,7 @@ SIGNATURES = [
     ("cwen_gemvb_pair", _I, [_VP, _VP, _VP, _I, _VP, _VP, _I, _I, _VP]),
     ("cwen_gemvb_swiglu", _I, [_VP, _VP, _VP, _I, _VP, _I, _I, _VP]),
     ("cwen_mlp_block", _I, [_VP, _VP, _VP, _VP, _I, _VP, _I, _I, _VP]),
+    ("cwen_mlp_block_noalloc", _I, [_VP, _VP, _VP, _I, _VP, _I, _I, _VP]),
     ("cwen_act_to_f16", _I, [_VP, _VP, _I, _VP, _I, _I, _VP]),
     ("cwen_gemvb_f16", _I, [_VP, _VP, _I, _VP, _VP, _I, _VP, _I, _I, _VP]),
     ("cwen_gemvb_swiglu_f16", _I, [_VP, _VP, _VP, _VP, _I, _VP, _I, _VP]),
@@ -227,6 +228,16 @@ def mlp_block(ctx: Context, Wgu: Weight, Wd: Weight, X, Y, B: int, xs: int | Non
     ys = Wd.M if ys is None else ys
     check("cwen_mlp_block", lib().cwen_mlp_block(ctx.h, Wgu.h, Wd.h, _ptr(X), xs, _ptr(Y), ys, B,
                                                  _stream(stream)))
+
+
+def mlp_block_noalloc(Wgu: Weight, Wd: Weight, X, Y, B: int, xs: int | None = None,
+                      ys: int | None = None, stream=None) -> None:
+    """mlp_block on the library's static per-GPU scratch (no allocation, no
+    context scratch); raises CwenError(ESCRATCH) beyond its limits."""
+    xs = Wgu.K if xs is None else xs
+    ys = Wd.M if ys is None else ys
+    check("cwen_mlp_block_noalloc", lib().cwen_mlp_block_noalloc(Wgu.h, Wd.h, _ptr(X), xs, _ptr(Y), ys, B,
+                                                                 _stream(stream)))
 
 
 def act_to_f16(ctx: Context, X, Xh, K: int, B: int, xs: int | None = None, stream=None) -> None:

@@ -119,6 +119,26 @@ int cwen_gemvb_swiglu(cwen_ctx *ctx, const cwen_weight *W, const float *X, int x
 int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd,
                    const float *X, int xs, float *Y, int ys, int B, void *stream);
 
+/* cwen_mlp_block without any allocation and without the context's scratch:
+ * the same kernels and launch decomposition, so Y is bit-identical to
+ * cwen_mlp_block's.  No counterpart in the reference: it is for callers that
+ * cannot allocate or touch a context's shared buffers (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Its scratch
+ * (the f16 operands of X and of the hidden activations, split-K partials and
+ * arrival counters) is one static device array of CWEN_STATIC_SCRATCH_BYTES
+ * per GPU, held until the process ends; its address on a device is looked up
+ * when the first context is created there (cwen_ctx_create), so Wgu and Wd
+ * must come from a context.  Limits: d_model and d_ffn (Wgu's ne0 and ne1)
+ * at most CWEN_STATIC_KMAX, and launch decompositions whose split-K pieces
+ * fit the array (every 27B-shape FFN does); beyond them it returns
+ * CWEN_ESCRATCH before any launch.  Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (any streams, any contexts) race and
+ * must be serialised by the caller. */
+#define CWEN_STATIC_KMAX 32768
+#define CWEN_STATIC_SCRATCH_BYTES (2u * 2u * CWEN_BMAX * CWEN_STATIC_KMAX + 4u * 1048576u + 4u * 4096u)
+int cwen_mlp_block_noalloc(const cwen_weight *Wgu, const cwen_weight *Wd, const float *X, int xs, float *Y,
+                           int ys, int B, void *stream);
+
 /* LM head + acceptance of one verify block, on the device.  logits_b = W . X_b
  * for b < B (W: the output head, M = vocab rows, any uploaded single-sided
  * type), then the per-column argmax -- argmax_of (run.c:2647-2668): the first
