@@ -283,7 +283,7 @@ __device__ void argmax_finish(const unsigned long long *key, int B, const Argmax
 }
 
 struct GemvParams {
-  const uint8_t *w;    // super-tiled weights
+  const uint8_t *w;    // super-tiled weights, round-major: super-tile (st, rg, side) at ((st*nrg + rg)*nsw + side)
   uint32_t wbytes;     // bytes of the tiled weights (buffer range)
   int nsw;             // sides stored per super-tile position (1 or 2)
   int side0;           // first side computed (NS == 1)
@@ -303,7 +303,7 @@ struct GemvParams {
   float eps;
   int K, B;
   float *part;         // split-K partials
-  int *cnt;            // per row-tile arrival counters (zero between launches)
+  int *cnt;            // per split-tile arrival counters (zero between launches)
   GemvOut out;
 };
 
@@ -317,24 +317,30 @@ __device__ __forceinline__ uint4 cvt8(const uint4 (&x)[2]) {
 }
 
 // FMT: weight format.  NS: sides of an interleaved pair computed (2: both;
-// the two waves of a wave pair take sides 0 and 1 of the same row groups and
-// combine them through LDS).  R: row groups per wave; each wave carries R
-// weight streams.  EPI: epilogue.  CB: activation columns staged (4, 8 or
-// 16; >= B).  XN: f32 activations, converted to f16 while staging.
-template <int FMT, int NS, int R, int EPI, int CB, bool XN>
+// the two waves of a wave pair take sides 0 and 1 of the same row group and
+// combine them through LDS).  EPI: epilogue.  CB: activation columns staged
+// (4, 8 or 16; >= B).  XN: f32 activations, converted to f16 while staging.
+template <int FMT, int NS, int EPI, int CB, bool XN>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   using F = Fmt<FMT>;
-  constexpr int NSET = R;
-  constexpr int RPW = NS == 2 ? WAVES / 2 : WAVES;  // row-group slots per workgroup
-  constexpr int XL = CB / WAVES;            // staging loads per wave per round
+  constexpr int SPW = WAVES;                 // weight streams per workgroup (one per wave)
+  constexpr int RPW = NS == 2 ? SPW / 2 : SPW;  // row groups per workgroup
+  constexpr int TW = TILES;                  // tiles of a super-tile per wave
+  constexpr int XL = CB / WAVES;             // staging loads per lane per round
   constexpr int TV = F::TV;
-  __shared__ uint4 act[2][16 * 64];         // [buf][column c][unit u ^ c], f16 x 8 per unit
+  // One round of weights in flight per wave: round rd + 1 is requested while
+  // round rd is computed (measured: two rounds in flight were slower).
+  constexpr int PD = 1;
+  // The main loop's double-buffered activation chunks; the epilogue reuses
+  // the same LDS for its exchanges, so a workgroup holds CB * 2 KB.
+  __shared__ uint4 act[2][CB * 64];          // [buf][column c][unit u ^ c], f16 x 8 per unit
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
   // Wave index as a scalar: loop bounds and addresses are then provably
   // wave-uniform, which keeps the loop's load-counter waits exact.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ws = wave;                             // stream of the workgroup
   const int lane = tid & 63;
   const int n = lane & 15, g = lane >> 4;
   const bool split = (int)blockIdx.x < p.nsplit;
@@ -347,32 +353,31 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 
   // Post-scale: the producer's partial sums of squares of every staged
   // column, loaded first, so that waiting for them waits for nothing else
-  // (see psc below); ssq has CWEN_MAX_PARTS rows, so the loads need no guard.
-  float pa[CB], pb[CB];
+  // (see psc below); ssq has CWEN_MAX_PARTS = 128 rows, so the loads need no
+  // guard.
+  float pp[2][CB];
   if (p.pss) {
 #pragma unroll
-    for (int c = 0; c < CB; ++c) {
-      pa[c] = p.pss[lane * CWEN_BMAX + c];
-      pb[c] = p.pss[(lane + 64) * CWEN_BMAX + c];
-    }
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int c = 0; c < CB; ++c) pp[j][c] = p.pss[(lane + 64 * j) * CWEN_BMAX + c];
   }
   __builtin_amdgcn_sched_barrier(0);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.wbytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(XN ? (const void *)p.xf : (const void *)p.xh, p.xbytes);
 
-  // Weight streams of this wave: stream r is row group rgs[r], side `side`.
-  const uint32_t sstride = (uint32_t)p.nsw * F::ST_BYTES;
-  const int side = NS == 2 ? (wave & 1) : p.side0;
-  uint32_t wofs[NSET];
-  int rgs[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    rgs[r] = (rt * RPW + (NS == 2 ? wave >> 1 : wave)) * R + r;
-    const int rgc = rgs[r] < p.nrg ? rgs[r] : p.nrg - 1;  // idle streams read a valid tile
-    wofs[r] = (((uint32_t)rgc * p.nst + st0) * p.nsw + side) * F::ST_BYTES;
-  }
+  // This wave's weight stream: row group rg, side `side`, super-tiles st0 ...
+  // (round-major: consecutive rounds of a stream are nrg * nsw super-tiles
+  // apart, so at any moment the launch reads one contiguous region).
+  const uint32_t sstride = (uint32_t)p.nrg * p.nsw * F::ST_BYTES;
+  const int side = NS == 2 ? (ws & 1) : p.side0;
+  const int slot = NS == 2 ? ws >> 1 : ws;         // row-group slot of the workgroup
+  const int rg = rt * RPW + slot;
+  const int rgc = rg < p.nrg ? rg : p.nrg - 1;     // idle streams read a valid tile
+  const uint32_t wofs = (((uint32_t)st0 * p.nrg + rgc) * p.nsw + side) * F::ST_BYTES;
   constexpr bool DM = FMT == GEMV_Q41 || FMT == GEMV_Q5K;  // per-block (scale, offset) pairs
   const uint32_t lq = lane * 16, ls = F::SC_OFS + lane * (DM ? 16 : 8);
+  constexpr int jb = 0;                           // first tile of this wave
 
   // Activation staging: this wave copies columns c = wave + WAVES*i; lane
   // copies f16 unit `lane` (K elements 8*lane .. 8*lane+7) of the column's
@@ -388,33 +393,28 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     xslot[i] = c * 64 + (lane ^ c);
   }
 
-  // Loads of one round's weight data.  Tile u, vector v of a stream.
-  auto tile_ofs = [&](int u, int v) -> uint32_t {
-    return FMT == GEMV_Q8 ? lq + u * 2048 + v * 1024 : lq + u * 1024;
+  // Loads of one round's weight data: tile jb + t, vector v of the stream.
+  auto tile_ofs = [&](int t, int v) -> uint32_t {
+    return FMT == GEMV_Q8 ? lq + (jb + t) * 2048 + v * 1024 : lq + (jb + t) * 1024;
   };
 
   uint4 xs[XL][XN ? 2 : 1];
-  uint4 wq[TILES][NSET][TV];
-  // Scales of a round: 4 f16 (one per tile), or for Q4_1 4 (d, m) pairs.
+  uint4 wq[PD][TW][TV];
+  // Scales of a round: 4 f16 (one per tile), or for Q4_1 / Q5_K 4 pairs.
   using ScT = std::conditional_t<DM, uint4, uint2>;
-  ScT sc[NSET];
+  ScT sc[PD];
   auto sc_load = [&](uint32_t soff) __attribute__((always_inline)) -> ScT {
     if constexpr (DM) return bload16(wr, ls, soff);
     else return bload8(wr, ls, soff);
   };
-  uint4 h5[NSET];             // Q5_K: fifth bits of the round's 4 tiles (one dword each)
+  uint4 h5[PD];               // Q5_K: fifth bits of the round's 4 tiles (one dword each)
   auto h5_load = [&](uint32_t soff) __attribute__((always_inline)) -> uint4 {
     if constexpr (FMT == GEMV_Q5K) return bload16(wr, F::HI_OFS + lq, soff);
     else return make_uint4(0u, 0u, 0u, 0u);
   };
-  uint32_t dq[NSET];          // Q6_K: f16 d of the round's two super-blocks
-  uint4 hq[2][NSET];          // Q6_K: high bits of tile pairs (0,1) and (2,3)
-#pragma unroll
-  for (int q = 0; q < NSET; ++q) {
-    sc[q] = sc_load(wofs[q]);
-    h5[q] = h5_load(wofs[q]);
-    if constexpr (FMT == GEMV_Q6K) dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q], 0);
-  }
+  uint32_t dq[PD] = {};       // Q6_K: f16 d of the round's two super-blocks
+  constexpr int NHQ = (TW + 1) / 2;  // Q6_K: high-bit tile pairs of this wave
+  uint4 hq[PD][NHQ];          // Q6_K: high bits of tile pairs (jb, jb+1) ...
   auto stage_load = [&](uint32_t soff) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
@@ -424,34 +424,36 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   };
   stage_load(0);
 #pragma unroll
-  for (int j = 0; j < TILES; ++j) {
+  for (int k = 0; k < PD; ++k) {
+    const uint32_t ok = wofs + (uint32_t)(k < nround ? k : nround - 1) * sstride;
+    sc[k] = sc_load(ok);
+    h5[k] = h5_load(ok);
+    if constexpr (FMT == GEMV_Q6K) dq[k] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, ok, 0);
 #pragma unroll
-    for (int q = 0; q < NSET; ++q)
+    for (int t = 0; t < TW; ++t) {
 #pragma unroll
-      for (int v = 0; v < TV; ++v) wq[j][q][v] = bload16(wr, tile_ofs(j, v), wofs[q]);
-    if constexpr (FMT == GEMV_Q6K) {
-      if (j & 1) {
-#pragma unroll
-        for (int q = 0; q < NSET; ++q) hq[j >> 1][q] = bload16(wr, F::HI_OFS + (j >> 1) * 1024 + lq, wofs[q]);
+      for (int v = 0; v < TV; ++v) wq[k][t][v] = bload16(wr, tile_ofs(t, v), ok);
+      if constexpr (FMT == GEMV_Q6K) {
+        if (t & 1) hq[k][t >> 1] = bload16(wr, F::HI_OFS + ((jb + t) >> 1) * 1024 + lq, ok);
       }
+      __builtin_amdgcn_sched_barrier(0);  // issue the ring in slot order
     }
-    __builtin_amdgcn_sched_barrier(0);  // issue the ring in slot order
   }
   // Post-scale: the scales of this lane's output columns 4g .. 4g+3, while
   // the first round's weights are in flight.  Lane p adds partials p and
-  // p + 64, then one DPP tree over the wave: a fixed order, so every
-  // workgroup and every block size gets the same scale for a column.
-  // Every column index is a compile-time constant and nothing branches per
-  // column (a private array indexed at run time would move to LDS; a uniform
-  // branch per column reloads kernel arguments).
+  // p + 64 in that order, then one DPP tree over the wave: a
+  // fixed order, so every workgroup and every block size gets the same scale
+  // for a column.  Every column index is a compile-time constant and nothing
+  // branches per column (a private array indexed at run time would move to
+  // LDS; a uniform branch per column reloads kernel arguments).
   float psc[4] = {1.f, 1.f, 1.f, 1.f};
   if (p.pss) {
     const float kf = (float)p.K, eps = p.eps;
     const int nb = p.B, np = p.pnpart;
 #pragma unroll
     for (int c = 0; c < CB; ++c) {
-      float v = lane < np ? pa[c] : 0.f;
-      if (lane + 64 < np) v += pb[c];
+      float v = lane < np ? pp[0][c] : 0.f;
+      if (lane + 64 < np) v += pp[1][c];
       const float sc1 = 1.f / sqrtf(sum64(v) / kf + eps);
       psc[c & 3] = ((c >> 2) == g && c < nb) ? sc1 : psc[c & 3];
     }
@@ -467,122 +469,110 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   lds_barrier();
 
   const Unpack uc = unpack_consts();
-  floatx4_t acc[NSET][2];
-#pragma unroll
-  for (int q = 0; q < NSET; ++q) acc[q][0] = acc[q][1] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
-  // LDS unit of MFMA m of tile 0 for this lane (column n, K run 4g + m); tile
-  // j adds 16 units, which stay clear of the XOR (n < 16).
+  floatx4_t acc[2];
+  acc[0] = acc[1] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+  // LDS unit of MFMA m of this wave's first tile for this lane (column n, K
+  // run 4g + m); tile jb + t adds 16 (jb + t) units, which stay clear of the
+  // XOR (n < 16).
   int aslot[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) aslot[m] = n * 64 + ((4 * g + m) ^ n);
+  for (int m = 0; m < 4; ++m) aslot[m] = n * 64 + ((4 * g + m) ^ n) + 16 * jb;
 
-  // One round = one super-tile per stream.  The LDS buffer index is a
+  // One round = one super-tile of the stream.  The LDS buffer index is a
   // template constant (the loop is unrolled by two), so every LDS address is
   // a lane base plus an immediate.
   auto round = [&](int rd, auto cur_c) __attribute__((always_inline)) {
     constexpr int cur = decltype(cur_c)::value;
-    // Next round's super-tile (the last round re-reads its own, harmlessly).
+    // Next round's staging and the weights of round rd + PD (the last rounds
+    // re-read the last super-tile, harmlessly).
     const uint32_t nr = (uint32_t)(rd + 1 < nround ? rd + 1 : rd);
-    // Scales of this round: dd[q][tile][half] (Q4_0 / Q8_0: one per block,
+    const uint32_t nw = (uint32_t)(rd + PD < nround ? rd + PD : nround - 1);
+    const ScT &scc = sc[cur % PD];
+    const uint32_t dqc = dq[cur % PD];
+    // Scales of this round's tiles: dd[t][half] (Q4_0 / Q8_0: one per block,
     // both halves equal; Q6_K: one per 16-weight sub-block).
-    half2_t dd[NSET][TILES][2];
+    half2_t dd[TW][2];
 #pragma unroll
-    for (int q = 0; q < NSET; ++q) {
+    for (int t = 0; t < TW; ++t) {
       if constexpr (FMT == GEMV_Q6K) {
         // sub-scale (exact in f16) * d, rounded once to f16
-        const half2_t d0 = bcast_half(dq[q], false), d1 = bcast_half(dq[q], true);
-#pragma unroll
-        for (int u = 0; u < TILES; ++u) {
-          const half2_t s2 = i8pair(u < 2 ? sc[q].x : sc[q].y, uc.magic, u & 1);
-          const half2_t ds = s2 * (u < 2 ? d0 : d1);
-          dd[q][u][0] = (half2_t){ds[0], ds[0]};
-          dd[q][u][1] = (half2_t){ds[1], ds[1]};
-        }
+        const bool lo2 = t < 2;   // tiles 0-1: first super-block
+        const uint32_t sw = lo2 ? scc.x : scc.y;
+        const half2_t s2 = i8pair(sw, uc.magic, t & 1);
+        const half2_t ds = s2 * bcast_half(dqc, !lo2);
+        dd[t][0] = (half2_t){ds[0], ds[0]};
+        dd[t][1] = (half2_t){ds[1], ds[1]};
+      } else if constexpr (DM) {  // dd[t][0] = scale, dd[t][1] = offset
+        const uint32_t w = t == 0 ? scc.x : t == 1 ? scc.y : t == 2 ? scc.z : scc.w;
+        dd[t][0] = bcast_half(w, false);
+        dd[t][1] = bcast_half(w, true);
       } else {
-        if constexpr (DM) {  // dd[q][u][0] = scale, dd[q][u][1] = offset
-          const uint32_t w4[4] = {sc[q].x, sc[q].y, sc[q].z, sc[q].w};
-#pragma unroll
-          for (int u = 0; u < TILES; ++u) {
-            dd[q][u][0] = bcast_half(w4[u], false);
-            dd[q][u][1] = bcast_half(w4[u], true);
-          }
-        } else {
-          dd[q][0][0] = dd[q][0][1] = bcast_half(sc[q].x, false);
-          dd[q][1][0] = dd[q][1][1] = bcast_half(sc[q].x, true);
-          dd[q][2][0] = dd[q][2][1] = bcast_half(sc[q].y, false);
-          dd[q][3][0] = dd[q][3][1] = bcast_half(sc[q].y, true);
-        }
+        const uint32_t w = t < 2 ? scc.x : scc.y;
+        dd[t][0] = dd[t][1] = bcast_half(w, (t & 1) != 0);
       }
     }
-    uint4 h5c[NSET];  // Q5_K: this round's fifth bits (h5 is reloaded for the next)
-#pragma unroll
-    for (int q = 0; q < NSET; ++q) {
-      h5c[q] = h5[q];
-      sc[q] = sc_load(wofs[q] + nr * sstride);
-      if constexpr (FMT == GEMV_Q5K) h5[q] = h5_load(wofs[q] + nr * sstride);
-      if constexpr (FMT == GEMV_Q6K)
-        dq[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs[q] + nr * sstride, 0);
-    }
+    const uint4 h5c = h5[cur % PD];  // Q5_K: this round's fifth bits (the set is reloaded for round rd + PD)
+    sc[cur % PD] = sc_load(wofs + nw * sstride);
+    if constexpr (FMT == GEMV_Q5K) h5[cur % PD] = h5_load(wofs + nw * sstride);
+    if constexpr (FMT == GEMV_Q6K) dq[cur % PD] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs + nw * sstride, 0);
     stage_load(nr * xround);
+    // LDS operands one tile ahead of their MFMAs: tile t + 1's reads are in
+    // flight while tile t's products issue.
+    half8_t an[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) an[m] = __builtin_bit_cast(half8_t, act[cur][aslot[m]]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < TILES; ++j) {
-      half8_t b[NSET][4];
-#pragma unroll
-      for (int q = 0; q < NSET; ++q) {
-        if constexpr (FMT == GEMV_Q4) {
-          b[q][0] = unpack8_q4(wq[j][q][0].x, uc, dd[q][j][0]);
-          b[q][1] = unpack8_q4(wq[j][q][0].y, uc, dd[q][j][0]);
-          b[q][2] = unpack8_q4(wq[j][q][0].z, uc, dd[q][j][0]);
-          b[q][3] = unpack8_q4(wq[j][q][0].w, uc, dd[q][j][0]);
-        } else if constexpr (FMT == GEMV_Q5K) {
-          const uint32_t h = j == 0 ? h5c[q].x : j == 1 ? h5c[q].y : j == 2 ? h5c[q].z : h5c[q].w;
-          const half2_t d5 = dd[q][j][0], m5 = dd[q][j][1];
-          b[q][0] = unpack8_q5(wq[j][q][0].x, h, h >> 8, h << 8, uc, d5, m5);
-          b[q][1] = unpack8_q5(wq[j][q][0].y, h >> 1, h >> 9, h << 7, uc, d5, m5);
-          b[q][2] = unpack8_q5(wq[j][q][0].z, h >> 2, h >> 10, h << 6, uc, d5, m5);
-          b[q][3] = unpack8_q5(wq[j][q][0].w, h >> 3, h >> 11, h << 5, uc, d5, m5);
-        } else if constexpr (FMT == GEMV_Q41) {
-          b[q][0] = unpack8_q41(wq[j][q][0].x, uc, dd[q][j][0], dd[q][j][1]);
-          b[q][1] = unpack8_q41(wq[j][q][0].y, uc, dd[q][j][0], dd[q][j][1]);
-          b[q][2] = unpack8_q41(wq[j][q][0].z, uc, dd[q][j][0], dd[q][j][1]);
-          b[q][3] = unpack8_q41(wq[j][q][0].w, uc, dd[q][j][0], dd[q][j][1]);
-        } else if constexpr (FMT == GEMV_Q6K) {
-          const uint4 &h4 = hq[j >> 1][q];
-          const uint32_t ha = (j & 1) ? h4.z : h4.x;   // runs 0, 1
-          const uint32_t hb = (j & 1) ? h4.w : h4.y;   // runs 2, 3
-          b[q][0] = unpack8_q6(wq[j][q][0].x, ha, uc, dd[q][j][0]);
-          b[q][1] = unpack8_q6(wq[j][q][0].y, rotl8(ha), uc, dd[q][j][0]);
-          b[q][2] = unpack8_q6(wq[j][q][0].z, hb, uc, dd[q][j][1]);
-          b[q][3] = unpack8_q6(wq[j][q][0].w, rotl8(hb), uc, dd[q][j][1]);
-        } else {
-          b[q][0] = unpack8_q8(wq[j][q][0].x, wq[j][q][0].y, uc.magic, dd[q][j][0]);
-          b[q][1] = unpack8_q8(wq[j][q][0].z, wq[j][q][0].w, uc.magic, dd[q][j][0]);
-          b[q][2] = unpack8_q8(wq[j][q][1].x, wq[j][q][1].y, uc.magic, dd[q][j][0]);
-          b[q][3] = unpack8_q8(wq[j][q][1].z, wq[j][q][1].w, uc.magic, dd[q][j][0]);
-        }
+    for (int t = 0; t < TW; ++t) {
+      half8_t b[4];
+      if constexpr (FMT == GEMV_Q4) {
+        b[0] = unpack8_q4(wq[cur % PD][t][0].x, uc, dd[t][0]);
+        b[1] = unpack8_q4(wq[cur % PD][t][0].y, uc, dd[t][0]);
+        b[2] = unpack8_q4(wq[cur % PD][t][0].z, uc, dd[t][0]);
+        b[3] = unpack8_q4(wq[cur % PD][t][0].w, uc, dd[t][0]);
+      } else if constexpr (FMT == GEMV_Q5K) {
+        const uint32_t h = t == 0 ? h5c.x : t == 1 ? h5c.y : t == 2 ? h5c.z : h5c.w;
+        const half2_t d5 = dd[t][0], m5 = dd[t][1];
+        b[0] = unpack8_q5(wq[cur % PD][t][0].x, h, h >> 8, h << 8, uc, d5, m5);
+        b[1] = unpack8_q5(wq[cur % PD][t][0].y, h >> 1, h >> 9, h << 7, uc, d5, m5);
+        b[2] = unpack8_q5(wq[cur % PD][t][0].z, h >> 2, h >> 10, h << 6, uc, d5, m5);
+        b[3] = unpack8_q5(wq[cur % PD][t][0].w, h >> 3, h >> 11, h << 5, uc, d5, m5);
+      } else if constexpr (FMT == GEMV_Q41) {
+        b[0] = unpack8_q41(wq[cur % PD][t][0].x, uc, dd[t][0], dd[t][1]);
+        b[1] = unpack8_q41(wq[cur % PD][t][0].y, uc, dd[t][0], dd[t][1]);
+        b[2] = unpack8_q41(wq[cur % PD][t][0].z, uc, dd[t][0], dd[t][1]);
+        b[3] = unpack8_q41(wq[cur % PD][t][0].w, uc, dd[t][0], dd[t][1]);
+      } else if constexpr (FMT == GEMV_Q6K) {
+        const uint4 &h4 = hq[cur % PD][t >> 1];
+        const uint32_t ha = (t & 1) ? h4.z : h4.x;   // runs 0, 1
+        const uint32_t hb = (t & 1) ? h4.w : h4.y;   // runs 2, 3
+        b[0] = unpack8_q6(wq[cur % PD][t][0].x, ha, uc, dd[t][0]);
+        b[1] = unpack8_q6(wq[cur % PD][t][0].y, rotl8(ha), uc, dd[t][0]);
+        b[2] = unpack8_q6(wq[cur % PD][t][0].z, hb, uc, dd[t][1]);
+        b[3] = unpack8_q6(wq[cur % PD][t][0].w, rotl8(hb), uc, dd[t][1]);
+      } else {
+        b[0] = unpack8_q8(wq[cur % PD][t][0].x, wq[cur % PD][t][0].y, uc.magic, dd[t][0]);
+        b[1] = unpack8_q8(wq[cur % PD][t][0].z, wq[cur % PD][t][0].w, uc.magic, dd[t][0]);
+        b[2] = unpack8_q8(wq[cur % PD][t][1].x, wq[cur % PD][t][1].y, uc.magic, dd[t][0]);
+        b[3] = unpack8_q8(wq[cur % PD][t][1].z, wq[cur % PD][t][1].w, uc.magic, dd[t][0]);
       }
       // Refill the slots once their registers are consumed, so the loads
       // land in the same registers (no loop-carried copies, no counter drain).
 #pragma unroll
-      for (int q = 0; q < NSET; ++q)
-#pragma unroll
-        for (int v = 0; v < TV; ++v) wq[j][q][v] = bload16(wr, tile_ofs(j, v), wofs[q] + nr * sstride);
+      for (int v = 0; v < TV; ++v) wq[cur % PD][t][v] = bload16(wr, tile_ofs(t, v), wofs + nw * sstride);
       if constexpr (FMT == GEMV_Q6K) {
-        if (j & 1) {
-#pragma unroll
-          for (int q = 0; q < NSET; ++q)
-            hq[j >> 1][q] = bload16(wr, F::HI_OFS + (j >> 1) * 1024 + lq, wofs[q] + nr * sstride);
-        }
+        if (t & 1) hq[cur % PD][t >> 1] = bload16(wr, F::HI_OFS + ((jb + t) >> 1) * 1024 + lq, wofs + nw * sstride);
       }
       half8_t a[4];
 #pragma unroll
-      for (int m = 0; m < 4; ++m) a[m] = __builtin_bit_cast(half8_t, act[cur][aslot[m] + 16 * j]);
+      for (int m = 0; m < 4; ++m) a[m] = an[m];
+      if (t + 1 < TW) {
 #pragma unroll
-      for (int q = 0; q < NSET; ++q)
+        for (int m = 0; m < 4; ++m) an[m] = __builtin_bit_cast(half8_t, act[cur][aslot[m] + 16 * (t + 1)]);
+      }
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          acc[q][m & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b[q][m], acc[q][m & 1], 0, 0, 0);
+      for (int m = 0; m < 4; ++m)
+        acc[m & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b[m], acc[m & 1], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);  // keep slots in issue order
     }
     stage_store(act[cur ^ 1]);
@@ -595,25 +585,23 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   }
   if (rd < nround) round(rd, std::integral_constant<int, 0>{});
 
-  floatx4_t res[NSET];
-#pragma unroll
-  for (int q = 0; q < NSET; ++q) res[q] = acc[q][0] + acc[q][1];
+  floatx4_t res = acc[0] + acc[1];
+  // The epilogue's exchanges reuse the activation buffers (the main loop's
+  // last barrier has passed).
+  constexpr bool carry = true;
 
   if (EPI != GEMV_EPI_ARGMAX && S > 1) {
     // Publish this split's partials.  Agent-scope atomic stores reach the
     // device coherence point; the wait makes them complete before the
     // counter bump, and the last arriver reads them the same way.
-    const bool cols_on = g * 4 < p.B;
+    const bool cols_on = carry && g * 4 < p.B;
     uint64_t *part = (uint64_t *)p.part;
-#pragma unroll
-    for (int q = 0; q < NSET; ++q) {
-      const size_t base = ((((size_t)ti * WAVES + wave) * NSET + q) * S + sp) * 128 + lane * 2;
-      if (cols_on) {
-        __hip_atomic_store(part + base, __builtin_bit_cast(uint64_t, (float2){res[q][0], res[q][1]}),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(part + base + 1, __builtin_bit_cast(uint64_t, (float2){res[q][2], res[q][3]}),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+    const size_t base = (((size_t)ti * SPW + ws) * S + sp) * 128 + lane * 2;
+    if (cols_on) {
+      __hip_atomic_store(part + base, __builtin_bit_cast(uint64_t, (float2){res[0], res[1]}), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(part + base + 1, __builtin_bit_cast(uint64_t, (float2){res[2], res[3]}), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // stores acknowledged
     __builtin_amdgcn_s_barrier();
@@ -621,35 +609,29 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       s_last = __hip_atomic_fetch_add(p.cnt + ti, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    if (!s_last) return;
+    if (!s_last) return;   // workgroup-uniform
     // Sum the splits in split order.  The loads of a chunk of KCH splits are
     // all issued before the first is consumed, so the reduction costs one
     // memory round trip per chunk, not one per split.
     constexpr int KCH = 8;
-#pragma unroll
-    for (int q = 0; q < NSET; ++q) res[q] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    res = (floatx4_t){0.f, 0.f, 0.f, 0.f};
     if (cols_on) {
+      const size_t b0 = (((size_t)ti * SPW + ws) * S) * 128 + lane * 2;
       for (int k0 = 0; k0 < S; k0 += KCH) {
-        uint64_t lo[NSET][KCH], hi[NSET][KCH];
+        uint64_t lo[KCH], hi[KCH];
 #pragma unroll
-        for (int q = 0; q < NSET; ++q) {
-          const size_t base = ((((size_t)ti * WAVES + wave) * NSET + q) * S) * 128 + lane * 2;
-#pragma unroll
-          for (int u = 0; u < KCH; ++u) {
-            const size_t k = (size_t)min(k0 + u, S - 1);
-            lo[q][u] = __hip_atomic_load(part + base + k * 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            hi[q][u] = __hip_atomic_load(part + base + k * 128 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
+        for (int u = 0; u < KCH; ++u) {
+          const size_t k = (size_t)min(k0 + u, S - 1);
+          lo[u] = __hip_atomic_load(part + b0 + k * 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          hi[u] = __hip_atomic_load(part + b0 + k * 128 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
 #pragma unroll
-        for (int q = 0; q < NSET; ++q)
-#pragma unroll
-          for (int u = 0; u < KCH; ++u)
-            if (k0 + u < S) {
-              const float2 a = __builtin_bit_cast(float2, lo[q][u]);
-              const float2 b = __builtin_bit_cast(float2, hi[q][u]);
-              res[q] += (floatx4_t){a.x, a.y, b.x, b.y};
-            }
+        for (int u = 0; u < KCH; ++u)
+          if (k0 + u < S) {
+            const float2 a = __builtin_bit_cast(float2, lo[u]);
+            const float2 b = __builtin_bit_cast(float2, hi[u]);
+            res += (floatx4_t){a.x, a.y, b.x, b.y};
+          }
       }
     }
     if (tid == 0) __hip_atomic_store(p.cnt + ti, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -657,26 +639,22 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 
   if (p.pss) {
 #pragma unroll
-    for (int q = 0; q < NSET; ++q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) res[q][e] *= psc[e];
+    for (int e = 0; e < 4; ++e) res[e] *= psc[e];
   }
   const GemvOut &o = p.out;
+  const int row = rg * Q4_ROWS + n;
+  const bool row_ok = carry && rg < p.nrg && row < p.M;
   if constexpr (EPI == GEMV_EPI_ARGMAX) {
     // Logits (optional), then the per-column argmax over this workgroup's
-    // rows: lane (g, n) holds row n of each row group for columns 4g..4g+3.
-    __shared__ unsigned long long s_key[WAVES][16];
+    // rows: lane (g, n) holds row n of its row group for columns 4g..4g+3.
+    unsigned long long *const s_key = (unsigned long long *)&act[1][0];   // [SPW][16]
     unsigned long long best[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = rgs[r] * Q4_ROWS + n;
-      if (rgs[r] >= p.nrg || row >= p.M) continue;
+    if (row_ok) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int c = g * 4 + e;
-        if (c < p.B && o.y) o.y[(size_t)c * o.ys + row] = res[r][e];
-        const unsigned long long k = amax_key(res[r][e], row);
-        best[e] = k > best[e] ? k : best[e];
+        if (c < p.B && o.y) o.y[(size_t)c * o.ys + row] = res[e];
+        best[e] = amax_key(res[e], row);
       }
     }
 #pragma unroll
@@ -687,16 +665,16 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
         best[e] = other > best[e] ? other : best[e];
       }
     }
-    if (n == 0) {
+    if (carry && n == 0) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s_key[wave][g * 4 + e] = best[e];
+      for (int e = 0; e < 4; ++e) s_key[ws * 16 + g * 4 + e] = best[e];
     }
     __syncthreads();
-    __shared__ unsigned long long s_col[16];
+    unsigned long long *const s_col = s_key + SPW * 16;   // [16]
     if (tid < 16) {
-      unsigned long long k = s_key[0][tid];
+      unsigned long long k = s_key[tid];
 #pragma unroll
-      for (int w = 1; w < WAVES; ++w) k = s_key[w][tid] > k ? s_key[w][tid] : k;
+      for (int w = 1; w < SPW; ++w) k = s_key[w * 16 + tid] > k ? s_key[w * 16 + tid] : k;
       s_col[tid] = k;
     }
     __syncthreads();
@@ -704,32 +682,25 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     return;
   }
 
-  floatx4_t up[NSET];  // SwiGLU: the up side from the partner wave
+  floatx4_t up = (floatx4_t){0.f, 0.f, 0.f, 0.f};  // SwiGLU: the up side from the partner wave
+  bool store = row_ok;
   if constexpr (NS == 2 && EPI == GEMV_EPI_SWIGLU) {
-    __shared__ floatx4_t s_up[WAVES / 2][R][64];
-    if (wave & 1) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) s_up[wave >> 1][r][lane] = res[r];
-    }
+    floatx4_t *const s_up = (floatx4_t *)&act[1][0];   // [RPW][64]
+    if (carry && (ws & 1)) s_up[slot * 64 + lane] = res;
     __syncthreads();
-    if (wave & 1) return;  // the gate wave stores the pair's output
-#pragma unroll
-    for (int r = 0; r < R; ++r) up[r] = s_up[wave >> 1][r][lane];
+    store = row_ok && !(ws & 1);   // the gate wave stores the pair's output
+    if (store) up = s_up[slot * 64 + lane];
   }
-  float *const y0 = (NS == 2 && EPI == GEMV_EPI_PAIR && (wave & 1)) ? o.y1 : o.y;  // PAIR: each side its own output
+  float *const y0 = (NS == 2 && EPI == GEMV_EPI_PAIR && (ws & 1)) ? o.y1 : o.y;  // PAIR: each side its own output
 
   float sq[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of the row tile's sum of squares
   bool bad = false;                    // an f16 copy out of range
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = rgs[r] * Q4_ROWS + n;
-    if (rgs[r] >= p.nrg || row >= p.M) continue;
+  if (store) {
     float v[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float a0 = res[r][e];
-      if constexpr (NS == 2 && EPI == GEMV_EPI_SWIGLU) v[e] = silu_f(a0) * up[r][e];
-      else v[e] = a0;
+      if constexpr (NS == 2 && EPI == GEMV_EPI_SWIGLU) v[e] = silu_f(res[e]) * up[e];
+      else v[e] = res[e];
     }
     const float nwr = o.yh && o.nwh ? o.nwh[row] : 1.f;  // loaded with the residual
     if (y0 && o.accumulate) {  // all residual loads in flight together
@@ -758,20 +729,21 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   if (bad) raise_flag(o.rflag);
   if (o.ssq) {
     // Sum of squares of this row tile's outputs per column, in a fixed order
-    // (rows of a wave by the DPP tree, then waves in order): ssq[rt][c], the
-    // partials a normalising consumer sums.
-    __shared__ float s_sq[WAVES][16];
+    // (rows of a wave by the DPP tree, then row groups in order): ssq[rt][c],
+    // the partials a normalising consumer sums.  (STORE only: NS == 1, so
+    // slot == ws.)
+    float *const s_sq = (float *)&act[0][0];   // [SPW][16]
 #pragma unroll
     for (int e = 0; e < 4; ++e) sq[e] = sum16(sq[e]);
-    if (n == 0) {
+    if (carry && n == 0) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s_sq[wave][g * 4 + e] = sq[e];
+      for (int e = 0; e < 4; ++e) s_sq[ws * 16 + g * 4 + e] = sq[e];
     }
     __syncthreads();
     if (tid < 16 && tid < p.B) {
-      float t = s_sq[0][tid];
+      float t = s_sq[tid];
 #pragma unroll
-      for (int w = 1; w < WAVES; ++w) t += s_sq[w][tid];
+      for (int w = 1; w < SPW; ++w) t += s_sq[w * 16 + tid];
       o.ssq[rt * CWEN_BMAX + tid] = t;
     }
   }
@@ -788,7 +760,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 // nrg row groups) lands at destination row group rg_off onward; side_sel >= 0
 // takes that side of a Q4_0RSI source into a single-sided destination.
 __global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_t *sc, int type,
-                                 int M, int K, int nrg, int nst, int nsw, int rg_off, int side_sel) {
+                                 int M, int K, int nrg, int nst, int nsw, int rg_off, int side_sel, int nrg_dst) {
   const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   const size_t total = (size_t)nrg * nst * nsw * 64;
   if (id >= total) return;
@@ -803,7 +775,7 @@ __global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_
   const int sside = side_sel >= 0 ? side_sel : side;
   const bool q41 = type == CWEN_T_Q4_1;
   const uint32_t stb = q41 ? Fmt<GEMV_Q41>::ST_BYTES : Fmt<GEMV_Q4>::ST_BYTES;
-  uint8_t *stile = dst + (((size_t)(rg + rg_off) * nst + st) * nsw + side) * stb;
+  uint8_t *stile = dst + (((size_t)st * nrg_dst + rg + rg_off) * nsw + side) * stb;   // round-major
   uint16_t d[TILES], m[TILES];
   for (int u = 0; u < TILES; ++u) {
     const int blk = (st * TILES + u) * 4 + g;
@@ -879,7 +851,7 @@ __global__ void repack_q5k_kernel(uint8_t *dst, const uint8_t *src, int M, int K
   const int row = rg * Q4_ROWS + n;
   const int nsb = K / 256;
   using F = Fmt<GEMV_Q5K>;
-  uint8_t *stile = dst + ((size_t)rg * nst + st) * F::ST_BYTES;
+  uint8_t *stile = dst + ((size_t)st * nrg + rg) * F::ST_BYTES;   // round-major
   uint32_t hw[TILES], dm[TILES];
   for (int u = 0; u < TILES; ++u) {
     const int k0 = st * Q4_ST_K + u * Q4_TILE_K + g * 32;   // first K of the lane's sub-block
@@ -930,7 +902,7 @@ __global__ void repack_q6k_kernel(uint8_t *dst, const uint8_t *src, int M, int K
   const int row = rg * Q4_ROWS + n;
   const int nsb = K / 256;
   using F = Fmt<GEMV_Q6K>;
-  uint8_t *stile = dst + ((size_t)rg * nst + st) * F::ST_BYTES;
+  uint8_t *stile = dst + ((size_t)st * nrg + rg) * F::ST_BYTES;   // round-major
   uint8_t scb[8];
   uint32_t hiw[TILES][2];
   for (int u = 0; u < TILES; ++u) {
@@ -986,7 +958,7 @@ __global__ void repack_q8_kernel(uint8_t *dst, const uint8_t *src, int M, int K,
   const int row = rg * Q4_ROWS + n;
   const int nb = K / 32;
   using F = Fmt<GEMV_Q8>;
-  uint8_t *stile = dst + ((size_t)rg * nst + st) * F::ST_BYTES;
+  uint8_t *stile = dst + ((size_t)st * nrg + rg) * F::ST_BYTES;   // round-major
   uint16_t d[TILES];
   for (int u = 0; u < TILES; ++u) {
     const int blk = (st * TILES + u) * 4 + g;
@@ -1045,31 +1017,30 @@ __global__ __launch_bounds__(256) void argmax_walk_kernel(const float *lg, long 
   argmax_finish(s_col, B, a, tid, &s_flag);
 }
 
-template <int FMT, int NS, int R, int EPI, int CB, bool XN>
+template <int FMT, int NS, int EPI, int CB, bool XN>
 void launch_one(const GemvParams &p, int grid, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_kernel<FMT, NS, R, EPI, CB, XN>), dim3((unsigned)grid), dim3(64 * WAVES), 0, st, p);
+  hipLaunchKernelGGL((gemv_kernel<FMT, NS, EPI, CB, XN>), dim3((unsigned)grid), dim3(64 * WAVES), 0, st, p);
 }
 
-template <int FMT, int NS, int R, int EPI, bool XN>
+template <int FMT, int NS, int EPI, bool XN>
 void launch_xn(const GemvParams &p, int nrt, hipStream_t st) {
-  if (p.B <= 4) launch_one<FMT, NS, R, EPI, 4, XN>(p, nrt, st);
-  else if (p.B <= 8) launch_one<FMT, NS, R, EPI, 8, XN>(p, nrt, st);
-  else launch_one<FMT, NS, R, EPI, 16, XN>(p, nrt, st);
+  if (p.B <= 4) launch_one<FMT, NS, EPI, 4, XN>(p, nrt, st);
+  else if (p.B <= 8) launch_one<FMT, NS, EPI, 8, XN>(p, nrt, st);
+  else launch_one<FMT, NS, EPI, 16, XN>(p, nrt, st);
 }
 
-template <int FMT, int NS, int R, int EPI>
+template <int FMT, int NS, int EPI>
 void launch_cb(const GemvParams &p, int nrt, hipStream_t st) {
-  if (p.xf) launch_xn<FMT, NS, R, EPI, true>(p, nrt, st);
-  else launch_xn<FMT, NS, R, EPI, false>(p, nrt, st);
+  if (p.xf) launch_xn<FMT, NS, EPI, true>(p, nrt, st);
+  else launch_xn<FMT, NS, EPI, false>(p, nrt, st);
 }
 
 template <int FMT>
-int launch_fmt(const GemvParams &p, int nrt, int R, int nsides, int epi, hipStream_t st) {
-  if (R != 1) return CWEN_EINVAL;  // one row group per wave (gemv_choose_split)
+int launch_fmt(const GemvParams &p, int nrt, int nsides, int epi, hipStream_t st) {
   if (nsides == 1 && epi == GEMV_EPI_STORE) {
-    launch_cb<FMT, 1, 1, GEMV_EPI_STORE>(p, nrt, st);
+    launch_cb<FMT, 1, GEMV_EPI_STORE>(p, nrt, st);
   } else if (nsides == 1 && epi == GEMV_EPI_ARGMAX) {
-    launch_cb<FMT, 1, 1, GEMV_EPI_ARGMAX>(p, nrt, st);
+    launch_cb<FMT, 1, GEMV_EPI_ARGMAX>(p, nrt, st);
   } else {
     return CWEN_EINVAL;
   }
@@ -1101,7 +1072,7 @@ int gemv_repack(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, hipStr
   const size_t grid = (threads + blk - 1) / blk;
   if (w->fmt == GEMV_Q4 || w->fmt == GEMV_Q41)
     hipLaunchKernelGGL(repack_q4_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, dsc,
-                       w->type, w->ne1, w->ne0, w->nrg, w->nst, w->nside, 0, -1);
+                       w->type, w->ne1, w->ne0, w->nrg, w->nst, w->nside, 0, -1, w->nrg);
   else if (w->fmt == GEMV_Q6K)
     hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)grid), dim3(blk), 0, st, w->dev, dsrc, w->ne1,
                        w->ne0, w->nrg, w->nst);
@@ -1123,27 +1094,32 @@ int gemv_repack_part(cwen_weight *w, const uint8_t *dsrc, const uint16_t *dsc, i
   const size_t threads = (size_t)nrg * w->nst * 64;
   const int blk = 256;
   hipLaunchKernelGGL(repack_q4_kernel, dim3((unsigned)((threads + blk - 1) / blk)), dim3(blk), 0, st, w->dev, dsrc,
-                     dsc, type, M, w->ne0, nrg, w->nst, 1, row_off / Q4_ROWS, side_sel);
+                     dsc, type, M, w->ne0, nrg, w->nst, 1, row_off / Q4_ROWS, side_sel, w->nrg);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }
 
 // Split-K scratch of a decomposition: WAVES x 256 partial floats per piece
-// (one row group per wave) and one arrival counter per split tile.
+// at most (one 16-row stream per wave) and one arrival counter per split
+// tile.
 bool gemv_grid_fits(const GemvGrid &g, size_t partials_floats, int ncounters) {
   return g.nsplit == 0 || ((size_t)g.nsplit * WAVES * 256 <= partials_floats && g.nsplit / g.S <= ncounters);
 }
 
 namespace {
+// Row groups of one workgroup (its row tile): one 16-row stream per wave; a
+// pair computed whole puts its two sides on a wave pair.
+int tile_rows(int nsides) { return nsides == 2 ? WAVES / 2 : WAVES; }
+
 // Estimated length of a launch (microseconds at the 27B FFN shape's rates).
 // Workgroup i runs on CU i mod ncu (dispatch fills every CU's first slot,
 // then every second slot, ...).  A CU works through its workgroups' rounds,
 // plus one round of start-up each, at a rate that grows with the number of
-// workgroups it holds (measured: a lone four-wave workgroup is latency-bound);
-// the busiest CU sets the length.  Split remainder tiles add their
-// partial-sum hand-off, early in the launch: their pieces are dispatched
-// first, so they are the oldest workgroups on their CUs, which the hardware
-// serves first.
+// workgroups it holds (measured: a lone
+// four-wave workgroup is latency-bound); the busiest CU sets the length.
+// Split remainder tiles add their partial-sum hand-off, early in the launch:
+// their pieces are dispatched first, so they are the oldest workgroups on
+// their CUs, which the hardware serves first.
 constexpr double kSplitEarly = 0.3;
 double cu_rate(int wgs) {  // rounds per microsecond
   return wgs <= 1 ? 0.6 : wgs == 2 ? 1.2 : wgs == 3 ? 1.35 : wgs == 4 ? 1.45 : 1.5;
@@ -1163,11 +1139,12 @@ double grid_cost(int ncu, int nst, const GemvGrid &c, double extra) {
 }
 
 // Decomposition of ntile row tiles of nst rounds.  A launch with fewer tiles
-// than CUs splits every tile into S pieces (at least two rounds each) for at
-// most wg_per_cu workgroups per CU.  A larger one takes whole tiles, except
-// that the ntile mod ncu remainder tiles are split into the pieces (chosen by
-// grid_cost) that spread them over the CUs: without that, the CUs that get
-// one whole tile more than the others would set the launch's length.
+// than CUs splits every tile into S pieces (at least two rounds each)
+// for at most wg_per_cu workgroups per CU.  A larger one takes whole tiles,
+// except that the ntile mod ncu remainder tiles are split into the pieces
+// (chosen by grid_cost) that spread them over the CUs: without that, the
+// CUs that get one whole tile more than the others would set the launch's
+// length.
 GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
   GemvGrid best = {ntile, 0, 1, nst, 0};
   if (ntile < ctx->ncu) {
@@ -1177,8 +1154,8 @@ GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
     int S = std::min(std::max(target / ntile, 1), std::max(nst / 2, 1));
     const int rps = (nst + S - 1) / S;
     S = (nst + rps - 1) / rps;
-    const bool fits = gemv_grid_fits(GemvGrid{ntile * S, ntile * S, S, rps, 0}, ctx->partials_floats, ctx->ncounters);
-    if (S > 1 && fits) best = {ntile * S, ntile * S, S, rps, 0};
+    const GemvGrid cand = {ntile * S, ntile * S, S, rps, 0};
+    if (S > 1 && gemv_grid_fits(cand, ctx->partials_floats, ctx->ncounters)) best = cand;
     return best;
   }
   const int rem = ntile % ctx->ncu;
@@ -1199,19 +1176,17 @@ GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
 }  // namespace
 
 // Launch shape from the weight's shape only (never from B), so every output
-// bit is independent of the block size.  One row group (16 rows) per wave:
-// fewer registers and split partials than two, measured faster on every
-// 27B-shape matrix.  An interleaved pair computed whole puts its two sides on
-// a wave pair: half the row groups per workgroup.
+// bit is independent of the block size.  One row group (16 rows) per wave;
+// an interleaved pair computed whole puts its two sides on a wave pair.
 void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
   w->rows = 1;
   for (int ns = 1; ns <= w->nside; ++ns) {
-    const int rpw = ns == 2 ? WAVES / 2 : WAVES;
+    const int rpw = tile_rows(ns);
     w->cfg[ns - 1] = choose_grid(ctx, (w->nrg + rpw - 1) / rpw, w->nst);
   }
 }
 
-int gemv_row_tiles(const cwen_weight *w) { return (w->nrg + WAVES * w->rows - 1) / (WAVES * w->rows); }
+int gemv_row_tiles(const cwen_weight *w) { return (w->nrg + WAVES - 1) / WAVES; }
 
 int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int epi,
                 const _Float16 *xh, const GemvOut &out, int B, hipStream_t st, const GemvF32 *xf,
@@ -1242,9 +1217,8 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   p.part = scr ? scr->partials : ctx->partials;
   p.cnt = scr ? scr->counters : ctx->counters;
   p.out = out;
-  const int R = w->rows;
-  const int rpw = nsides == 2 ? WAVES / 2 : WAVES;  // row groups per row tile
-  const int ntile = (w->nrg + rpw * R - 1) / (rpw * R);
+  const int rpw = tile_rows(nsides);
+  const int ntile = (w->nrg + rpw - 1) / rpw;
   if (epi == GEMV_EPI_ARGMAX) cfg = {ntile, 0, 1, w->nst, 0};  // final row values in one workgroup
   if (scr && !gemv_grid_fits(cfg, scr->partials_floats, scr->ncounters)) return CWEN_ESCRATCH;
   p.nsplit = cfg.nsplit;
@@ -1255,22 +1229,22 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
   int rc = CWEN_EINVAL;
   if (w->fmt == GEMV_Q4) {
     if (nsides == 2 && epi == GEMV_EPI_PAIR) {
-      launch_cb<GEMV_Q4, 2, 1, GEMV_EPI_PAIR>(p, nrt, st);
+      launch_cb<GEMV_Q4, 2, GEMV_EPI_PAIR>(p, nrt, st);
       rc = CWEN_OK;
     } else if (nsides == 2 && epi == GEMV_EPI_SWIGLU) {
-      launch_cb<GEMV_Q4, 2, 1, GEMV_EPI_SWIGLU>(p, nrt, st);
+      launch_cb<GEMV_Q4, 2, GEMV_EPI_SWIGLU>(p, nrt, st);
       rc = CWEN_OK;
     } else {
-      rc = launch_fmt<GEMV_Q4>(p, nrt, R, nsides, epi, st);
+      rc = launch_fmt<GEMV_Q4>(p, nrt, nsides, epi, st);
     }
   } else if (w->fmt == GEMV_Q6K) {
-    rc = launch_fmt<GEMV_Q6K>(p, nrt, R, nsides, epi, st);
+    rc = launch_fmt<GEMV_Q6K>(p, nrt, nsides, epi, st);
   } else if (w->fmt == GEMV_Q8) {
-    rc = launch_fmt<GEMV_Q8>(p, nrt, R, nsides, epi, st);
+    rc = launch_fmt<GEMV_Q8>(p, nrt, nsides, epi, st);
   } else if (w->fmt == GEMV_Q41) {
-    rc = launch_fmt<GEMV_Q41>(p, nrt, R, nsides, epi, st);
+    rc = launch_fmt<GEMV_Q41>(p, nrt, nsides, epi, st);
   } else if (w->fmt == GEMV_Q5K) {
-    rc = launch_fmt<GEMV_Q5K>(p, nrt, R, nsides, epi, st);
+    rc = launch_fmt<GEMV_Q5K>(p, nrt, nsides, epi, st);
   }
   if (rc) return rc;
   CWEN_HIP_TRY(hipGetLastError());
