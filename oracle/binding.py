@@ -190,7 +190,23 @@ class Reference:
         L.ref_attention.argtypes = [_VP, _VP, _I, _I, _VP, _VP, _VP]
         L.ref_embed.restype = _I
         L.ref_embed.argtypes = [_I, _VP, _VP, _I, _VP]
+        L.ref_model_init.restype = _I
+        L.ref_model_init.argtypes = [_I]
+        L.ref_set_tensor.restype = _I
+        L.ref_set_tensor.argtypes = [_I, _I, _I, _VP, _VP, _I, _I]
+        L.ref_layer_step.restype = _I
+        L.ref_layer_step.argtypes = [_I, _I, _VP]
+        L.ref_head.restype = _I
+        L.ref_head.argtypes = [_VP, _VP, _I]
+        L.ref_gdn_state.restype = _I
+        L.ref_gdn_state.argtypes = [_I, _VP, _VP]
+        L.ref_mtp_step.restype = _I
+        L.ref_mtp_step.argtypes = [_I, _I, _VP, _VP]
+        L.ref_mtp_commit.restype = _I
+        L.ref_mtp_commit.argtypes = [_I, _I, _VP, _VP]
         self.L = L
+        self._model_ctx = None
+        self._bound = []   # tensors the reference's globals point into, kept alive
         self.vocab = L.ref_vocab()
 
     def gemvb(self, wtype, data, scales, K, M, X, side=0, out: np.ndarray | None = None):
@@ -283,3 +299,53 @@ class Reference:
         out = np.empty(5120, dtype=np.float32)
         self.L.ref_embed(wtype, qs.ctypes.data, None if sc is None else sc.ctypes.data, token, _f32p(out))
         return out
+
+    # ---- the reference's model composition (ref_harness.c), native dims only
+    def model_init(self, ctx: int = 64) -> None:
+        """alloc_state with ctx slots (once per process)."""
+        if self._model_ctx is None:
+            if self.L.ref_model_init(ctx):
+                raise RuntimeError("ref_model_init")
+            self._model_ctx = ctx
+        elif self._model_ctx != ctx:
+            raise RuntimeError("the reference's state was allocated with another context")
+
+    def set_tensor(self, layer: int, tid: int, wtype: int, data: np.ndarray, scales, ne0: int, ne1: int) -> None:
+        data = np.ascontiguousarray(data)
+        sc = None if scales is None else np.ascontiguousarray(scales)
+        self._bound.append((data, sc))
+        if self.L.ref_set_tensor(layer, tid, wtype, data.ctypes.data, None if sc is None else sc.ctypes.data,
+                                 ne0, ne1):
+            raise RuntimeError(f"ref_set_tensor({layer}, {tid})")
+
+    def layer_step(self, layer: int, pos: int, x: np.ndarray) -> np.ndarray:
+        x = np.array(x, dtype=np.float32, copy=True)
+        if self.L.ref_layer_step(layer, pos, _f32p(x)):
+            raise RuntimeError("ref_layer_step")
+        return x
+
+    def head(self, x: np.ndarray, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.float32)
+        if self.L.ref_head(_f32p(np.ascontiguousarray(x, np.float32)), _f32p(out), n):
+            raise RuntimeError("ref_head")
+        return out
+
+    def gdn_state(self, layer: int) -> tuple[np.ndarray, np.ndarray]:
+        S = np.empty((48, 128, 128), dtype=np.float32)
+        hist = np.empty((10240, 3), dtype=np.float32)
+        if self.L.ref_gdn_state(layer, _f32p(S), _f32p(hist)):
+            raise RuntimeError("ref_gdn_state")
+        return S, hist
+
+    def mtp_step(self, tok: int, pos: int, h: np.ndarray) -> np.ndarray:
+        out = np.empty(5120, dtype=np.float32)
+        if self.L.ref_mtp_step(tok, pos, _f32p(np.ascontiguousarray(h, np.float32)), _f32p(out)):
+            raise RuntimeError("ref_mtp_step")
+        return out
+
+    def mtp_commit(self, pos: int, tok: int, x_pre: np.ndarray) -> tuple[int, np.ndarray]:
+        hprev = np.empty(5120, dtype=np.float32)
+        hp = self.L.ref_mtp_commit(pos, tok, _f32p(np.ascontiguousarray(x_pre, np.float32)), _f32p(hprev))
+        if hp < -1:
+            raise RuntimeError("ref_mtp_commit")
+        return hp, hprev

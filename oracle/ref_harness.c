@@ -134,3 +134,140 @@ int ref_embed(int type, const void *qs, const void *sc, int token, float *dst) {
   tok_embd = saved;
   return 0;
 }
+
+/* ---- the model composition, for pinning the oracle's serial forward ----
+ * The reference's own layer functions over its global state: W[l] (and NW,
+ * tok_embd, output_norm, output) bound to caller tensors, the activation x,
+ * pos_n, Srec / Cstate and the KV caches from alloc_state.  Dimensions are
+ * the reference's compile-time ones (H 5120, I 17408, 24/4 heads of 256,
+ * GDN 16/48 x 128). */
+
+/* tensor ids of include/cwen_gpu.h (CWEN_TOK_EMBD ...) */
+enum { ID_TOK_EMBD, ID_OUTPUT_NORM, ID_OUTPUT, ID_ATTN_NORM, ID_POST_NORM, ID_FFN_GATE_UP, ID_FFN_DOWN,
+       ID_ATTN_QKV, ID_ATTN_GATE, ID_SSM_ALPHA, ID_SSM_BETA, ID_SSM_A, ID_SSM_DT, ID_SSM_CONV, ID_SSM_NORM,
+       ID_SSM_OUT, ID_ATTN_Q, ID_ATTN_KV, ID_ATTN_OUTPUT, ID_ATTN_Q_NORM, ID_ATTN_K_NORM, ID_NEXTN_EH_PROJ,
+       ID_NEXTN_ENORM, ID_NEXTN_HNORM, ID_NEXTN_SHEAD_NORM };
+
+/* alloc_state (run.c:3928) with a context of ctx slots and the nextn stream
+ * on; every layer l with l % FULL_INT != FULL_INT - 1 is linear.  Once per
+ * process. */
+int ref_model_init(int ctx) {
+  if (ctx < 2 || ctx > MAX_SEQ || logits) return -1;
+  g_ctx = ctx;
+  mtp_use = 1;
+  spec_enabled = 0;
+  alloc_state();
+  for (int l = 0; l < L; l++) W[l].is_linear = (l % FULL_INT) != FULL_INT - 1;
+  mtp_hpos = -1;
+  return 0;
+}
+
+/* Bind one tensor: layer -1 the globals and the nextn projection / norms,
+ * layer L the nextn decoder block (NW), else W[layer].  A Q4_0RSI pair binds
+ * both of its Tensors (pair_side 0 and 1), as load_cwenr does. */
+int ref_set_tensor(int layer, int id, int type, const void *data, const void *scales, int ne0, int ne1) {
+  const Tensor t0 = mk(type, data, scales, ne0, ne1, 0), t1 = mk(type, data, scales, ne0, ne1, 1);
+  if (layer < 0) {
+    switch (id) {
+      case ID_TOK_EMBD: tok_embd = t0; return 0;
+      case ID_OUTPUT_NORM: output_norm = t0; return 0;
+      case ID_OUTPUT: output = t0; return 0;
+      case ID_NEXTN_EH_PROJ: NW.eh_proj = t0; return 0;
+      case ID_NEXTN_ENORM: NW.enorm = t0; return 0;
+      case ID_NEXTN_HNORM: NW.hnorm = t0; return 0;
+      case ID_NEXTN_SHEAD_NORM: NW.shared_head_norm = t0; return 0;
+      default: return -1;
+    }
+  }
+  if (layer == L) {
+    switch (id) {
+      case ID_ATTN_NORM: NW.attn_norm = t0; return 0;
+      case ID_POST_NORM: NW.post_norm = t0; return 0;
+      case ID_FFN_GATE_UP: NW.ffn_gate = t0; NW.ffn_up = t1; return 0;
+      case ID_FFN_DOWN: NW.ffn_down = t0; return 0;
+      case ID_ATTN_Q: NW.wq = t0; return 0;
+      case ID_ATTN_KV: NW.wk = t0; NW.wv = t1; return 0;
+      case ID_ATTN_OUTPUT: NW.wo = t0; return 0;
+      case ID_ATTN_Q_NORM: NW.q_norm = t0; return 0;
+      case ID_ATTN_K_NORM: NW.k_norm = t0; return 0;
+      default: return -1;
+    }
+  }
+  if (layer >= L) return -1;
+  LayerW *w = &W[layer];
+  switch (id) {
+    case ID_ATTN_NORM: w->attn_norm = t0; return 0;
+    case ID_POST_NORM: w->post_norm = t0; return 0;
+    case ID_FFN_GATE_UP: w->ffn_gate = t0; w->ffn_up = t1; return 0;
+    case ID_FFN_DOWN: w->ffn_down = t0; return 0;
+    case ID_ATTN_QKV: w->qkv = t0; return 0;
+    case ID_ATTN_GATE: w->gate_z = t0; return 0;
+    case ID_SSM_ALPHA: w->ssm_alpha = t0; return 0;
+    case ID_SSM_BETA: w->ssm_beta = t0; return 0;
+    case ID_SSM_A: w->ssm_a = t0; return 0;
+    case ID_SSM_DT: w->ssm_dt = t0; return 0;
+    case ID_SSM_CONV: w->ssm_conv = t0; return 0;
+    case ID_SSM_NORM: w->ssm_norm = t0; return 0;
+    case ID_SSM_OUT: w->ssm_out = t0; return 0;
+    case ID_ATTN_Q: w->wq = t0; return 0;
+    case ID_ATTN_KV: w->wk = t0; w->wv = t1; return 0;
+    case ID_ATTN_OUTPUT: w->wo = t0; return 0;
+    case ID_ATTN_Q_NORM: w->q_norm = t0; return 0;
+    case ID_ATTN_K_NORM: w->k_norm = t0; return 0;
+    default: return -1;
+  }
+}
+
+/* One decoder layer at position pos on the residual xio[H]:
+ * layer_linear (run.c:2323) or layer_full (run.c:2412), in place. */
+int ref_layer_step(int layer, int pos, float *xio) {
+  if (!logits || layer < 0 || layer >= L || pos < 0 || pos >= g_ctx) return -1;
+  memcpy(x, xio, sizeof x);
+  pos_n = pos;
+  if (W[layer].is_linear) layer_linear(layer);
+  else layer_full(layer);
+  memcpy(xio, x, sizeof x);
+  return 0;
+}
+
+/* The head tail of forward_ex (run.c:2640-2644) on residual xin[H]: the
+ * first n logits of output . rmsnorm(x, output_norm). */
+int ref_head(const float *xin, float *out, int n) {
+  if (!logits || n < 1 || n > output.ne1) return -1;
+  memcpy(x, xin, sizeof x);
+  rmsnorm(xb, x, (const float *)output_norm.data, H);
+  gemv(&output, xb, logits);
+  memcpy(out, logits, (size_t)n * sizeof(float));
+  return 0;
+}
+
+/* Layer l's recurrent state [LVH][LSD][LSD] and conv history [QKV_DIM][3]. */
+int ref_gdn_state(int layer, float *S, float *hist) {
+  if (!Srec || layer < 0 || layer >= L) return -1;
+  if (S) memcpy(S, Srec + (size_t)layer * LVH * LSD * LSD, (size_t)LVH * LSD * LSD * sizeof(float));
+  if (hist) memcpy(hist, Cstate + (size_t)layer * QKV_DIM * (CONV_K - 1), (size_t)QKV_DIM * (CONV_K - 1) * sizeof(float));
+  return 0;
+}
+
+/* mtp_step (run.c:3099): the nextn block at stream slot pos on token tok and
+ * predecessor hidden h[H]; out[H] the shared-head-normed hidden. */
+int ref_mtp_step(int tok, int pos, const float *h, float *out) {
+  static float hb_[H] __attribute__((aligned(64))), ob_[H] __attribute__((aligned(64)));
+  if (!NKc || pos < 1 || pos >= g_ctx || tok < 0 || tok >= V) return -1;
+  memcpy(hb_, h, sizeof hb_);
+  mtp_step(tok, pos, hb_, ob_);
+  memcpy(out, ob_, sizeof ob_);
+  return 0;
+}
+
+/* mtp_commit (run.c:3146): fold position pos (token tok, target residual
+ * x_pre[H]) into the nextn stream; hprev[H] (nullable) receives the parked
+ * hidden.  Returns the parked position. */
+int ref_mtp_commit(int pos, int tok, const float *x_pre, float *hprev) {
+  static float xb_[H] __attribute__((aligned(64)));
+  if (!NKc || pos < 0 || pos >= g_ctx || tok < 0 || tok >= V) return -1;
+  memcpy(xb_, x_pre, sizeof xb_);
+  mtp_commit(pos, tok, xb_);
+  if (hprev) memcpy(hprev, NHprev, sizeof NHprev);
+  return mtp_hpos;
+}

@@ -54,32 +54,52 @@ class OracleModel:
         return self.t[(layer, tid)][1]
 
     def step(self, tok: int, pos: int) -> np.ndarray:
+        """forward_ex (run.c:2594-2645): embed, every layer, the MTP commit
+        when present, the head."""
         from cwen_amd import gpu as G
         O, c = self.O, self.c
         wtype, qs, sc, H, _ = self.t[(-1, G.TOK_EMBD)]
         x = O.embed(wtype, qs, sc, int(tok), H)
         for l in range(c["n_layers"]):
-            xb = O.rmsnorm(x, self.f32(l, G.ATTN_NORM))
-            if l in self.S:
-                qkv = self.mv(l, G.ATTN_QKV, xb)
-                z = self.mv(l, G.ATTN_GATE, xb)
-                a = self.mv(l, G.SSM_ALPHA, xb)
-                b = self.mv(l, G.SSM_BETA, xb)
-                A, dt = self.f32(l, G.SSM_A), self.f32(l, G.SSM_DT)
-                xa = (a + dt).astype(np.float32)
-                sp = np.where(xa > 20, xa, np.log(np.float32(1) + np.exp(xa))).astype(np.float32)
-                decay = (A * sp).astype(np.float32)
-                beta = (np.float32(1) / (np.float32(1) + np.exp(-b))).astype(np.float32)
-                xc, self.hist[l] = O.conv1d_update(qkv, self.hist[l], self.f32(l, G.SSM_CONV).reshape(-1, 4))
-                self.S[l], _, o = O.gdn_step(self.S[l], xc, z, decay, beta, self.f32(l, G.SSM_NORM),
-                                             c["gdn_nkh"], c["gdn_nvh"], 128)
-                x = (x + self.mv(l, G.SSM_OUT, o)).astype(np.float32)
-            else:
-                x = self.full_attn(l, x, xb, pos, 0)
-            x = self.mlp(l, x)
+            x = self.layer(l, x, pos)
         self.mtp_commit(pos, int(tok), x)
-        xb = O.rmsnorm(x, self.f32(-1, G.OUTPUT_NORM))
-        return self.mv(-1, G.OUTPUT, xb)
+        return self.head(x)
+
+    def layer(self, l, x, pos):
+        """layer_linear (run.c:2323-2358) or layer_full (run.c:2412-2458)
+        on residual x at position pos."""
+        return self.linear_layer(l, x) if l in self.S else self.full_layer(l, x, pos)
+
+    def linear_layer(self, l, x):
+        """layer_linear (run.c:2323-2358): the GatedDeltaNet sublayer, then the MLP."""
+        from cwen_amd import gpu as G
+        O, c = self.O, self.c
+        xb = O.rmsnorm(x, self.f32(l, G.ATTN_NORM))
+        qkv = self.mv(l, G.ATTN_QKV, xb)
+        z = self.mv(l, G.ATTN_GATE, xb)
+        a = self.mv(l, G.SSM_ALPHA, xb)
+        b = self.mv(l, G.SSM_BETA, xb)
+        A, dt = self.f32(l, G.SSM_A), self.f32(l, G.SSM_DT)
+        xa = (a + dt).astype(np.float32)
+        sp = np.where(xa > 20, xa, np.log(np.float32(1) + np.exp(xa))).astype(np.float32)
+        decay = (A * sp).astype(np.float32)
+        beta = (np.float32(1) / (np.float32(1) + np.exp(-b))).astype(np.float32)
+        xc, self.hist[l] = O.conv1d_update(qkv, self.hist[l], self.f32(l, G.SSM_CONV).reshape(-1, 4))
+        self.S[l], _, o = O.gdn_step(self.S[l], xc, z, decay, beta, self.f32(l, G.SSM_NORM),
+                                     c["gdn_nkh"], c["gdn_nvh"], 128)
+        x = (x + self.mv(l, G.SSM_OUT, o)).astype(np.float32)
+        return self.mlp(l, x)
+
+    def full_layer(self, l, x, pos):
+        """layer_full (run.c:2412-2458): gated attention over slots 0..pos, then the MLP."""
+        from cwen_amd import gpu as G
+        xb = self.O.rmsnorm(x, self.f32(l, G.ATTN_NORM))
+        return self.mlp(l, self.full_attn(l, x, xb, pos, 0))
+
+    def head(self, x):
+        """The head tail of forward_ex (run.c:2640-2644)."""
+        from cwen_amd import gpu as G
+        return self.mv(-1, G.OUTPUT, self.O.rmsnorm(x, self.f32(-1, G.OUTPUT_NORM)))
 
     def full_attn(self, l, x, xb, pos, t0):
         """layer_full (run.c:2412-2458): x + the gated attention over slots t0..pos."""
