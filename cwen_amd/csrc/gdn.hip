@@ -30,9 +30,10 @@
 // the commit (cwen_gdn_commit, or the model's device commit).
 //
 // Design (gfx950): three launches on the caller's stream.
-//  1. conv: one thread per channel runs the B positions in order, writes the
-//     post-SiLU values to the pending buffer and the history after every
-//     position to the ring.
+//  1. conv: one thread per (channel, position): the 4-tap filter reads its
+//     inputs from the block's rows or the start history slot, so every
+//     position is computed at once; it writes the post-SiLU value to the
+//     pending buffer and that position's history slot to the ring.
 //  2. recurrence: the delta rule is column-local (sk[j], delta[j] and o[j]
 //     read only column j), so a head's 128 columns split over 8 single-wave
 //     workgroups of 16 columns (384 workgroups at 48 heads).  A lane owns a

@@ -16,38 +16,44 @@
 #include <stdlib.h>
 #include <unistd.h>
 
-static uint32_t rd_u32(FILE *f) {
-  uint32_t v = 0;
-  return fread(&v, 4, 1, f) == 1 ? v : 0xffffffffu;
-}
+#define END_WORD 0xffffffffu
 
-/* Read and drop n words; a short read leaves the stream at its end, which
- * the next header read reports. */
-static void drain(FILE *f, uint64_t n) {
-  uint32_t buf[1024];
-  while (n) {
-    const size_t take = n > 1024 ? 1024 : (size_t)n;
-    if (fread(buf, 4, take, f) != take) return;
-    n -= take;
+/* Skip `words` 4-byte words of a rejected frame's payload.  Pipes cannot
+ * seek, so the bytes are read into a scratch block and dropped; a stream that
+ * ends early is left at its end, where the next header read sees it. */
+static void skip_payload(FILE *f, uint64_t words) {
+  unsigned char scratch[4096];
+  uint64_t left = words * 4u;
+  while (left > 0) {
+    const size_t want = left < sizeof scratch ? (size_t)left : sizeof scratch;
+    const size_t got = fread(scratch, 1, want, f);
+    if (got != want) break;
+    left -= got;
   }
 }
 
+/* One request frame; see cwen_read_frame in cwen_host.h for the outcomes. */
 static int read_frame(FILE *in, int *tokens, int max_ctx, int vocab, uint32_t *np, uint32_t *ng) {
-  const uint32_t n_prompt = rd_u32(in), n_gen = rd_u32(in);
-  if (n_prompt == 0xffffffffu || n_gen == 0xffffffffu) return CWEN_FRAME_END;
-  if (!n_prompt || n_prompt > (uint32_t)max_ctx || !n_gen || n_gen > (uint32_t)max_ctx) {
-    fprintf(stderr, "cwen server: bad frame %u %u\n", n_prompt, n_gen);
-    drain(in, n_prompt);
+  uint32_t hdr[2];
+  if (fread(hdr, sizeof hdr[0], 2, in) != 2 || hdr[0] == END_WORD || hdr[1] == END_WORD)
+    return CWEN_FRAME_END;                        /* closed stream or the end marker */
+  const uint32_t lim = (uint32_t)max_ctx;
+  const int counts_ok = hdr[0] >= 1 && hdr[0] <= lim && hdr[1] >= 1 && hdr[1] <= lim;
+  if (!counts_ok) {
+    fprintf(stderr, "cwen_serve: rejecting a frame of %u prompt / %u new tokens (each must be 1..%d)\n",
+            hdr[0], hdr[1], max_ctx);
+    skip_payload(in, hdr[0]);                     /* keep the next header aligned */
     return CWEN_FRAME_REJECTED;
   }
-  if (fread(tokens, 4, n_prompt, in) != n_prompt) return CWEN_FRAME_END;
-  for (uint32_t i = 0; i < n_prompt; i++)
-    if (tokens[i] < 0 || tokens[i] >= vocab) {
-      fprintf(stderr, "cwen server: token %d out of range [0,%d)\n", tokens[i], vocab);
-      return CWEN_FRAME_REJECTED;
-    }
-  *np = n_prompt;
-  *ng = n_gen;
+  if (fread(tokens, sizeof tokens[0], hdr[0], in) != hdr[0]) return CWEN_FRAME_END;  /* cut short */
+  for (uint32_t i = 0; i < hdr[0]; i++) {
+    if (tokens[i] >= 0 && tokens[i] < vocab) continue;
+    fprintf(stderr, "cwen_serve: rejecting a frame whose token %u is %d (vocabulary 0..%d)\n", i, tokens[i],
+            vocab - 1);
+    return CWEN_FRAME_REJECTED;
+  }
+  *np = hdr[0];
+  *ng = hdr[1];
   return CWEN_FRAME_OK;
 }
 
@@ -74,7 +80,7 @@ int cwen_read_frame(int fd, int *tokens, int max_ctx, int vocab, uint32_t *n_pro
 
 static int put_reply(FILE *out, const int *tok, uint32_t n) {
   if (fwrite(&n, 4, 1, out) != 1 || (n && fwrite(tok, 4, n, out) != n) || fflush(out)) {
-    fprintf(stderr, "cwen server: reply write failed\n");
+    fprintf(stderr, "cwen_serve: a reply could not be written\n");
     return CWEN_EIO;
   }
   return CWEN_OK;
