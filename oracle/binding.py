@@ -204,6 +204,7 @@ class Reference:
         L.ref_mtp_step.argtypes = [_I, _I, _VP, _VP]
         L.ref_mtp_commit.restype = _I
         L.ref_mtp_commit.argtypes = [_I, _I, _VP, _VP]
+        L.ref_snap_roundtrip.restype = _I
         self.L = L
         self._model_ctx = None
         self._bound = []   # tensors the reference's globals point into, kept alive
@@ -349,3 +350,8 @@ class Reference:
         if hp < -1:
             raise RuntimeError("ref_mtp_commit")
         return hp, hprev
+
+    def snap_roundtrip(self) -> None:
+        """snap_save + snap_load over the whole model's GDN state."""
+        if self.L.ref_snap_roundtrip():
+            raise RuntimeError("ref_snap_roundtrip")

@@ -271,3 +271,18 @@ int ref_mtp_commit(int pos, int tok, const float *x_pre, float *hprev) {
   if (hprev) memcpy(hprev, NHprev, sizeof NHprev);
   return mtp_hpos;
 }
+
+/* The rollback copies of a drafted cycle: snap_save then snap_load
+ * (run.c:2802-2809) over all L layers' Srec and Cstate, allocating the
+ * state (ref_model_init) and the snapshot buffers on first use. */
+int ref_snap_roundtrip(void) {
+  if (!logits && ref_model_init(2)) return -1;
+  if (!SnapS) {
+    SnapS = aligned_alloc(64, (size_t)L * LVH * LSD * LSD * sizeof(float));
+    SnapC = aligned_alloc(64, (size_t)L * QKV_DIM * (CONV_K - 1) * sizeof(float));
+    if (!SnapS || !SnapC) return -1;
+  }
+  snap_save();
+  snap_load();
+  return 0;
+}

@@ -186,11 +186,13 @@ def test_head_argument_errors(env):
 
 
 @pytest.mark.slow
-def test_head_full_size(env, oracle):
-    """The 151936 x 5120 Q6_K head at B=8: logits on a row sample vs the
-    oracle, argmax and walk vs the oracle on the GPU's logits."""
+@pytest.mark.parametrize("V", [151936, 248320])
+def test_head_full_size(env, oracle, V):
+    """The Q6_K head at B=8 at the workload's vocabulary (151936) and the real
+    model's (248320, run.c:84; 1.04 GB of weights): logits on a row sample vs
+    the oracle, argmax and walk vs the oracle on the GPU's logits."""
     _, gpu, ctx = env
-    V, K, B = 151936, 5120, 8
+    K, B = 5120, 8
     data = synth.q6_k(0, V, K)
     W = gpu.Weight(ctx, T_Q6_K, data, None, K, V)
     X = synth.activations(0, B, K)
