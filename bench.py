@@ -571,22 +571,36 @@ def main() -> int:
     if 8 not in Bs:
         print("bench.py: --Bs must include the headline B=8", file=sys.stderr)
         return 2
+    t_start = time.time()
+
+    def done(what: str) -> None:
+        print(f"bench.py: {what} done at {time.time() - t_start:.1f} s", file=sys.stderr, flush=True)
+
     if args.calibrate_copy:
         calibrate_copy()
     res = gpu_leg(args.steps, args.warmup, Bs)
+    done("FFN leg")
     extra = None if args.no_extra else extra_leg(args.steps, args.warmup)
+    if extra is not None:
+        done("c0/c2/c3/head legs")
     c4 = None if args.no_c4 else c4_leg(args.c4_prompt, args.c4_cycles, serial=not args.c4_spec_only)
+    if c4 is not None:
+        done("27B-shape model leg")
     mtp = mtp_leg(args.c4_prompt, 64) if args.mtp else None
     traffic = load_traffic()
     cpu_base = None
     if not args.no_cpu_baseline:
         cpu_base = cpu_leg("c1", 8)
+        done("CPU leg c1")
         if cpu_base is not None:
             cpu_base["host"] = host_cpu_info()
             cpu_base["threads_note"] = ("OMP threads = the reference's default of 16 (cwen_tune.h:7), bounded by "
                                         "the host's logical CPUs; see host.physical_cores_per_socket")
             if not args.no_extra:
-                cpu_base["other_configs"] = {name: cpu_leg(name) for name in ("c0", "c2", "c3")}
+                cpu_base["other_configs"] = {}
+                for name in ("c0", "c2", "c3"):
+                    cpu_base["other_configs"][name] = cpu_leg(name)
+                    done(f"CPU leg {name}")
     h = res[8]
     b1, _ = ffn_bytes(8)
     line = {
