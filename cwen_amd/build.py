@@ -66,7 +66,7 @@ def build_gpu(verbose: bool = False) -> Path:
 
 def build_host(verbose: bool = False) -> Path:
     """The C host drivers (cwen_amd/host), linked against libcwen_gpu.so."""
-    srcs = [PKG / "host" / "cwen_host.c", PKG / "host" / "cwen_gguf.c", PKG / "host" / "cwen_serve.c"]
+    srcs = [PKG / "host" / f for f in ("cwen_host.c", "cwen_ngram.c", "cwen_gguf.c", "cwen_serve.c")]
     tmp = HOST_LIB.with_suffix(".so.tmp")
     _run(["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", "-fPIC", "-shared", f"-I{ROOT / 'include'}",
           *map(str, srcs), f"-L{PKG}", "-lcwen_gpu", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])
@@ -74,6 +74,22 @@ def build_host(verbose: bool = False) -> Path:
     if verbose:
         print(f"built {HOST_LIB}")
     return HOST_LIB
+
+
+CLI = PKG / "cwen_run"
+
+
+def build_cli(verbose: bool = False) -> Path:
+    """cwen_run, the command-line front end (cwen_amd/host/cwen_run.c), linked
+    against libcwen_host.so and libcwen_gpu.so next to it."""
+    tmp = CLI.with_suffix(".tmp")
+    _run(["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", f"-I{ROOT / 'include'}", f"-I{PKG / 'host'}",
+          str(PKG / "host" / "cwen_run.c"), f"-L{PKG}", "-lcwen_host", "-lcwen_gpu", "-Wl,-rpath,$ORIGIN",
+          "-o", str(tmp)])
+    os.replace(tmp, CLI)
+    if verbose:
+        print(f"built {CLI}")
+    return CLI
 
 
 def build_oracle(verbose: bool = False) -> None:
@@ -89,5 +105,6 @@ def build_oracle(verbose: bool = False) -> None:
 if __name__ == "__main__":
     build_gpu(verbose=True)
     build_host(verbose=True)
+    build_cli(verbose=True)
     if "--oracle" in sys.argv:
         build_oracle(verbose=True)

@@ -69,6 +69,18 @@ HOST_SIGNATURES = [
     ("cwen_prefill", _I, [_VP, _VP, _I, C.POINTER(_I)]),
     ("cwen_generate_serial", _I, [_VP, _VP, _I, _I, _VP, _VP]),
     ("cwen_generate_spec", _I, [_VP, _VP, _I, _I, _VP, _VP, _VP]),
+    ("cwen_spec_replay", _I, [_VP, _I, _I, _I, _I, _VP, _VP, _VP]),
+    ("cwen_ngmap_create", _I, [_I, _I, C.c_size_t, C.POINTER(_VP)]),
+    ("cwen_ngmap_free", None, [_VP]),
+    ("cwen_ngmap_n_key", _I, [_VP]),
+    ("cwen_ngmap_used", C.c_size_t, [_VP]),
+    ("cwen_ngmap_evictions", None, [_VP, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    ("cwen_ngmap_update", None, [_VP, _VP, _I, _I]),
+    ("cwen_ngmap_update_range", None, [_VP, _VP, _I, _I]),
+    ("cwen_ngmap_draft", _I, [_VP, _VP, _I, _VP, _I]),
+    ("cwen_ngmap_save", _I, [_VP, C.c_char_p]),
+    ("cwen_ngmap_load", _I, [_VP, C.c_char_p]),
+    ("cwen_ngmap_dump", _I, [_VP, _VP, _VP, _VP, _VP]),
     ("cwen_gguf_open", _I, [C.c_char_p, C.POINTER(_VP)]),
     ("cwen_gguf_close", None, [_VP]),
     ("cwen_gguf_error", C.c_char_p, []),
@@ -81,6 +93,7 @@ HOST_SIGNATURES = [
     ("cwen_gguf_apply_cwenr", _I, [_VP, C.c_char_p, C.c_char_p]),
     ("cwen_f32_to_f16", C.c_uint16, [C.c_float]),
     ("cwen_model_load_gguf", _I, [_VP, _VP, _VP]),
+    ("cwen_model_cfg_from_gguf", _I, [_VP, _I, _VP]),
     ("cwen_read_frame", _I, [_I, _VP, _I, _I, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     ("cwen_serve", _I, [_VP, _VP, _I, _I, _VP, C.POINTER(_I)]),
 ]
@@ -335,7 +348,91 @@ class ModelCfg(C.Structure):
 
 class SpecCfg(C.Structure):
     _fields_ = [("n_key", C.c_int), ("max_draft", C.c_int), ("min_draft", C.c_int), ("cooldown", C.c_int),
-                ("max_cycles", C.c_int), ("mtp", C.c_int)]
+                ("max_cycles", C.c_int), ("mtp", C.c_int), ("ngmap", C.c_void_p), ("cycle_log", C.c_void_p),
+                ("cycle_log_cap", C.c_int), ("debug", C.c_int)]
+
+
+def spec_cfg(n_key: int = 16, max_draft: int = 8, min_draft: int = 2, cooldown: int = 8, max_cycles: int = 0,
+             mtp: int = 1, ngmap: "NgMap | None" = None, cycle_log: np.ndarray | None = None,
+             debug: int = 0) -> SpecCfg:
+    """A speculation config; cycle_log (int32, even length) receives (E, k) per cycle."""
+    return SpecCfg(n_key, max_draft, min_draft, cooldown, max_cycles, mtp, None if ngmap is None else ngmap.h,
+                   None if cycle_log is None else cycle_log.ctypes.data,
+                   0 if cycle_log is None else cycle_log.size // 2, debug)
+
+
+class NgMap:
+    """The host library's counted n-gram map (cwen_ngmap_*; no GPU needed)."""
+
+    def __init__(self, n_key: int = 16, vocab: int = 248320, cap: int = 0):
+        h = C.c_void_p()
+        check("cwen_ngmap_create", host_lib().cwen_ngmap_create(n_key, vocab, cap, C.byref(h)))
+        self.h, self.n_key = h, n_key
+        self.cap = cap or (1 << 18)
+
+    def update(self, key, tok: int, hits: int = 1) -> None:
+        k = np.ascontiguousarray(key, dtype=np.int32)
+        host_lib().cwen_ngmap_update(self.h, k.ctypes.data, int(tok), int(hits))
+
+    def update_range(self, hist, a: int, b: int) -> None:
+        h = np.ascontiguousarray(hist, dtype=np.int32)
+        host_lib().cwen_ngmap_update_range(self.h, h.ctypes.data, a, b)
+
+    def draft(self, hist, max_d: int) -> np.ndarray:
+        h = np.ascontiguousarray(hist, dtype=np.int32)
+        out = np.zeros(max(max_d, 1), dtype=np.int32)
+        n = host_lib().cwen_ngmap_draft(self.h, h.ctypes.data, h.size, out.ctypes.data, max_d)
+        return out[:n]
+
+    def save(self, path) -> None:
+        check("cwen_ngmap_save", host_lib().cwen_ngmap_save(self.h, str(path).encode()))
+
+    def load(self, path) -> int:
+        n = host_lib().cwen_ngmap_load(self.h, str(path).encode())
+        if n < 0:
+            raise CwenError("cwen_ngmap_load", n)
+        return n
+
+    def used(self) -> int:
+        return host_lib().cwen_ngmap_used(self.h)
+
+    def evictions(self) -> tuple[int, int]:
+        """(entries evicted, evictions that shifted no entry into the freed slot)."""
+        a, b = C.c_size_t(), C.c_size_t()
+        host_lib().cwen_ngmap_evictions(self.h, C.byref(a), C.byref(b))
+        return a.value, b.value
+
+    def dump(self) -> tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]:
+        keys = np.zeros((self.cap, self.n_key), np.int32)
+        tok = np.zeros(self.cap, np.int32)
+        cnt = np.zeros(self.cap, np.int32)
+        used = np.zeros(self.cap, np.uint8)
+        check("cwen_ngmap_dump", host_lib().cwen_ngmap_dump(self.h, keys.ctypes.data, tok.ctypes.data,
+                                                            cnt.ctypes.data, used.ctypes.data))
+        return keys, tok, cnt, used
+
+    def free(self) -> None:
+        if self.h:
+            host_lib().cwen_ngmap_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def spec_replay(stream, n_prompt: int, n_gen: int, max_ctx: int, cfg: SpecCfg) -> tuple[np.ndarray, "SpecStats"]:
+    """cwen_spec_replay: the speculative driver against a recorded greedy stream."""
+    s = np.ascontiguousarray(stream, dtype=np.int32)
+    out = np.zeros(max(n_gen, 1), dtype=np.int32)
+    st = SpecStats()
+    n = host_lib().cwen_spec_replay(s.ctypes.data, s.size, n_prompt, n_gen, max_ctx, C.byref(cfg), out.ctypes.data,
+                                    C.byref(st))
+    if n < 0:
+        raise CwenError("cwen_spec_replay", n)
+    return out[:n], st
 
 
 class SpecStats(C.Structure):
@@ -403,6 +500,14 @@ class GGUF:
     @staticmethod
     def last_error() -> str:
         return host_lib().cwen_gguf_error().decode()
+
+    def model_cfg(self, max_ctx: int = 4096) -> dict:
+        """The model geometry read from the tensor shapes (cwen_model_cfg_from_gguf)."""
+        c = ModelCfg()
+        rc = host_lib().cwen_model_cfg_from_gguf(self.h, max_ctx, C.byref(c))
+        if rc != CWEN_OK:
+            raise CwenError(f"cwen_model_cfg_from_gguf ({host_lib().cwen_gguf_error().decode()})", rc)
+        return {name: getattr(c, name) for name, _ in ModelCfg._fields_}
 
     def close(self) -> None:
         if self.h:
@@ -488,10 +593,11 @@ class Model:
         return (out[:n], st) if with_stats else out[:n]
 
     def generate_spec(self, prompt, n_gen: int, n_key: int = 16, max_draft: int = 8, min_draft: int = 2,
-                      cooldown: int = 8, max_cycles: int = 0, mtp: int = 1) -> tuple[np.ndarray, SpecStats]:
+                      cooldown: int = 8, max_cycles: int = 0, mtp: int = 1, ngmap: NgMap | None = None,
+                      cycle_log: np.ndarray | None = None) -> tuple[np.ndarray, SpecStats]:
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.zeros(n_gen, dtype=np.int32)
-        cfg = SpecCfg(n_key, max_draft, min_draft, cooldown, max_cycles, mtp)
+        cfg = spec_cfg(n_key, max_draft, min_draft, cooldown, max_cycles, mtp, ngmap, cycle_log)
         st = SpecStats()
         n = host_lib().cwen_generate_spec(self.h, p.ctypes.data, p.size, n_gen, C.byref(cfg), out.ctypes.data,
                                           C.byref(st))

@@ -756,3 +756,73 @@ int cwen_model_load_gguf(cwen_model *m, const cwen_model_cfg *c, const cwen_gguf
   g_err[0] = 0;
   return CWEN_OK;
 }
+
+/* The model geometry from the shapes of the tensors cwen_model_load_gguf
+ * binds.  The reference compiles its geometry in (run.c:83-91) and pins
+ * every shape to it at load; read back from the shapes of its own model
+ * file, this gives those constants.  RoPE (64 rotated dimensions, theta
+ * 1e7) and the norm epsilon (1e-6) leave no trace in the shapes and are the
+ * reference's values. */
+static int dim_of(const cwen_gguf *g, const char *name, int which, int *out) {
+  const int i = cwen_gguf_find(g, name);
+  if (i < 0) {
+    char m[160];
+    snprintf(m, sizeof m, "geometry: missing %.100s", name);
+    return fail(m);
+  }
+  *out = which ? g->t[i].ne1 : g->t[i].ne0;
+  return CWEN_OK;
+}
+
+int cwen_model_cfg_from_gguf(const cwen_gguf *g, int max_ctx, cwen_model_cfg *c) {
+  if (!g || !c) return fail("null argument");
+  memset(c, 0, sizeof *c);
+  char n[G_NAME];
+  int rc, nl = 0, first_full = -1, first_linear = -1, qkv = 0, qrows = 0, krows = 0;
+  if ((rc = dim_of(g, "token_embd.weight", 0, &c->d_model)) || (rc = dim_of(g, "token_embd.weight", 1, &c->vocab)))
+    return rc;
+  for (;; nl++) {
+    snprintf(n, sizeof n, "blk.%d.attn_norm.weight", nl);
+    if (cwen_gguf_find(g, n) < 0) break;
+    snprintf(n, sizeof n, "blk.%d.nextn.eh_proj.weight", nl);
+    if (cwen_gguf_find(g, n) >= 0) break;   /* the MTP block follows the decoder layers */
+    snprintf(n, sizeof n, "blk.%d.attn_q.weight", nl);
+    const int full = cwen_gguf_find(g, n) >= 0;
+    if (full && first_full < 0) first_full = nl;
+    if (!full && first_linear < 0) first_linear = nl;
+  }
+  if (nl < 1) return fail("geometry: no decoder layers (blk.0.attn_norm.weight)");
+  if (first_full < 0) return fail("geometry: no full-attention layer (blk.N.attn_q.weight)");
+  c->n_layers = nl;
+  c->full_interval = first_full + 1;
+  if ((rc = dim_of(g, "blk.0.ffn_down.weight", 0, &c->d_ffn))) return rc;
+  const int f = first_full;
+#define DIM(fmt, l, which, dst)                          \
+  do {                                                   \
+    snprintf(n, sizeof n, fmt, l);                       \
+    if ((rc = dim_of(g, n, which, dst))) return rc;      \
+  } while (0)
+  DIM("blk.%d.attn_q_norm.weight", f, 0, &c->head_dim);
+  DIM("blk.%d.attn_q.weight", f, 1, &qrows);
+  DIM("blk.%d.attn_k.weight", f, 1, &krows);
+  if (c->head_dim < 1 || qrows % (2 * c->head_dim) || krows % c->head_dim)
+    return fail("geometry: attention rows are not whole heads");
+  c->n_head = qrows / (2 * c->head_dim);
+  c->n_kv_head = krows / c->head_dim;
+  if (first_linear >= 0) {
+    DIM("blk.%d.ssm_norm.weight", first_linear, 0, &c->gdn_dk);
+    DIM("blk.%d.ssm_alpha.weight", first_linear, 1, &c->gdn_nvh);
+    DIM("blk.%d.attn_qkv.weight", first_linear, 1, &qkv);
+    const int kd = qkv - c->gdn_nvh * c->gdn_dk;
+    if (c->gdn_dk < 1 || kd < 0 || kd % (2 * c->gdn_dk)) return fail("geometry: GatedDeltaNet rows are not whole heads");
+    c->gdn_nkh = kd / (2 * c->gdn_dk);
+  }
+#undef DIM
+  c->n_rot = 64;
+  c->n_rot_pairs = 32;
+  c->rope_theta = 1e7f;
+  c->rms_eps = 1e-6f;
+  c->max_ctx = max_ctx;
+  g_err[0] = 0;
+  return CWEN_OK;
+}

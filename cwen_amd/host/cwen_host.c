@@ -1,5 +1,6 @@
 /* Host decode drivers over the cwen_gpu C ABI (see cwen_host.h). */
 #define _POSIX_C_SOURCE 199309L
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
@@ -21,6 +22,10 @@ void cwen_spec_default(cwen_spec_cfg *cfg) {
   cfg->cooldown = 8;
   cfg->max_cycles = 0;
   cfg->mtp = 1;
+  cfg->ngmap = NULL;
+  cfg->cycle_log = NULL;
+  cfg->cycle_log_cap = 0;
+  cfg->debug = 0;
 }
 
 /* run.c:4533-4549 */
@@ -85,12 +90,24 @@ int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_g
   return n;
 }
 
-int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen, const cwen_spec_cfg *cfg_in,
-                       int *out, cwen_spec_stats *stats) {
-  if (!m || !out || n_gen < 0) return CWEN_EINVAL;
+/* What the speculative loop needs of a model. */
+typedef struct {
+  void *ud;
+  int (*prefill)(void *ud, const int *prompt, int n_prompt, int *next);
+  int (*pos)(void *ud);
+  int (*capacity)(void *ud);
+  int (*verify)(void *ud, const int *blk, int B, int *k, int *bonus);
+  int (*mtp_draft)(void *ud, int pend, int n, int *out);   /* NULL: no MTP block */
+} spec_model;
+
+/* generate_tokens_spec (run.c:4882-5025) over m. */
+static int spec_loop(const spec_model *M, const int *prompt, int n_prompt, int n_gen, const cwen_spec_cfg *cfg_in,
+                     int *out, cwen_spec_stats *stats) {
+  if (!out || n_gen < 0 || !prompt || n_prompt < 1) return CWEN_EINVAL;
   cwen_spec_cfg cfg;
   if (cfg_in) cfg = *cfg_in; else cwen_spec_default(&cfg);
   if (cfg.max_draft > CWEN_BMAX - 1) cfg.max_draft = CWEN_BMAX - 1;
+  if (cfg.ngmap && cwen_ngmap_n_key(cfg.ngmap) != cfg.n_key) return CWEN_EINVAL;
   cwen_spec_stats st;
   memset(&st, 0, sizeof st);
   st.prefill_tokens = n_prompt;
@@ -98,23 +115,24 @@ int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen
   if (!hist) return CWEN_ENOMEM;
   int pend, rc;
   double t0 = now_s();
-  if ((rc = cwen_prefill(m, prompt, n_prompt, &pend))) { free(hist); return rc; }
+  if ((rc = M->prefill(M->ud, prompt, n_prompt, &pend))) { free(hist); return rc; }
   double t1 = now_s();
   st.prefill_s = t1 - t0;
   memcpy(hist, prompt, sizeof(int) * (size_t)n_prompt);
-  const int cap = cwen_model_capacity(m);
-  int hn = n_prompt, g = 0, streak = 0, cool = 0, fa_streak = 0;
-  if (n_gen > 0 && cwen_model_pos(m) + 1 < cap) {
+  const int cap = M->capacity(M->ud);
+  int hn = n_prompt, g = 0, streak = 0, cool = 0, fa_streak = 0, upd = 0;
+  if (n_gen > 0 && M->pos(M->ud) + 1 < cap) {
     hist[hn++] = pend;
     out[g++] = pend;
   }
+  if (cfg.ngmap) { cwen_ngmap_update_range(cfg.ngmap, hist, upd, hn); upd = hn; }
   const int cap_hard = cfg.max_draft;
-  const int use_mtp = cfg.mtp && cwen_model_has_mtp(m) == 1;
+  const int use_mtp = cfg.mtp && M->mtp_draft;
   int E_cap = cap_hard;
-  int blk[CWEN_BMAX];
+  int blk[CWEN_BMAX], scan[CWEN_BMAX];
   while (g > 0 && g < n_gen) {
     if (cfg.max_cycles > 0 && st.cycles >= cfg.max_cycles) break;
-    const int pos = cwen_model_pos(m);
+    const int pos = M->pos(M->ud);
     if (pos + 1 >= cap) break;                     /* same context cap as the serial loop */
     int E = 0;
     if (cool > 0) {
@@ -123,17 +141,31 @@ int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen
       const int room = cap - 1 - (pos + 1);        /* block slots must stay in range */
       const int lim = E_cap < room ? E_cap : room;
       if (use_mtp) {
-        E = cwen_model_mtp_draft(m, hist[hn - 1], lim, blk + 1, NULL);
+        E = M->mtp_draft(M->ud, hist[hn - 1], lim, blk + 1);
         if (E < 0) { free(hist); return E; }
       } else {
-        E = cwen_ngram_draft(hist, hn, blk + 1, cfg.n_key, lim);
+        /* the map's chained lookups first; the history scan wins when it
+         * proposes a longer run */
+        E = cfg.ngmap ? cwen_ngmap_draft(cfg.ngmap, hist, hn, blk + 1, lim) : 0;
+        const int esc = cwen_ngram_draft(hist, hn, scan, cfg.n_key, lim);
+        if (esc > E) {
+          E = esc;
+          memcpy(blk + 1, scan, sizeof(int) * (size_t)E);
+        }
       }
       if (E && E < cfg.min_draft) E = 0;
     }
     blk[0] = hist[hn - 1];                         /* pend */
+    if (cfg.debug)
+      fprintf(stderr, "spec cycle %lld: history %d, position %d, drafts %d, pending %d\n", st.cycles, hn, pos, E,
+              blk[0]);
     int k = 0, bonus;
+    if ((rc = M->verify(M->ud, blk, E + 1, &k, &bonus))) { free(hist); return rc; }
+    if (cfg.cycle_log && st.cycles < cfg.cycle_log_cap) {
+      cfg.cycle_log[2 * st.cycles] = E;
+      cfg.cycle_log[2 * st.cycles + 1] = k;
+    }
     st.cycles++;
-    if ((rc = cwen_model_verify(m, blk, E + 1, &k, &bonus, NULL))) { free(hist); return rc; }
     if (E > 0) {
       st.drafted++;
       st.kept += k;
@@ -148,6 +180,7 @@ int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen
     }
     for (int i = 0; i < k; i++) hist[hn++] = blk[i + 1];
     hist[hn++] = bonus;
+    if (cfg.ngmap) { cwen_ngmap_update_range(cfg.ngmap, hist, upd, hn); upd = hn; }
     for (int i = 0; i < k && g < n_gen; i++) out[g++] = blk[i + 1];
     if (g >= n_gen) break;
     out[g++] = bonus;
@@ -156,6 +189,65 @@ int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen
   }
   st.decode_s = now_s() - t1;
   free(hist);
+  if (cfg.debug)
+    fprintf(stderr, "spec: %lld passes, %lld with drafts (%lld kept whole, %lld cut short), %.2f drafts kept on "
+                    "average\n", st.cycles, st.drafted, st.full, st.rejected,
+            st.drafted ? (double)st.kept / (double)st.drafted : 0.0);
   if (stats) *stats = st;
   return g;
+}
+
+/* ---- the device model ---- */
+static int dev_prefill(void *ud, const int *p, int n, int *next) { return cwen_prefill((cwen_model *)ud, p, n, next); }
+static int dev_pos(void *ud) { return cwen_model_pos((cwen_model *)ud); }
+static int dev_capacity(void *ud) { return cwen_model_capacity((cwen_model *)ud); }
+static int dev_verify(void *ud, const int *blk, int B, int *k, int *bonus) {
+  return cwen_model_verify((cwen_model *)ud, blk, B, k, bonus, NULL);
+}
+static int dev_mtp_draft(void *ud, int pend, int n, int *out) {
+  return cwen_model_mtp_draft((cwen_model *)ud, pend, n, out, NULL);
+}
+
+int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen, const cwen_spec_cfg *cfg,
+                       int *out, cwen_spec_stats *stats) {
+  if (!m) return CWEN_EINVAL;
+  const spec_model M = {m, dev_prefill, dev_pos, dev_capacity, dev_verify,
+                        cwen_model_has_mtp(m) == 1 ? dev_mtp_draft : NULL};
+  return spec_loop(&M, prompt, n_prompt, n_gen, cfg, out, stats);
+}
+
+/* ---- a recorded greedy stream ---- */
+typedef struct {
+  const int *s;
+  int n, n_prompt, max_ctx, pos;   /* pos: last filled position */
+} replay_model;
+
+static int rp_prefill(void *ud, const int *p, int n, int *next) {
+  replay_model *r = (replay_model *)ud;
+  if (n != r->n_prompt || n >= r->n || memcmp(p, r->s, sizeof(int) * (size_t)n) != 0) return CWEN_EINVAL;
+  r->pos = n - 1;
+  *next = r->s[n];
+  return CWEN_OK;
+}
+static int rp_pos(void *ud) { return ((replay_model *)ud)->pos; }
+static int rp_capacity(void *ud) { return ((replay_model *)ud)->max_ctx; }
+static int rp_verify(void *ud, const int *blk, int B, int *k, int *bonus) {
+  replay_model *r = (replay_model *)ud;
+  /* blk[b] sits at position pos + 1 + b; the greedy id after it is s[pos + 2 + b] */
+  const int p = r->pos + 1;
+  if (B < 1 || p + B >= r->n || blk[0] != r->s[p]) return CWEN_EINVAL;
+  int kk = 0;
+  while (kk < B - 1 && blk[kk + 1] == r->s[p + 1 + kk]) kk++;
+  *k = kk;
+  *bonus = r->s[p + 1 + kk];
+  r->pos = p + kk;
+  return CWEN_OK;
+}
+
+int cwen_spec_replay(const int *stream, int n_stream, int n_prompt, int n_gen, int max_ctx,
+                     const cwen_spec_cfg *cfg, int *out, cwen_spec_stats *stats) {
+  if (!stream || n_prompt < 1 || n_stream <= n_prompt || max_ctx < 2) return CWEN_EINVAL;
+  replay_model r = {stream, n_stream, n_prompt, max_ctx, -1};
+  const spec_model M = {&r, rp_prefill, rp_pos, rp_capacity, rp_verify, NULL};
+  return spec_loop(&M, stream, n_prompt, n_gen, cfg, out, stats);
 }

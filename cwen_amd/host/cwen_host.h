@@ -15,6 +15,47 @@
 extern "C" {
 #endif
 
+/* ---- counted n-gram map (cwen_ngram.c) ----
+ * The reference's NGMap (run.c:204-221, 4552-4723): a key of n_key confirmed
+ * tokens -> the token that last followed it and a hit count, in an
+ * open-addressed table of cap entries (a power of two; the reference's is
+ * 1 << 18).  A full table evicts one least-hit entry to admit a new key.
+ * The hash, probe and eviction order are the reference's, so the same
+ * updates leave the same entries in the same slots. */
+typedef struct cwen_ngmap cwen_ngmap;
+#define CWEN_NGMAP_CAP ((size_t)1 << 18)
+/* n_key in [1, 256]; vocab is recorded in saved files; cap 0 means
+ * CWEN_NGMAP_CAP. */
+int cwen_ngmap_create(int n_key, int vocab, size_t cap, cwen_ngmap **out);
+void cwen_ngmap_free(cwen_ngmap *m);
+int cwen_ngmap_n_key(const cwen_ngmap *m);
+size_t cwen_ngmap_used(const cwen_ngmap *m);
+/* Entries evicted so far, and how many of those evictions shifted no entry
+ * back into the freed slot. */
+void cwen_ngmap_evictions(const cwen_ngmap *m, size_t *evicted, size_t *in_place);
+/* ng_update_key_n (run.c:4579-4593): add hits to key's count (saturating at
+ * INT_MAX) and make tok its continuation, inserting the key if absent. */
+void cwen_ngmap_update(cwen_ngmap *m, const int *key, int tok, int hits);
+/* ng_update_range (run.c:4631-4637): every position p in [a, b) with
+ * p >= n_key adds key h[p - n_key .. p) -> h[p]. */
+void cwen_ngmap_update_range(cwen_ngmap *m, const int *h, int a, int b);
+/* ng_draft_map (run.c:4639-4654): chained lookups from the last n_key
+ * history tokens, up to max_d ids into out.  Returns the count. */
+int cwen_ngmap_draft(const cwen_ngmap *m, const int *h, int hn, int *out, int max_d);
+/* ng_save (run.c:4659-4678): write the NGC2 file {magic "NGC2", n_key,
+ * vocab, entries} then {key, tok, count} per entry in slot order, through
+ * path.tmp and a rename.  CWEN_OK or CWEN_EIO (nothing written). */
+int cwen_ngmap_save(const cwen_ngmap *m, const char *path);
+/* ng_load (run.c:4683-4723): merge the entries of an NGC2 file (counts add
+ * to live ones).  A missing file, a short or foreign header, or another
+ * n_key or vocab leaves the map as it is and returns 0; records with a token
+ * outside [0, vocab) or a count below 1 are skipped; reading stops at a cut
+ * record or a full map.  Returns the number of entries merged. */
+int cwen_ngmap_load(cwen_ngmap *m, const char *path);
+/* Copy the table (keys [cap][n_key], tokens, counts, in-use flags; any may
+ * be NULL) for inspection. */
+int cwen_ngmap_dump(const cwen_ngmap *m, int *keys, int *tok, int *cnt, unsigned char *used);
+
 /* Speculation knobs (run.c:193-198 Scfg_*). */
 typedef struct {
   int n_key;       /* n-gram lookup key length (16)            */
@@ -24,6 +65,16 @@ typedef struct {
   int max_cycles;  /* stop after this many verify cycles (0: no limit) */
   int mtp;         /* draft with the model's MTP block when it has one,
                       else the n-gram drafter (1; run.c CWEN_MTP)      */
+  cwen_ngmap *ngmap; /* counted n-gram map (NULL: none).  Learns from the
+                      history as it grows whatever the drafter; the n-gram
+                      drafter asks it first and keeps the history scan's
+                      proposal when that is longer (run.c:4900, 4925-4931,
+                      5003).  Its n_key must equal n_key.  It persists
+                      across calls, as the reference's does across frames. */
+  int *cycle_log;  /* when non-NULL, cycle c < cycle_log_cap stores its
+                      draft count E at [2c] and kept drafts k at [2c + 1] */
+  int cycle_log_cap;
+  int debug;       /* one line per cycle on stderr (run.c CWEN_SPEC_DEBUG) */
 } cwen_spec_cfg;
 
 typedef struct {
@@ -57,6 +108,17 @@ int cwen_generate_serial(cwen_model *m, const int *prompt, int n_prompt, int n_g
  * the model has one, else from the n-gram drafter. */
 int cwen_generate_spec(cwen_model *m, const int *prompt, int n_prompt, int n_gen, const cwen_spec_cfg *cfg,
                        int *out, cwen_spec_stats *stats);
+
+/* The speculative driver of cwen_generate_spec run against a recorded
+ * greedy stream instead of a model, on the host: stream[0 .. n_stream) is
+ * the prompt (its first n_prompt ids) followed by what greedy decode emits
+ * after it, and a verify block keeps each draft while it equals the stream's
+ * next id.  The drafts, the draft sizing, the cycle count and the output are
+ * those the driver produces on a model whose greedy decode is that stream;
+ * max_ctx plays the model's capacity.  The n-gram drafter is used (cfg->mtp
+ * is ignored).  CWEN_EINVAL when a block reaches past the stream. */
+int cwen_spec_replay(const int *stream, int n_stream, int n_prompt, int n_gen, int max_ctx,
+                     const cwen_spec_cfg *cfg, int *out, cwen_spec_stats *stats);
 
 /* ---- GGUF weights (cwen_gguf.c) ----
  * load_gguf (run.c:3188-3301): map a GGUF v2/v3 file read-only and read its
@@ -103,6 +165,15 @@ uint16_t cwen_f32_to_f16(float x);
  * is).  When blk.<n_layers>.nextn.eh_proj.weight is present the MTP nextn
  * block is bound too, every part required (run.c:3409-3464). */
 int cwen_model_load_gguf(cwen_model *m, const cwen_model_cfg *cfg, const cwen_gguf *g);
+/* The geometry cwen_model_load_gguf needs, read from g's tensor shapes:
+ * d_model and vocab from token_embd, the layer count up to the MTP block,
+ * the full-attention interval from the first layer with attn_q, head sizes
+ * and counts from the attention and GatedDeltaNet matrices.  RoPE (64
+ * dimensions, theta 1e7) and the norm epsilon 1e-6 are the reference's
+ * compiled values (run.c:83-91), which the shapes do not record.  max_ctx is
+ * the caller's.  CWEN_EINVAL when a tensor is missing or a size does not
+ * divide into heads (cwen_gguf_error names it). */
+int cwen_model_cfg_from_gguf(const cwen_gguf *g, int max_ctx, cwen_model_cfg *cfg);
 
 /* ---- binary-frame server (cwen_serve.c) ---- */
 #define CWEN_EIO (-7) /* a reply could not be written */

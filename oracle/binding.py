@@ -205,6 +205,17 @@ class Reference:
         L.ref_mtp_commit.restype = _I
         L.ref_mtp_commit.argtypes = [_I, _I, _VP, _VP]
         L.ref_snap_roundtrip.restype = _I
+        L.ref_ng_init.restype = _I
+        L.ref_ng_init.argtypes = [_I]
+        L.ref_ng_cap.restype = C.c_long
+        L.ref_ng_used.restype = C.c_long
+        L.ref_ng_update_key_n.argtypes = [_VP, _I, _I]
+        L.ref_ng_update_range.argtypes = [_VP, _I, _I]
+        L.ref_ng_draft_map.restype = _I
+        L.ref_ng_draft_map.argtypes = [_VP, _I, _VP, _I]
+        L.ref_ng_save.argtypes = [C.c_char_p]
+        L.ref_ng_load.argtypes = [C.c_char_p]
+        L.ref_ng_dump.argtypes = [_VP, _VP, _VP, _VP]
         self.L = L
         self._model_ctx = None
         self._bound = []   # tensors the reference's globals point into, kept alive
@@ -355,3 +366,42 @@ class Reference:
         """snap_save + snap_load over the whole model's GDN state."""
         if self.L.ref_snap_roundtrip():
             raise RuntimeError("ref_snap_roundtrip")
+
+    # ---- the counted n-gram map (run.c:4552-4723) on the reference's globals
+    def ng_init(self, n_key: int) -> None:
+        if self.L.ref_ng_init(n_key):
+            raise RuntimeError("ref_ng_init")
+        self._ng_key = n_key
+
+    def ng_update(self, key, tok: int, hits: int = 1) -> None:
+        k = np.ascontiguousarray(key, dtype=np.int32)
+        self.L.ref_ng_update_key_n(_i32p(k), int(tok), int(hits))
+
+    def ng_update_range(self, hist, a: int, b: int) -> None:
+        h = np.ascontiguousarray(hist, dtype=np.int32)
+        self.L.ref_ng_update_range(_i32p(h), a, b)
+
+    def ng_draft(self, hist, max_d: int) -> np.ndarray:
+        h = np.ascontiguousarray(hist, dtype=np.int32)
+        out = np.zeros(max(max_d, 1), dtype=np.int32)
+        n = self.L.ref_ng_draft_map(_i32p(h), h.size, _i32p(out), max_d)
+        return out[:n]
+
+    def ng_save(self, path) -> None:
+        self.L.ref_ng_save(str(path).encode())
+
+    def ng_load(self, path) -> None:
+        self.L.ref_ng_load(str(path).encode())
+
+    def ng_used(self) -> int:
+        return self.L.ref_ng_used()
+
+    def ng_dump(self) -> tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]:
+        """(keys [cap][n_key], tokens, counts, in-use flags) of the reference's table."""
+        cap = self.L.ref_ng_cap()
+        keys = np.zeros((cap, self._ng_key), np.int32)
+        tok = np.zeros(cap, np.int32)
+        cnt = np.zeros(cap, np.int32)
+        used = np.zeros(cap, np.uint8)
+        self.L.ref_ng_dump(keys.ctypes.data, tok.ctypes.data, cnt.ctypes.data, used.ctypes.data)
+        return keys, tok, cnt, used

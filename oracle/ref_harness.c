@@ -286,3 +286,38 @@ int ref_snap_roundtrip(void) {
   snap_load();
   return 0;
 }
+
+/* The counted n-gram map (run.c:204-221, 4552-4723) on the reference's own
+ * globals.  ref_ng_init allocates NGM at NG_CAP as alloc_state does with
+ * speculation on (run.c:3972-3978), with lookup key length n_key
+ * (Scfg_n_key), and rewinds the eviction hand; the map starts empty. */
+int ref_ng_init(int n_key) {
+  if (n_key < 1 || n_key > 256) return -1;
+  free(NGM.keys);
+  free(NGM.tok);
+  free(NGM.cnt);
+  free(NGM.used);
+  memset(&NGM, 0, sizeof NGM);
+  Scfg_n_key = n_key;
+  NG_evict_hand = 0;
+  NGM.cap = NG_CAP;
+  NGM.keys = malloc(sizeof(int) * NG_CAP * (size_t)n_key);
+  NGM.tok = malloc(sizeof(int) * NG_CAP);
+  NGM.cnt = calloc(NG_CAP, sizeof(int));
+  NGM.used = calloc(NG_CAP, 1);
+  return NGM.keys && NGM.tok && NGM.cnt && NGM.used ? 0 : -1;
+}
+long ref_ng_cap(void) { return (long)NG_CAP; }
+long ref_ng_used(void) { return (long)NGM.used_n; }
+void ref_ng_update_key_n(const int *key, int tok, int hits) { ng_update_key_n(key, tok, hits); }
+void ref_ng_update_range(const int *h, int a, int b) { ng_update_range(h, a, b); }
+int ref_ng_draft_map(const int *h, int hn, int *out, int max_d) { return ng_draft_map(h, hn, out, max_d); }
+void ref_ng_save(const char *path) { ng_save(path); }
+void ref_ng_load(const char *path) { ng_load(path); }
+/* Copy the table: keys [cap][n_key], tokens, counts, in-use flags. */
+void ref_ng_dump(int *keys, int *tok, int *cnt, unsigned char *used) {
+  memcpy(keys, NGM.keys, sizeof(int) * NGM.cap * (size_t)Scfg_n_key);
+  memcpy(tok, NGM.tok, sizeof(int) * NGM.cap);
+  memcpy(cnt, NGM.cnt, sizeof(int) * NGM.cap);
+  memcpy(used, NGM.used, NGM.cap);
+}

@@ -28,6 +28,7 @@ from cwen_amd import synth
 from util import rel_err
 
 pytestmark = pytest.mark.gpu
+CWEN_BMAX = 16
 
 CFG = dict(n_layers=4, d_model=1024, d_ffn=2048, vocab=4096, n_head=4, n_kv_head=2, head_dim=256,
            n_rot_pairs=32, n_rot=64, gdn_nkh=2, gdn_nvh=4, gdn_dk=128, full_interval=4, max_ctx=512,
@@ -304,6 +305,36 @@ def test_spec_decode_equals_serial(env, n_key):
     assert st.cycles <= n_gen
     if n_key <= 4:
         assert st.drafted > 0
+
+
+@pytest.mark.parametrize("use_map", [True, False])
+def test_spec_cycles_equal_replay_of_serial(env, use_map):
+    """The device speculative driver with the counted n-gram map: its drafts
+    and walk, cycle by cycle, equal the host replay of the same driver over
+    the model's own serial stream (cwen_spec_replay), which the CPU tests pin
+    to the reference's generate_tokens_spec.  So on the device, too, the
+    cycle count follows the reference, not only the tokens."""
+    gpu, ctx, m, _ = env
+    prompt = synth.prompt_tokens(6, 64, CFG["vocab"], period=11, noise=0.05)
+    n_gen = 120
+    # the stream runs a block past n_gen: the last cycle's walk reads that far
+    longer = m.generate_serial(prompt, n_gen + CWEN_BMAX)
+    serial = longer[:n_gen]
+    stream = np.concatenate([prompt, longer]).astype(np.int32)
+    logs = []
+    for replay in (False, True):
+        log = np.full(2 * 1024, -1, np.int32)
+        mp = gpu.NgMap(4, CFG["vocab"]) if use_map else None
+        cfg = gpu.spec_cfg(4, 8, 2, 8, 0, 0, mp, log)
+        if replay:
+            out, st = gpu.spec_replay(stream, prompt.size, n_gen, CFG["max_ctx"], cfg)
+        else:
+            out, st = m.generate_spec(prompt, n_gen, n_key=4, mtp=0, ngmap=mp, cycle_log=log)
+        assert np.array_equal(out, serial)
+        logs.append((log[:2 * st.cycles].copy(), [st.cycles, st.drafted, st.full, st.rejected, st.kept]))
+    assert np.array_equal(logs[0][0], logs[1][0])
+    assert logs[0][1] == logs[1][1]
+    assert logs[0][1][1] > 0
 
 
 def test_out_of_range_operand_is_reported(env):
