@@ -138,7 +138,8 @@ int check_cfg(const cwen_model_cfg *c) {
   if ((c->n_head * c->head_dim) % Q4_K_ALIGN) return CWEN_EINVAL;
   if (c->gdn_dk != 128 || c->gdn_nkh <= 0 || c->gdn_nvh % c->gdn_nkh || (c->gdn_nvh * 128) % Q4_K_ALIGN)
     return CWEN_EINVAL;
-  if (c->full_interval <= 0 || c->max_ctx < 2 || c->n_rot_pairs < 0 || 2 * c->n_rot_pairs > c->head_dim)
+  if (c->full_interval <= 0 || c->max_ctx < 2 || c->max_ctx > CWEN_CTX_MAX || c->n_rot_pairs < 0 ||
+      2 * c->n_rot_pairs > c->head_dim)
     return CWEN_EINVAL;
   return CWEN_OK;
 }

@@ -58,6 +58,8 @@ extern "C" {
 
 /* Largest verify block (SPEC_BMAX, run.c:192). */
 #define CWEN_BMAX 16
+/* Largest context (MAX_SEQ, run.c:85); cwen_model_create refuses more. */
+#define CWEN_CTX_MAX 32768
 
 typedef struct cwen_ctx cwen_ctx;        /* device, stream-independent scratch */
 typedef struct cwen_weight cwen_weight;  /* one device-resident weight matrix  */
@@ -214,7 +216,7 @@ typedef struct {
   int n_rot_pairs, n_rot;                     /* RoPE pairs (32) and NROT (64)   */
   int gdn_nkh, gdn_nvh, gdn_dk;               /* LKH, LVH, LSD (LSD must be 128) */
   int full_interval;                          /* FULL_INT                        */
-  int max_ctx;                                /* KV / position capacity          */
+  int max_ctx;                                /* KV / position capacity, 2..CWEN_CTX_MAX */
   float rope_theta, rms_eps;                  /* ROPE_THETA, RMS_EPS             */
 } cwen_model_cfg;
 typedef struct cwen_model cwen_model;

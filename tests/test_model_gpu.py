@@ -337,6 +337,31 @@ def test_spec_cycles_equal_replay_of_serial(env, use_map):
     assert logs[0][1][1] > 0
 
 
+def test_chunk_mapping_changes_no_bit(env):
+    """The attention's partials are per 32-key chunk and merged in chunk
+    order, so which workgroup computes a chunk cannot change a bit: with
+    max_ctx 4096 every chunk has a workgroup of its own, with 16384 the
+    workgroups loop over chunks (the stride path); a 4000-token prompt and
+    a verify block give bit-identical logits in both.  A context beyond
+    CWEN_CTX_MAX (32768, the reference's MAX_SEQ) is refused."""
+    gpu, ctx, m, tensors = env
+    prompt = synth.prompt_tokens(9, 4000, CFG["vocab"])
+    out = []
+    for max_ctx in (4096, 16384):
+        mm = gpu.Model(ctx, **{**CFG, "max_ctx": max_ctx})
+        for t in tensors:
+            mm.set(*t)
+        for i in range(0, prompt.size - 8, 16):
+            mm.forward(prompt[i:min(i + 16, prompt.size - 8)], want_argmax=False)
+        am = mm.forward(prompt[-8:])
+        out.append((am, mm.logits(8)))
+        mm.free()
+    assert np.array_equal(out[0][0], out[1][0])
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+    with pytest.raises(gpu.CwenError):
+        gpu.Model(ctx, **{**CFG, "max_ctx": 32769})
+
+
 def test_out_of_range_operand_is_reported(env):
     """The RMSNorm is split between producer and consumer, so the f16 operand
     holds a residual element times its norm weight before normalisation.
