@@ -103,3 +103,18 @@ def test_composition_catches_a_planted_mistake(oracle, tensors):
     OM = Broken(oracle, mg.CFG, tensors)
     x = OM.linear_layer(mg.LIN, mg.residuals(mg.N_LIN, 1)[0])
     assert rel_err(x, np.load(GOLDEN)["linear_x"][0]) > 100 * TOL
+
+
+def test_64_layer_fixture_is_consistent():
+    """tests/golden/model_64_layer_logits.npz holds run.c's own 64-layer chain
+    and the oracle composition on the same weights (written by
+    tests/golden/make_drift_golden.py): they agree within the composition's
+    tolerance over the whole depth, and rounding only the GEMV inputs to f16
+    moves the logits by less than the per-GEMV bound."""
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import make_drift_golden as dg
+    fx = np.load(dg.OUT)
+    for p in range(dg.N_POS):
+        assert rel_err(fx["logits_oracle"][p], fx["logits_ref"][p]) <= TOL
+        assert rel_err(fx["logits_f16_inputs"][p], fx["logits_ref"][p]) <= 1e-3
+

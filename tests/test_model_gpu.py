@@ -13,7 +13,9 @@ Checked:
     random-init model (position 14 of the 70-token case) rounding the inputs
     alone moves the oracle's own logits by 1.4e-2 -- in either direction,
     depending on how the roundings fall.  The second term allows exactly
-    that measured spread, nothing else.
+    that measured spread, and the whole bound is capped at 4e-2.  The fixed
+    1e-3 bound at the native dimensions over all 64 layers is
+    tests/test_model_drift_gpu.py's.
   * block == serial, bit for bit: one block of B positions gives the same
     logits as B single-position passes (the property spec == serial rests on).
   * verify with crafted drafts walks and rolls back exactly: accepted drafts
@@ -29,6 +31,7 @@ from util import rel_err
 
 pytestmark = pytest.mark.gpu
 CWEN_BMAX = 16
+TOL_CAP = 4e-2
 
 CFG = dict(n_layers=4, d_model=1024, d_ffn=2048, vocab=4096, n_head=4, n_kv_head=2, head_dim=256,
            n_rot_pairs=32, n_rot=64, gdn_nkh=2, gdn_nvh=4, gdn_dk=128, full_interval=4, max_ctx=512,
@@ -60,7 +63,7 @@ def _oracle_logits(oracle, tensors, toks):
     ref = np.stack([OM.step(t, p) for p, t in enumerate(toks)])
     O16 = OracleModel(oracle, CFG, tensors, f16_inputs=True)
     ref16 = np.stack([O16.step(t, p) for p, t in enumerate(toks)])
-    tol = np.array([1e-2 + 2 * rel_err(ref16[p], ref[p]) for p in range(len(toks))])
+    tol = np.array([min(1e-2 + 2 * rel_err(ref16[p], ref[p]), TOL_CAP) for p in range(len(toks))])
     return ref, tol
 
 
