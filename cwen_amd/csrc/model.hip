@@ -40,8 +40,25 @@ __device__ __forceinline__ float sum256(float v, float *red) {
 }
 __device__ __forceinline__ float f16f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
-// ---- embedding: Q4_0 (GGUF blocks) or Q4_0RS (split scales) rows, exact
-// f32 dequant w = (n - 8) * d.  Grid: B, 256 threads, thread = block.
+// ---- embedding: Q4_0 (GGUF blocks), Q4_0RS (split scales) or Q6_K rows,
+// exact f32 dequant: w = (n - 8) * d, or for Q6_K (d * sc) * (q6 - 32) in
+// the reference's order (run.c:1829-1848).  Grid: B, 256 threads, thread =
+// 32-weight block.
+__device__ __forceinline__ void embed_block_q6k(const uint8_t *row, int i, float *w) {
+  // block i = weights 32 i .. 32 i + 31 = quarter q of half h of super-block sb
+  const int sb = i >> 3, h = (i >> 2) & 1, q = i & 3;
+  const uint8_t *b = row + (size_t)sb * 210;
+  const uint8_t *ql = b + h * 64 + (q & 1) * 32, *qh = b + 128 + h * 32;
+  const int8_t *sc = (const int8_t *)(b + 192) + h * 8 + 2 * q;
+  const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(b[208] | (b[209] << 8)));
+  const int shift = q >= 2 ? 4 : 0;
+#pragma unroll 4
+  for (int l = 0; l < 32; ++l) {
+    const int v = ((ql[l] >> shift) & 0xF) | (((qh[l] >> (2 * q)) & 3) << 4);
+    w[l] = __fmul_rn(__fmul_rn(d, (float)sc[l >> 4]), (float)(v - 32));
+  }
+}
+
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uint16_t *sc, int type,
                                                     const int *toks, int H, float *X, int xs, float *ssq,
                                                     _Float16 *xh, const float *nw, int *rflag) {
@@ -51,19 +68,30 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uin
   const int nb = H / 32;
   float sq = 0.f;
   for (int i = threadIdx.x; i < nb; i += 256) {
-    const uint8_t *q;
-    float d;
-    if (type == CWEN_T_Q4_0) {
-      const uint8_t *blk = qs + (tok * nb + i) * 18;
-      d = f16f((uint16_t)(blk[0] | (blk[1] << 8)));
-      q = blk + 2;
+    float w[32];
+    if (type == CWEN_T_Q6_K) {
+      embed_block_q6k(qs + tok * (size_t)(H / 256) * 210, i, w);
     } else {
-      q = qs + (tok * nb + i) * 16;
-      d = f16f(sc[tok * nb + i]);
+      const uint8_t *q;
+      float d;
+      if (type == CWEN_T_Q4_0) {
+        const uint8_t *blk = qs + (tok * nb + i) * 18;
+        d = f16f((uint16_t)(blk[0] | (blk[1] << 8)));
+        q = blk + 2;
+      } else {
+        q = qs + (tok * nb + i) * 16;
+        d = f16f(sc[tok * nb + i]);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        w[j] = (float)((int)(q[j] & 0xF) - 8) * d;
+        w[j + 16] = (float)((int)(q[j] >> 4) - 8) * d;
+      }
     }
     float *dst = X + (size_t)b * xs + i * 32;
+#pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const float lo = (float)((int)(q[j] & 0xF) - 8) * d, hi = (float)((int)(q[j] >> 4) - 8) * d;
+      const float lo = w[j], hi = w[j + 16];
       dst[j] = lo;
       dst[j + 16] = hi;
       if (xh) {

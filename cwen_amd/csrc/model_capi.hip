@@ -731,13 +731,15 @@ int cwen_model_set(cwen_model *m, int layer, int id, int type, const void *data,
   CWEN_HIP_TRY(hipSetDevice(m->ctx->device));
   const bool f32 = type == CWEN_T_F32;
   if (id == CWEN_TOK_EMBD) {  // rows dequantised one token at a time (embed_token_to)
-    if ((type != CWEN_T_Q4_0 && type != CWEN_T_Q4_0RS) || ne0 != H || ne1 != c.vocab) return CWEN_EINVAL;
-    if (type == CWEN_T_Q4_0RS && !scales) return CWEN_EINVAL;
+    if ((type != CWEN_T_Q4_0 && type != CWEN_T_Q4_0RS && type != CWEN_T_Q6_K) || ne0 != H || ne1 != c.vocab)
+      return CWEN_EINVAL;
+    if ((type == CWEN_T_Q4_0RS && !scales) || (type == CWEN_T_Q6_K && H % 256)) return CWEN_EINVAL;
     const size_t nblk = (size_t)(H / 32) * c.vocab;
     if (m->emb_qs) (void)hipFree(m->emb_qs);
     if (m->emb_sc) (void)hipFree(m->emb_sc);
     m->emb_qs = nullptr; m->emb_sc = nullptr;
-    const size_t qb = type == CWEN_T_Q4_0 ? nblk * 18 : nblk * 16;
+    const size_t qb = type == CWEN_T_Q4_0 ? nblk * 18
+                    : type == CWEN_T_Q6_K ? (size_t)(H / 256) * 210 * c.vocab : nblk * 16;
     if (dmalloc(&m->emb_qs, qb)) return CWEN_ENOMEM;
     CWEN_HIP_TRY(hipMemcpy(m->emb_qs, data, qb, hipMemcpyHostToDevice));
     if (type == CWEN_T_Q4_0RS) {

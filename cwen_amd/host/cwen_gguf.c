@@ -629,7 +629,7 @@ int cwen_model_load_gguf(cwen_model *m, const cwen_model_cfg *c, const cwen_gguf
   const int Qo = c->n_head * c->head_dim, Ko = c->n_kv_head * c->head_dim;
   const gguf_tensor *t, *u;
   NEED(t, need(g, "token_embd.weight", &rc));
-  if (!q4_family(t->type)) return fail("token_embd.weight: the device embedding takes Q4_0");
+  if (!q4_family(t->type) && t->type != CWEN_T_Q6_K) return fail("token_embd.weight: the device embedding takes Q4_0 or Q6_K");
   if (t->ne0 != H || t->ne1 != V) return fail("token_embd.weight: shape");
   TRY(set_mat(m, -1, CWEN_TOK_EMBD, t));
   NEED(u, vec(g, "output_norm.weight", H, &rc));

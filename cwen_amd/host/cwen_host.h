@@ -160,7 +160,7 @@ uint16_t cwen_f32_to_f16(float x);
  * path uses, by the reference's names, with its shape pins, into model m
  * created with cfg.  ffn_gate/ffn_up and attn_k/attn_v (GGUF Q4_0) are
  * interleaved on the host into the device's pair form; output.weight falls
- * back to token_embd.weight (tied).  The embedding must be Q4_0.  Tensors a
+ * back to token_embd.weight (tied).  The embedding is Q4_0 or Q6_K.  Tensors a
  * sidecar rebound are uploaded from its views (an interleaved pair as it
  * is).  When blk.<n_layers>.nextn.eh_proj.weight is present the MTP nextn
  * block is bound too, every part required (run.c:3409-3464). */

@@ -224,7 +224,7 @@ typedef struct cwen_model cwen_model;
 /* Tensor ids of cwen_model_set, named after the GGUF tensors the reference
  * binds (run.c:3367-3406). */
 enum {
-  CWEN_TOK_EMBD = 0,     /* token_embd.weight      Q4_0 / Q4_0RS, [V][H]          */
+  CWEN_TOK_EMBD = 0,     /* token_embd.weight      Q4_0 / Q4_0RS / Q6_K, [V][H]   */
   CWEN_OUTPUT_NORM,      /* output_norm.weight     F32 [H]                        */
   CWEN_OUTPUT,           /* output.weight          any GEMV type, [V][H]          */
   CWEN_ATTN_NORM,        /* blk.l.attn_norm        F32 [H]                        */

@@ -56,7 +56,7 @@ class Oracle:
         L.orc_walk.argtypes = [_VP, C.c_long, _I, _VP, _I, C.POINTER(_I)]
         L.orc_ngram_draft.restype = _I
         L.orc_ngram_draft.argtypes = [_VP, _I, _VP, _I, _I]
-        L.orc_embed_q4.argtypes = [_VP, _VP, _I, _I, _I, _VP]
+        L.orc_embed.argtypes = [_VP, _VP, _I, _I, _I, _VP]
         L.orc_rope_apply.argtypes = [_VP, _I, _I, _I, _I, _I, _F]
         L.orc_attention.argtypes = [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _I, _VP]
         self.L = L
@@ -120,7 +120,7 @@ class Oracle:
 
     def embed(self, wtype: int, qs: np.ndarray, sc, token: int, H: int) -> np.ndarray:
         out = np.empty(H, dtype=np.float32)
-        self.L.orc_embed_q4(qs.ctypes.data, None if sc is None else sc.ctypes.data, wtype, token, H, _f32p(out))
+        self.L.orc_embed(qs.ctypes.data, None if sc is None else sc.ctypes.data, wtype, token, H, _f32p(out))
         return out
 
     def rope(self, q: np.ndarray, pos: int, npairs: int = 32, nrot: int = 64, theta: float = 1e7) -> np.ndarray:

@@ -353,8 +353,37 @@ int orc_ngram_draft(const int *h, int hn, int *out, int n_key, int max_d) {
   return best;
 }
 
-/* run.c:1849-1887 (Q4_0RS and Q4_0 branches) */
-void orc_embed_q4(const uint8_t *qs, const uint16_t *sc, int type, int token, int H, float *dst) {
+/* run.c:1829-1848 embed_q6_k: per 256-weight super-block {ql[128], qh[64],
+ * i8 scales[16], f16 d}, each half of 128 weights taking 64 ql bytes, 32 qh
+ * bytes and 8 scales; weight n0 + 32 q + l (quarter q, l < 32) is
+ * (d * sc[2q + l/16]) * (q6 - 32), the 6-bit value from the low (q = 0, 1)
+ * or high (q = 2, 3) nibble of ql[32 (q & 1) + l] and bits 2q, 2q+1 of qh[l]. */
+static void embed_q6_k_row(const uint8_t *row, int H, float *dst) {
+  for (int i = 0; i < H / 256; i++) {
+    const uint8_t *b = row + (size_t)i * 210;
+    const uint8_t *ql = b, *qh = b + 128;
+    const int8_t *sc = (const int8_t *)(b + 192);
+    const float d = orc_f16_to_f32(ld16(b + 208));
+    float *o = dst + (size_t)i * 256;
+    for (int n0 = 0; n0 < 256; n0 += 128) {
+      for (int l = 0; l < 32; l++) {
+        const int is = l / 16;
+        o[n0 + l] = d * sc[is + 0] * ((int8_t)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32);
+        o[n0 + l + 32] = d * sc[is + 2] * ((int8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32);
+        o[n0 + l + 64] = d * sc[is + 4] * ((int8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
+        o[n0 + l + 96] = d * sc[is + 6] * ((int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
+      }
+      ql += 64; qh += 32; sc += 8;
+    }
+  }
+}
+
+/* run.c:1849-1887 embed_token_to: the Q4_0RS, Q4_0 and Q6_K branches */
+void orc_embed(const uint8_t *qs, const uint16_t *sc, int type, int token, int H, float *dst) {
+  if (type == ORC_Q6_K) {
+    embed_q6_k_row(qs + (size_t)token * (H / 256) * 210, H, dst);
+    return;
+  }
   int nb = H / 32;
   for (int i = 0; i < nb; i++) {
     const uint8_t *q;

@@ -85,9 +85,10 @@ int orc_walk(const float *logits, long ls, int V, const int *drafts, int E, int 
 /* Prompt-lookup drafter (run.c:4533-4549). */
 int orc_ngram_draft(const int *h, int hn, int *out, int n_key, int max_d);
 
-/* run.c:1849-1887 embed_token_to for Q4_0 (18-byte blocks, scales NULL) and
- * Q4_0RS rows: dst[H] = ((n - 8) * d) of row `token`. */
-void orc_embed_q4(const uint8_t *qs, const uint16_t *sc, int type, int token, int H, float *dst);
+/* run.c:1849-1887 embed_token_to for Q4_0 (18-byte blocks, scales NULL),
+ * Q4_0RS rows ((n - 8) * d) and Q6_K rows (run.c:1829-1848, scales NULL):
+ * dst[H] of row `token`. */
+void orc_embed(const uint8_t *qs, const uint16_t *sc, int type, int token, int H, float *dst);
 
 /* run.c:1903-1948 rope_tables + rope_apply without YaRN: on each of n_heads
  * heads of hd floats, pairs (2i, 2i+1), i < npairs, rotate by

@@ -140,6 +140,46 @@ def test_real_model_types(env, oracle):
     m.free()
 
 
+def test_q6_k_embedding(env, oracle):
+    """A Q6_K token_embd (run.c:1882-1883).  (1) Forward parity vs the oracle
+    with a random Q6_K table, same tolerance as above.  (2) Exactness: a Q6_K
+    table built so every row dequantizes to the same f32 values as a Q4_0RS
+    table (d = 2^-12, equal scale pairs sc, q = n + 24, Q4_0RS scale sc * 2^-12)
+    gives the same logits, bit for bit, as that Q4_0RS table."""
+    from util import q6_k_pack
+    gpu, ctx, _, tensors = env
+    V, H = CFG["vocab"], CFG["d_model"]
+    rest = [t for t in tensors if not (t[0] == -1 and t[1] == gpu.TOK_EMBD)]
+    q6 = (-1, gpu.TOK_EMBD, gpu.T_Q6_K, synth.q6_k(9, V, H, key=77), None, H, V)
+    m = gpu.Model(ctx, **CFG)
+    for t in rest + [q6]:
+        m.set(*t)
+    toks = synth.prompt_tokens(8, 10, CFG["vocab"])
+    ref, tol = _oracle_logits(oracle, rest + [q6], toks)
+    m.forward(toks)
+    got = m.logits(len(toks))
+    for p in range(len(toks)):
+        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
+    # (2) the same values through both layouts
+    g = np.random.default_rng(10)
+    n = g.integers(0, 16, (V, H)).astype(np.uint8)
+    s32 = g.integers(1, 128, (V, H // 32))
+    qs_rs = (n.reshape(V, H // 32, 2, 16)[:, :, 0] | (n.reshape(V, H // 32, 2, 16)[:, :, 1] << 4)).astype(np.uint8)
+    sc_rs = (s32 * 2.0 ** -12).astype(np.float16).view(np.uint16)
+    assert np.array_equal(sc_rs.view(np.float16).astype(np.float64), s32 * 2.0 ** -12)
+    packed = q6_k_pack(n + 24, np.repeat(s32, 2, axis=1).astype(np.int8),
+                       np.full((V, H // 256), np.float16(2.0 ** -12)).view(np.uint16))
+    logits = {}
+    for name, t in (("rs", (-1, gpu.TOK_EMBD, gpu.T_Q4_0RS, qs_rs.reshape(-1), sc_rs.reshape(-1), H, V)),
+                    ("q6", (-1, gpu.TOK_EMBD, gpu.T_Q6_K, packed.reshape(-1), None, H, V))):
+        m.set(*t)
+        m.reset()
+        m.forward(toks)
+        logits[name] = m.logits(len(toks))
+    assert np.array_equal(logits["rs"].view(np.uint32), logits["q6"].view(np.uint32))
+    m.free()
+
+
 def test_gguf_load_equals_set(env, tmp_path):
     """cwen_model_load_gguf on a GGUF file written from the synthetic model
     (the reference's tensor names, GGUF Q4_0 matrices with gate/up and k/v as

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from cwen_amd import synth
-from util import rel_err
+from util import q6_k_pack, rel_err
 
 T_Q4_0, T_Q4_1, T_Q8_0, T_Q5_K, T_Q6_K, T_RS, T_RSI = 2, 3, 8, 13, 14, 101, 102
 
@@ -378,6 +378,41 @@ def test_embed_vs_reference_and_closed_form(oracle, ref_avx2):
     gfull = np.zeros((V, H // 32 * 18), np.uint8)
     gfull[:64] = g.reshape(64, -1)
     assert np.array_equal(oracle.embed(2, gfull, None, 5, H), ref_avx2.embed(2, gfull, None, 5))
+
+
+def test_embed_q6_k_vs_reference_and_gemv(oracle, ref_avx2):
+    """Q6_K embedding rows (run.c:1829-1848, 1882-1883) against run.c's own
+    embed_token_to, and against the Q6_K GEMV already pinned to run.c: a
+    row's embedding dotted with a one-hot x is that row's weight, so the
+    two unpackings of the same super-blocks must agree element for element."""
+    from cwen_amd import synth
+    V = ref_avx2.vocab
+    H = 5120
+    rows = synth.q6_k(0, 64, H, key=17)
+    full = np.zeros((V, H // 256 * 210), np.uint8)
+    full[:64] = rows.reshape(64, -1)
+    for tok in (0, 9, 63):
+        a = oracle.embed(T_Q6_K, full, None, tok, H)
+        assert np.array_equal(a, ref_avx2.embed(T_Q6_K, full, None, tok))
+    # closed form in natural order, from values packed by an independent
+    # writer of the layout: (d * sc) * (q - 32)
+    g = np.random.default_rng(5)
+    q6 = g.integers(0, 64, (3, H)).astype(np.uint8)
+    sc = g.integers(-128, 128, (3, H // 16)).astype(np.int8)
+    d = np.abs(g.standard_normal((3, H // 256)) * 0.01).astype(np.float16)
+    packed = np.zeros((V, H // 256 * 210), np.uint8)
+    packed[:3] = q6_k_pack(q6, sc, d.view(np.uint16))
+    for r in range(3):
+        want = (np.repeat(d[r].astype(np.float32), 256) * np.repeat(sc[r].astype(np.float32), 16)) \
+            * (q6[r].astype(np.float32) - 32)
+        assert np.array_equal(oracle.embed(T_Q6_K, packed, None, r, H), want)
+    tok = 9
+    a = oracle.embed(T_Q6_K, full, None, tok, H)
+    for k in (0, 31, 32, 100, 127, 128, 200, 255, 256, 4097, H - 1):
+        x = np.zeros(H, np.float32)
+        x[k] = 1.0
+        y = oracle.gemvb(T_Q6_K, full[:64].reshape(-1), None, H, 64, x[None])
+        assert y[0, tok] == a[k], (k, y[0, tok], a[k])
 
 
 @pytest.mark.parametrize("pos", [0, 1, 17, 4095, 8191])
