@@ -178,7 +178,10 @@ int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *sc
   *out = nullptr;
   const int fmt = gemv_fmt_of(type);
   if (fmt < 0) return CWEN_ETYPE;
-  if (ne0 % Q4_K_ALIGN || ne0 > CWEN_KMAX) return CWEN_EINVAL;
+  // K: whole blocks, as the reference's row_bytes (run.c:1293-1306) -- 32
+  // weights, 256 for the K-quants; the last super-tile is zero-padded.
+  const int kq = (type == CWEN_T_Q6_K || type == CWEN_T_Q5_K) ? 256 : 32;
+  if (ne0 % kq || ne0 > CWEN_KMAX) return CWEN_EINVAL;
   const bool split_scales = (type == CWEN_T_Q4_0RS || type == CWEN_T_Q4_0RSI);
   if (split_scales && !scales) return CWEN_EINVAL;
   CWEN_HIP_TRY(hipSetDevice(ctx->device));
@@ -205,7 +208,7 @@ int cwen_weight_upload(cwen_ctx *ctx, int type, const void *data, const void *sc
   w->ne1 = ne1;
   w->nside = nside;
   w->nrg = (ne1 + Q4_ROWS - 1) / Q4_ROWS;
-  w->nst = ne0 / Q4_ST_K;
+  w->nst = (ne0 + Q4_ST_K - 1) / Q4_ST_K;
   w->bytes = (size_t)w->nrg * w->nst * nside * gemv_st_bytes(fmt);
   if (w->bytes >= ((size_t)1 << 32)) {  // kernels address weights with 32-bit buffer offsets
     free(w);

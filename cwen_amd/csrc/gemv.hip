@@ -62,6 +62,8 @@
 namespace {
 
 constexpr int TILES = Q4_ST_TILES;  // tiles per round: one super-tile per stream
+// A per-lane buffer offset past any activation range: the load returns zeros.
+constexpr uint32_t kPastRange = 0xFFFFFFE0u;
 constexpr int WAVES = 4;            // waves per workgroup
 
 // K-run order inside a dword: the nibble unpack yields elements from nibbles
@@ -415,11 +417,19 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   uint32_t dq[PD] = {};       // Q6_K: f16 d of the round's two super-blocks
   constexpr int NHQ = (TW + 1) / 2;  // Q6_K: high-bit tile pairs of this wave
   uint4 hq[PD][NHQ];          // Q6_K: high bits of tile pairs (jb, jb+1) ...
-  auto stage_load = [&](uint32_t soff) __attribute__((always_inline)) {
+  // Staging of round r of this piece.  K need only be a multiple of 32: the
+  // last round's units past K (a lane's 8 elements lie wholly on one side)
+  // get a per-lane offset beyond the buffer range and load as zeros, so they
+  // meet the zero weights of the padded super-tile (never the next column's
+  // activations, which could be infinite).
+  auto stage_load = [&](uint32_t r) __attribute__((always_inline)) {
+    const uint32_t soff = r * xround;
+    const bool live = lane * 8 < p.K - (st0 + (int)r) * Q4_ST_K;
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
-      xs[i][0] = bload16(xr, xofs[i], soff);
-      if constexpr (XN) xs[i][1] = bload16(xr, xofs[i] + 16, soff);
+      const uint32_t vo = live ? xofs[i] : kPastRange;
+      xs[i][0] = bload16(xr, vo, soff);
+      if constexpr (XN) xs[i][1] = bload16(xr, vo + 16, soff);
     }
   };
   stage_load(0);
@@ -515,7 +525,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     sc[cur % PD] = sc_load(wofs + nw * sstride);
     if constexpr (FMT == GEMV_Q5K) h5[cur % PD] = h5_load(wofs + nw * sstride);
     if constexpr (FMT == GEMV_Q6K) dq[cur % PD] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs + nw * sstride, 0);
-    stage_load(nr * xround);
+    stage_load(nr);
     // LDS operands one tile ahead of their MFMAs: tile t + 1's reads are in
     // flight while tile t's products issue.
     half8_t an[4];
@@ -780,8 +790,8 @@ __global__ void repack_q4_kernel(uint8_t *dst, const uint8_t *src, const uint16_
   for (int u = 0; u < TILES; ++u) {
     const int blk = (st * TILES + u) * 4 + g;
     const uint8_t *qs = nullptr;
-    d[u] = m[u] = 0;  // rows past M: zero weights
-    if (row < M) {
+    d[u] = m[u] = 0;  // rows past M and blocks past K: zero weights
+    if (row < M && blk < nb) {
       const size_t bi = (size_t)row * nb + blk;
       if (type == CWEN_T_Q4_0) {
         const uint8_t *b = src + bi * 18;
@@ -855,7 +865,7 @@ __global__ void repack_q5k_kernel(uint8_t *dst, const uint8_t *src, int M, int K
   uint32_t hw[TILES], dm[TILES];
   for (int u = 0; u < TILES; ++u) {
     const int k0 = st * Q4_ST_K + u * Q4_TILE_K + g * 32;   // first K of the lane's sub-block
-    const uint8_t *b = (row < M) ? src + ((size_t)row * nsb + k0 / 256) * 176 : nullptr;
+    const uint8_t *b = (row < M && k0 < K) ? src + ((size_t)row * nsb + k0 / 256) * 176 : nullptr;
     const int sb = (k0 & 255) / 32, jj = sb / 2, hs = sb & 1;
     uint32_t lo[4] = {0, 0, 0, 0};
     hw[u] = 0;
@@ -907,7 +917,7 @@ __global__ void repack_q6k_kernel(uint8_t *dst, const uint8_t *src, int M, int K
   uint32_t hiw[TILES][2];
   for (int u = 0; u < TILES; ++u) {
     const int k0 = st * Q4_ST_K + u * Q4_TILE_K + g * 32;   // first K of the lane's block
-    const uint8_t *b = (row < M) ? src + ((size_t)row * nsb + k0 / 256) * 210 : nullptr;
+    const uint8_t *b = (row < M && k0 < K) ? src + ((size_t)row * nsb + k0 / 256) * 210 : nullptr;
     const int j0 = k0 & 255;
     uint32_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
     for (int m = 0; m < 4; ++m)
@@ -933,11 +943,11 @@ __global__ void repack_q6k_kernel(uint8_t *dst, const uint8_t *src, int M, int K
   scw.y = scb[4] | (scb[5] << 8) | (scb[6] << 16) | ((uint32_t)scb[7] << 24);
   *(uint2 *)(stile + F::SC_OFS + lane * 8) = scw;
   if (g == 0) {  // d of the super-tile's two super-blocks for row n
-    uint16_t d0 = 0, d1 = 0;
+    uint16_t d0 = 0, d1 = 0;   // super-blocks past K: zero
     if (row < M) {
       const uint8_t *b0 = src + ((size_t)row * nsb + st * 2) * 210;
       d0 = (uint16_t)(b0[208] | (b0[209] << 8));
-      d1 = (uint16_t)(b0[210 + 208] | (b0[210 + 209] << 8));
+      if (st * 2 + 1 < nsb) d1 = (uint16_t)(b0[210 + 208] | (b0[210 + 209] << 8));
     }
     *(uint32_t *)(stile + F::D_OFS + n * 4) = (uint32_t)d0 | ((uint32_t)d1 << 16);
   }
@@ -962,7 +972,7 @@ __global__ void repack_q8_kernel(uint8_t *dst, const uint8_t *src, int M, int K,
   uint16_t d[TILES];
   for (int u = 0; u < TILES; ++u) {
     const int blk = (st * TILES + u) * 4 + g;
-    const uint8_t *b = (row < M) ? src + ((size_t)row * nb + blk) * 34 : nullptr;
+    const uint8_t *b = (row < M && blk < nb) ? src + ((size_t)row * nb + blk) * 34 : nullptr;
     d[u] = b ? (uint16_t)(b[0] | (b[1] << 8)) : 0;
     uint8_t v[32];
     for (int k = 0; k < 32; ++k) v[k] = (uint8_t)((b ? (int)(int8_t)b[2 + k] : 0) + 128);

@@ -75,8 +75,11 @@ int cwen_ctx_destroy(cwen_ctx *ctx);
 
 /* Upload one weight matrix given in a reference layout in HOST memory and
  * repack it on the device into the tile layout the kernels stream.
- * Types: Q4_0, Q4_0RS, Q4_0RSI, Q6_K, Q8_0; ne0 (K) must be a multiple of 512
- * and at most CWEN_KMAX.
+ * Types: Q4_0, Q4_0RS, Q4_0RSI, Q4_1, Q8_0 (ne0 = K a multiple of 32) and
+ * Q6_K, Q5_K (K a multiple of 256), K at most CWEN_KMAX: whole blocks, as
+ * the reference's row_bytes requires (run.c:1293-1306).  The device tiles
+ * K in 512s; a last partial tile is padded with zero weights and the
+ * activations past K are read as zeros.
  * `data`/`scales` are what the reference's Tensor.data / Tensor.scales point
  * at (run.c:132): for Q4_0RS and Q4_0RSI `scales` is the f16 scale channel,
  * for the self-contained GGUF types it is NULL.  ne0 = K (inputs), ne1 = M

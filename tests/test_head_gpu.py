@@ -180,7 +180,7 @@ def test_head_argument_errors(env):
     with pytest.raises(gpu.CwenError):
         gpu.head_verify(ctx, W, X, 4, res, drafts=None, E=2)  # drafts missing
     with pytest.raises(gpu.CwenError):
-        gpu.Weight(ctx, T_Q6_K, synth.q6_k(0, 64, 256), None, 256, 64)  # K % 512
+        gpu.Weight(ctx, T_Q6_K, synth.q6_k(0, 64, 512), None, 384, 64)  # K not whole super-blocks
     gpu.head_verify(ctx, W, X, 4, res, drafts=d, E=3)
     torch.cuda.synchronize()
 

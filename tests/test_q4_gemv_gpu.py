@@ -169,7 +169,9 @@ def test_argument_errors(env):
         gpu.gemvb_swiglu(ctx, W, X, Y, 1)                  # needs a pair
     qs2, sc2 = synth.q4_rs(108, M, 96)
     with pytest.raises(gpu.CwenError):
-        gpu.Weight(ctx, T_RS, qs2, sc2, 96, M)             # K not a multiple of 512
+        gpu.Weight(ctx, T_RS, qs2, sc2, 80, M)             # K not whole 32-weight blocks
+    with pytest.raises(gpu.CwenError):
+        gpu.Weight(ctx, gpu.T_Q6_K, synth.q6_k(108, M, 512), None, 288, M)   # K-quant: whole 256s
     with pytest.raises(gpu.CwenError):
         gpu.Weight(ctx, 1, qs, sc, K, M)                   # F16 is not a supported type
 
@@ -269,3 +271,56 @@ def test_q5_k_parity(env, oracle, M, K):
             full = got
     one = _run(env, W, X[4:5])
     assert np.array_equal(one[0].view(np.uint32), full[4].view(np.uint32))
+
+
+RAGGED = [("rs", 32), ("rs", 96), ("rs", 544), ("rs", 5152), ("q4_0", 480), ("rsi", 1056), ("q8_0", 608),
+          ("q4_1", 800), ("q6_k", 256), ("q6_k", 768), ("q5_k", 1280)]
+
+
+@pytest.mark.parametrize("kind,K", RAGGED)
+def test_k_multiple_of_32(env, oracle, kind, K):
+    """K in whole blocks but not a multiple of the device's 512-wide tiles,
+    as the reference accepts (run.c:1293-1306): the last super-tile is
+    zero-padded and the activations past K read as zeros.  Parity vs the
+    oracle within TOL for B = 1, 5, 16, a column bit-identical alone and in
+    a block, and column 0 unaffected by an infinite first element of column
+    1 (which lies right after column 0's last element: a read past K would
+    turn column 0's padded products into NaN)."""
+    torch, gpu, ctx = env
+    M = 40
+    if kind == "rs":
+        data, sc = synth.q4_rs(111, M, K); wtype = T_RS
+    elif kind == "rsi":
+        data, sc = synth.q4_rsi(111, M, K); wtype = T_RSI
+    elif kind == "q4_0":
+        data, sc = synth.q4_gguf(111, M, K), None; wtype = T_Q4_0
+    elif kind == "q8_0":
+        data, sc = synth.q8_0(111, M, K), None; wtype = gpu.T_Q8_0
+    elif kind == "q4_1":
+        data, sc = synth.q4_1(111, M, K), None; wtype = gpu.T_Q4_1
+    elif kind == "q6_k":
+        data, sc = synth.q6_k(111, M, K), None; wtype = gpu.T_Q6_K
+    else:
+        data, sc = synth.q5_k(111, M, K), None; wtype = gpu.T_Q5_K
+    W = gpu.Weight(ctx, wtype, data, sc, K, M)
+    X = synth.activations(111, 16, K)
+    full = None
+    for B in (1, 5, 16):
+        got = _run(env, W, X[:B])
+        want = oracle.gemvb(wtype, data, sc, K, M, X[:B])
+        assert np.isfinite(got).all()
+        assert rel_err(got, want) <= TOL, (kind, K, B, rel_err(got, want))
+        if B == 16:
+            full = got
+    one = _run(env, W, X[11:12])
+    assert np.array_equal(one[0].view(np.uint32), full[11].view(np.uint32))
+    if kind == "rsi":
+        ya, yb = _run(env, W, X[:5], mode="pair")
+        wa, wb = oracle.gemvb(T_RSI, data, sc, K, M, X[:5], 0), oracle.gemvb(T_RSI, data, sc, K, M, X[:5], 1)
+        assert rel_err(ya, wa) <= TOL and rel_err(yb, wb) <= TOL
+        assert rel_err(_run(env, W, X[:5], mode="swiglu"), oracle.silu_mul(wa, wb)) <= TOL
+    Xi = X[:2].copy()
+    Xi[1, 0] = np.inf
+    got = _run(env, W, Xi)
+    assert np.isfinite(got[0]).all()
+    assert np.array_equal(got[0].view(np.uint32), full[0].view(np.uint32))
