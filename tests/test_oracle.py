@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 from cwen_amd import synth
+import dequant as D
 from util import q6_k_pack, rel_err
 
 T_Q4_0, T_Q4_1, T_Q8_0, T_Q5_K, T_Q6_K, T_RS, T_RSI = 2, 3, 8, 13, 14, 101, 102
@@ -46,33 +47,7 @@ def test_f32_to_f16_rne(oracle):
     assert oracle.L.orc_f32_to_f16(float("nan")) & 0x7e00 == 0x7e00
 
 
-# ---------------------------------------------------------------- dequant (numpy f64)
-def deq_q4_blocks(qs16: np.ndarray, d: np.ndarray) -> np.ndarray:
-    """[nblk,16] bytes + [nblk] f16 bits -> [nblk,32] float64 weights."""
-    lo = (qs16 & 0xF).astype(np.float64) - 8
-    hi = (qs16 >> 4).astype(np.float64) - 8
-    dd = d.view(np.float16).astype(np.float64)[:, None]
-    return np.concatenate([lo, hi], axis=1) * dd
-
-
-def deq_q6k(blk: np.ndarray, M: int, K: int) -> np.ndarray:
-    b = blk.reshape(-1, 210)
-    out = np.empty((b.shape[0], 256))
-    for s in range(b.shape[0]):
-        ql, qh = b[s, :128].astype(np.int32), b[s, 128:192].astype(np.int32)
-        sc = b[s, 192:208].view(np.int8).astype(np.float64)
-        d = float(b[s, 208:210].view(np.float16)[0])
-        for half in range(2):
-            L, Hh, S = ql[64 * half:64 * half + 64], qh[32 * half:32 * half + 32], sc[8 * half:8 * half + 8]
-            for l in range(32):
-                is_ = l // 16
-                q = [(L[l] & 0xF) | (((Hh[l] >> 0) & 3) << 4), (L[l + 32] & 0xF) | (((Hh[l] >> 2) & 3) << 4),
-                     (L[l] >> 4) | (((Hh[l] >> 4) & 3) << 4), (L[l + 32] >> 4) | (((Hh[l] >> 6) & 3) << 4)]
-                for j in range(4):
-                    out[s, 128 * half + l + 32 * j] = d * S[is_ + 2 * j] * (q[j] - 32)
-    return out.reshape(M, K)
-
-
+# ---------------------------------------------------------------- dequant (numpy f64, tests/dequant.py)
 SMALL = [(64, 256), (48, 512)]
 
 
@@ -80,7 +55,7 @@ SMALL = [(64, 256), (48, 512)]
 def test_q4_rs_vs_f64(oracle, M, K):
     qs, sc = synth.q4_rs(11, M, K)
     X = synth.activations(11, 3, K)
-    W = deq_q4_blocks(qs.reshape(-1, 16), sc).reshape(M, K)
+    W = D.rs(qs, sc, M, K)
     want = X.astype(np.float64) @ W.T
     got = oracle.gemvb(T_RS, qs, sc, K, M, X)
     assert rel_err(got, want) < 2e-6
@@ -92,31 +67,27 @@ def test_q4_rsi_vs_f64(oracle, side):
     qs, sc = synth.q4_rsi(12, M, K)
     X = synth.activations(12, 2, K)
     q1, s1 = synth.rsi_side(qs, sc, M, K, side)
-    W = deq_q4_blocks(q1.reshape(-1, 16), s1).reshape(M, K)
+    W = D.rs(q1, s1, M, K)
     got = oracle.gemvb(T_RSI, qs, sc, K, M, X, side=side)
     assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
 
 
 def test_q4_gguf_vs_f64(oracle):
     M, K = 32, 512
-    blk = synth.q4_gguf(13, M, K).reshape(-1, 18)
-    W = deq_q4_blocks(np.ascontiguousarray(blk[:, 2:]), np.ascontiguousarray(blk[:, :2]).view(np.uint16).ravel())
+    blk = synth.q4_gguf(13, M, K)
+    W = D.q4_0(blk, M, K)
     X = synth.activations(13, 2, K)
-    got = oracle.gemvb(T_Q4_0, blk.ravel(), None, K, M, X)
-    assert rel_err(got, X.astype(np.float64) @ W.reshape(M, K).T) < 2e-6
+    got = oracle.gemvb(T_Q4_0, blk, None, K, M, X)
+    assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
 
 
 def test_q4_1_vs_f64(oracle):
     """Q4_1 blocks {d, m, qs}: w = n*d + m, lo nibbles -> w[0..15], hi -> w[16..31]."""
     M, K = 24, 512
-    blk = synth.q4_1(16, M, K).reshape(-1, 20)
-    d = np.ascontiguousarray(blk[:, 0:2]).view(np.float16).astype(np.float64)
-    m = np.ascontiguousarray(blk[:, 2:4]).view(np.float16).astype(np.float64)
-    q = blk[:, 4:].astype(np.int64)
-    n = np.concatenate([q & 0xF, q >> 4], axis=1).astype(np.float64)
-    W = (n * d + m).reshape(M, K)
+    blk = synth.q4_1(16, M, K)
+    W = D.q4_1(blk, M, K)[0]
     X = synth.activations(16, 2, K)
-    got = oracle.gemvb(T_Q4_1, blk.ravel(), None, K, M, X)
+    got = oracle.gemvb(T_Q4_1, blk, None, K, M, X)
     assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
 
 
@@ -124,38 +95,26 @@ def test_q5_k_vs_f64(oracle):
     """Q5_K from the GGUF block definition in f64 (6-bit scale/min unpacking
     as ggml defines it, 5-bit quants split over qs nibbles and qh bits)."""
     M, K = 4, 512
-    blk = synth.q5_k(17, M, K).reshape(-1, 176)
-    W = np.empty((blk.shape[0], 256))
-    for s, b in enumerate(blk):
-        d, dmin = (float(v) for v in b[0:4].view(np.float16))
-        sc8, qh, qs = b[4:16].astype(np.int64), b[16:48].astype(np.int64), b[48:176].astype(np.int64)
-        sc = [sc8[j] & 63 if j < 4 else (sc8[j + 4] & 15) | ((sc8[j - 4] >> 6) << 4) for j in range(8)]
-        mn = [sc8[j + 4] & 63 if j < 4 else (sc8[j + 4] >> 4) | ((sc8[j] >> 6) << 4) for j in range(8)]
-        for jj in range(4):
-            for l in range(32):
-                for half in range(2):
-                    q = ((qs[32 * jj + l] >> (4 * half)) & 15) + 16 * ((qh[l] >> (2 * jj + half)) & 1)
-                    sb = 2 * jj + half
-                    W[s, 64 * jj + 32 * half + l] = d * sc[sb] * q - dmin * mn[sb]
+    blk = synth.q5_k(17, M, K)
+    W = D.q5_k(blk, M, K)[0]
     X = synth.activations(17, 2, K)
-    got = oracle.gemvb(T_Q5_K, blk.ravel(), None, K, M, X)
-    assert rel_err(got, X.astype(np.float64) @ W.reshape(M, K).T) < 2e-6
+    got = oracle.gemvb(T_Q5_K, blk, None, K, M, X)
+    assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
 
 
 def test_q8_0_vs_f64(oracle):
     M, K = 24, 256
-    blk = synth.q8_0(14, M, K).reshape(-1, 34)
-    d = np.ascontiguousarray(blk[:, :2]).view(np.float16).astype(np.float64)
-    W = (blk[:, 2:].view(np.int8).astype(np.float64) * d).reshape(M, K)
+    blk = synth.q8_0(14, M, K)
+    W = D.q8_0(blk, M, K)
     X = synth.activations(14, 2, K)
-    got = oracle.gemvb(T_Q8_0, blk.ravel(), None, K, M, X)
+    got = oracle.gemvb(T_Q8_0, blk, None, K, M, X)
     assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
 
 
 def test_q6_k_vs_f64(oracle):
     M, K = 6, 512
     blk = synth.q6_k(15, M, K)
-    W = deq_q6k(blk, M, K)
+    W = D.q6_k(blk, M, K)
     X = synth.activations(15, 2, K)
     got = oracle.gemvb(T_Q6_K, blk, None, K, M, X)
     assert rel_err(got, X.astype(np.float64) @ W.T) < 2e-6
@@ -452,3 +411,19 @@ def test_attention_vs_reference_and_f64(oracle, ref):
             p /= p.sum()
             want[h] = (p @ v) / (1 + np.exp(-gate[h].astype(np.float64)))
         assert rel_err(a, want) < 1e-5
+
+
+@pytest.mark.parametrize("kind", ["rs", "q4_0", "q8_0", "q4_1", "q5_k", "q6_k"])
+def test_elementwise_bound_has_teeth(kind):
+    """The GPU tests' element-wise bound (tests/elembound.py) is not
+    vacuous: exact outputs with one 32-weight block left out fall outside it
+    for about half of the elements or more (measured 52-81 %), and with a
+    single weight's sign flipped for a sixth or more (19-53 %)."""
+    from elembound import elem_bound, elem_case
+    K, M = (5120 if kind != "q5_k" else 6144), 256
+    _, _, _, _, W, A, cw = elem_case(kind, K, M)
+    X = synth.activations(121, 8, K).astype(np.float64)
+    bound = elem_bound(W, A, X, K, cw)
+    blk = slice(37 * 32, 38 * 32)
+    assert (np.abs(X[:, blk] @ W[:, blk].T) > bound).mean() > 0.45
+    assert (np.abs(2 * X[:, 100:101] * W[:, 100][None, :]) > bound).mean() > 0.15

@@ -324,3 +324,33 @@ def test_k_multiple_of_32(env, oracle, kind, K):
     got = _run(env, W, Xi)
     assert np.isfinite(got[0]).all()
     assert np.array_equal(got[0].view(np.uint32), full[0].view(np.uint32))
+
+
+ELEM_CASES = [("rs", 5120), ("rsi", 5120), ("q4_0", 5120), ("q8_0", 5120), ("q4_1", 5120), ("q5_k", 6144),
+              ("q6_k", 5120), ("rs", 17408)]
+
+
+@pytest.mark.parametrize("kind,K", ELEM_CASES)
+def test_elementwise_error_bound(env, kind, K):
+    """Every output element within a rounding bound of its own exact value
+    (float64 from the block definitions, tests/dequant.py, which the
+    oracle's tests pin) instead of a norm-wise tolerance; the bound and its
+    derivation are tests/elembound.py's.  The bound has teeth: leaving out
+    one 32-weight block breaks it for half of the elements or more, flipping
+    one weight's sign for a sixth or more (test_oracle.py's
+    test_elementwise_bound_has_teeth)."""
+    from elembound import elem_bound, elem_case
+    torch, gpu, ctx = env
+    M = 256
+    wtype, data, sc, side, Wx, A, cw = elem_case(kind, K, M)
+    W = gpu.Weight(ctx, wtype, data, sc, K, M)
+    X = synth.activations(121, 16, K)
+    X[:, ::97] *= 1e-6      # some activations below f16's normal range
+    worst = 0.0
+    for B in (1, 8, 16):
+        got = _run(env, W, X[:B], side=side).astype(np.float64)
+        exact = X[:B].astype(np.float64) @ Wx.T
+        r = np.abs(got - exact) / elem_bound(Wx, A, X[:B], K, cw)
+        assert (r <= 1).all(), (kind, K, B, float(r.max()))
+        worst = max(worst, float(r.max()))
+    print(f"{kind} K={K}: worst error / bound {worst:.3f}")
