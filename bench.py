@@ -154,6 +154,7 @@ C2_V = 151936
 C2_BYTES = C2_V * 20 * 210 + 8 * 5120 * 4 + 8 * C2_V * 4  # W + x + logits
 C3_BYTES = 29_445_632                                      # S + 8 snapshots + inputs + history + out
 F2_V = 248320                                              # the real model's vocabulary (run.c:84)
+C4_CPU_CTX = 4096                                          # context of the CPU verify-cycle sample
 F2_BYTES = F2_V * 20 * 210 + 8 * 5120 * 4 + 8 * F2_V * 4
 
 
@@ -428,7 +429,12 @@ def cpu_child(cfg: str, B: int, reps: int) -> None:
           reference's V with -inf;
       c3  conv1d_update + gdn_step for 8 positions of one layer
           (run.c:2183-2200, 2014-2180) + snap_save / snap_load of the whole
-          model's GDN state (run.c:2787-2809)."""
+          model's GDN state (run.c:2787-2809);
+      c4  the per-layer steps of forward_block at B=8 and context 4096 on the
+          27B shape: layer_linear_blk (a GatedDeltaNet layer) and
+          layer_full_blk (a full-attention layer) (run.c:2685-2745), and the
+          snap_save a drafted cycle pays (run.c:4952); the parent composes a
+          verify cycle from 48 + 16 of them and c2's head pass."""
     from cwen_amd import synth
     R, kind, cores, label = _reference_or_port()
     ref = kind == "reference"
@@ -487,12 +493,52 @@ def cpu_child(cfg: str, B: int, reps: int) -> None:
         nbytes = C3_BYTES
         what = (f"{len(ts)} blocks of 8 positions" + (" + snap_save/snap_load of 64 layers" if ref else "")
                 + f"; {label} conv1d_update/gdn_step")
+    elif cfg == "c4":
+        if not ref:
+            raise SystemExit("c4 needs the reference build")
+        c4cfg = dict(n_layers=64, d_model=H, d_ffn=I, vocab=151936, n_head=24, n_kv_head=4, head_dim=256,
+                     n_rot_pairs=32, n_rot=64, gdn_nkh=16, gdn_nvh=48, gdn_dk=128, full_interval=4,
+                     max_ctx=C4_CPU_CTX + 64, rope_theta=1e7, rms_eps=1e-6)
+        R.model_init(C4_CPU_CTX + 64)
+        for layer, linear in ((2, True), (3, False)):
+            for t in synth.model_tensors(c4cfg, seed=0, only_layer=layer, only_linear=linear):
+                R.set_tensor(*t)
+        X = synth.activations(0, B, H)
+        out = {}
+        for name, layer in (("linear", 2), ("full", 3)):
+            ts = _time_bounded(lambda i: R.block_layer(layer, C4_CPU_CTX, X), 50, 8.0)
+            out[name] = (float(np.median(ts)), len(ts))
+        ts = _time_bounded(lambda i: R.snap_save(), 20, 3.0)
+        out["snap"] = (float(np.median(ts)), len(ts))
+        print(json.dumps({"kind": kind, "cores": cores,
+                          "ms_linear_layer": out["linear"][0] * 1e3, "ms_full_layer": out["full"][0] * 1e3,
+                          "ms_snap_save": out["snap"][0] * 1e3,
+                          "sample": (f"{out['linear'][1]} layer_linear_blk and {out['full'][1]} layer_full_blk "
+                                     f"passes at B={B}, positions {C4_CPU_CTX}..{C4_CPU_CTX + B - 1}, "
+                                     f"{out['snap'][1]} snap_save; {label}; medians after 2 warmups")}))
+        return
     else:
         raise SystemExit(f"unknown cpu config {cfg}")
     med, mn = float(np.median(ts)), float(np.min(ts))
     print(json.dumps({"value": nbytes / med / 1e9, "unit": "GB/s", "cores": cores, "kind": kind,
                       "ms_median": med * 1e3, "ms_min": mn * 1e3,
                       "sample": f"{what}; median after 2 warmups"}))
+
+
+def c4_cpu_cycle(layers: dict | None, head: dict | None) -> dict | None:
+    """The reference's verify cycle on the 27B shape at B=8, context 4096,
+    composed from its measured parts: 48 GatedDeltaNet and 16 full-attention
+    layer blocks, the head pass with the walk (c2's leg) and one snap_save
+    (generate_tokens_spec, run.c:4952-4960 over forward_block, run.c:2752)."""
+    if layers is None or head is None:
+        return None
+    ms = 48 * layers["ms_linear_layer"] + 16 * layers["ms_full_layer"] + head["ms_median"] + layers["ms_snap_save"]
+    return {"value": round(ms, 2), "unit": "ms per verify cycle (B=8, context 4096)",
+            "columns_per_s": round(8 / ms * 1e3, 2), "cores": layers["cores"], "kind": layers["kind"],
+            "parts_ms": {"layer_linear_blk": round(layers["ms_linear_layer"], 3),
+                         "layer_full_blk": round(layers["ms_full_layer"], 3),
+                         "head_gemvb_walk": round(head["ms_median"], 3), "snap_save": round(layers["ms_snap_save"], 3)},
+            "sample": layers["sample"] + "; composed as 48 x linear + 16 x full + c2's head pass + snap_save"}
 
 
 def host_cpu_info() -> dict:
@@ -601,6 +647,9 @@ def main() -> int:
                 for name in ("c0", "c2", "c3"):
                     cpu_base["other_configs"][name] = cpu_leg(name)
                     done(f"CPU leg {name}")
+                if c4 is not None:
+                    cpu_base["other_configs"]["c4"] = c4_cpu_cycle(cpu_leg("c4"), cpu_base["other_configs"]["c2"])
+                    done("CPU leg c4")
     h = res[8]
     b1, _ = ffn_bytes(8)
     line = {

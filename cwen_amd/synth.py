@@ -137,7 +137,8 @@ def rsi_side(qs: np.ndarray, sc: np.ndarray, M: int, K: int, side: int) -> tuple
 
 
 # ---------------------------------------------------------------- whole model
-def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool = False, only_layer=None):
+def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool = False, only_layer=None,
+                  only_linear: bool = False):
     """Seeded random-init tensors of the hybrid decoder, in the reference's
     layouts: yields (layer, tensor id, type, data, scales, ne0, ne1); layer -1
     for the global tensors.  Q4_0 matrices are CWENR (RS, or RSI for the
@@ -146,8 +147,9 @@ def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool 
     model mixes in -- ffn_down of every other layer in Q4_1, every ssm_out
     in Q5_K.  mtp: also the MTP nextn drafter -- a full-attention block at
     layer n_layers and the nextn eh_proj (Q4_0RS, [H][2H]) and norms.
-    only_layer: that layer's tensors alone, as a full-attention layer (the
-    other tensors are not generated)."""
+    only_layer: that layer's tensors alone, as a full-attention layer, or a
+    GatedDeltaNet one with only_linear (the other tensors are not
+    generated)."""
     from . import gpu as G
     H, I, V = cfg["d_model"], cfg["d_ffn"], cfg["vocab"]
     nkh, nvh = cfg["gdn_nkh"], cfg["gdn_nvh"]
@@ -196,7 +198,7 @@ def model_tensors(cfg: dict, seed: int = 0, real_types: bool = False, mtp: bool 
             yield l, G.ATTN_K_NORM, G.T_F32, norm_w(k0 + 15, cfg["head_dim"]), None, cfg["head_dim"], 1
 
     if only_layer is not None:
-        yield from layer(only_layer, True, False)
+        yield from layer(only_layer, not only_linear, False)
         return
     qs, sc = q4_rs(seed, V, H, key=1000)
     yield -1, G.TOK_EMBD, G.T_Q4_0RS, qs, sc, H, V

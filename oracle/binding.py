@@ -205,6 +205,10 @@ class Reference:
         L.ref_mtp_commit.restype = _I
         L.ref_mtp_commit.argtypes = [_I, _I, _VP, _VP]
         L.ref_snap_roundtrip.restype = _I
+        L.ref_snap_save.restype = _I
+        L.ref_snap_load.restype = _I
+        L.ref_block_layer.restype = _I
+        L.ref_block_layer.argtypes = [_I, _I, _I, _VP]
         L.ref_ng_init.restype = _I
         L.ref_ng_init.argtypes = [_I]
         L.ref_ng_cap.restype = C.c_long
@@ -335,6 +339,21 @@ class Reference:
         if self.L.ref_layer_step(layer, pos, _f32p(x)):
             raise RuntimeError("ref_layer_step")
         return x
+
+    def block_layer(self, layer: int, pbase: int, X: np.ndarray) -> np.ndarray:
+        """layer_linear_blk / layer_full_blk over rows X[B][H] at positions pbase.. ."""
+        X = np.array(X, dtype=np.float32, copy=True, order="C")
+        if self.L.ref_block_layer(layer, X.shape[0], pbase, _f32p(X)):
+            raise RuntimeError("ref_block_layer")
+        return X
+
+    def snap_save(self) -> None:
+        if self.L.ref_snap_save():
+            raise RuntimeError("ref_snap_save")
+
+    def snap_load(self) -> None:
+        if self.L.ref_snap_load():
+            raise RuntimeError("ref_snap_load")
 
     def head(self, x: np.ndarray, n: int) -> np.ndarray:
         out = np.empty(n, dtype=np.float32)

@@ -230,6 +230,18 @@ int ref_layer_step(int layer, int pos, float *xio) {
   return 0;
 }
 
+/* One decoder layer over a block of B positions pbase .. pbase+B-1 on the
+ * residual rows xio[B][H]: layer_linear_blk (run.c:2685) or layer_full_blk
+ * (run.c:2714), in place -- forward_block's per-layer step. */
+int ref_block_layer(int layer, int B, int pbase, float *xio) {
+  if (!logits || layer < 0 || layer >= L || B < 1 || B > SPEC_BMAX || pbase < 0 || pbase + B > g_ctx) return -1;
+  memcpy(BXres, xio, (size_t)B * H * sizeof(float));
+  if (W[layer].is_linear) layer_linear_blk(layer, B);
+  else layer_full_blk(layer, B, pbase);
+  memcpy(xio, BXres, (size_t)B * H * sizeof(float));
+  return 0;
+}
+
 /* The head tail of forward_ex (run.c:2640-2644) on residual xin[H]: the
  * first n logits of output . rmsnorm(x, output_norm). */
 int ref_head(const float *xin, float *out, int n) {
@@ -275,14 +287,30 @@ int ref_mtp_commit(int pos, int tok, const float *x_pre, float *hprev) {
 /* The rollback copies of a drafted cycle: snap_save then snap_load
  * (run.c:2802-2809) over all L layers' Srec and Cstate, allocating the
  * state (ref_model_init) and the snapshot buffers on first use. */
-int ref_snap_roundtrip(void) {
+static int snap_alloc(void) {
   if (!logits && ref_model_init(2)) return -1;
   if (!SnapS) {
     SnapS = aligned_alloc(64, (size_t)L * LVH * LSD * LSD * sizeof(float));
     SnapC = aligned_alloc(64, (size_t)L * QKV_DIM * (CONV_K - 1) * sizeof(float));
     if (!SnapS || !SnapC) return -1;
   }
+  return 0;
+}
+int ref_snap_roundtrip(void) {
+  if (snap_alloc()) return -1;
   snap_save();
+  snap_load();
+  return 0;
+}
+/* snap_save alone: what a drafted cycle pays before its block (run.c:4952);
+ * snap_load puts the saved state back. */
+int ref_snap_save(void) {
+  if (snap_alloc()) return -1;
+  snap_save();
+  return 0;
+}
+int ref_snap_load(void) {
+  if (!SnapS) return -1;
   snap_load();
   return 0;
 }

@@ -88,6 +88,27 @@ def test_oracle_composition_vs_reference(oracle_outputs, ref_avx2, tensors):
         assert rel_err(oracle_outputs[key], live[key]) <= TOL, (key, rel_err(oracle_outputs[key], live[key]))
 
 
+def test_reference_block_layers_equal_serial_steps(ref_avx2, tensors):
+    """run.c's per-layer block steps (layer_linear_blk / layer_full_blk,
+    run.c:2685-2745, which forward_block and so bench.py's CPU verify-cycle
+    leg run) give the serial layer steps' residuals on 4 positions, within
+    TOL (gemvb and gemv order their sums differently)."""
+    R = ref_avx2
+    mg.bind(R, tensors)
+    X = mg.residuals(8, 6)
+    for p in range(4):                       # KV slots 0..3 hold known rows
+        R.layer_step(mg.FULL, p, X[p])
+    R.snap_save()
+    blk = R.block_layer(mg.LIN, 4, X[4:8])
+    R.snap_load()
+    ser = np.stack([R.layer_step(mg.LIN, 4 + b, X[4 + b]) for b in range(4)])
+    assert rel_err(blk, ser) <= TOL, rel_err(blk, ser)
+    blk = R.block_layer(mg.FULL, 4, X[4:8])
+    ser = np.stack([R.layer_step(mg.FULL, 4 + b, X[4 + b]) for b in range(4)])
+    assert rel_err(blk, ser) <= TOL, rel_err(blk, ser)
+    assert rel_err(blk, X[4:8]) > 100 * TOL          # the layer did something
+
+
 def test_composition_catches_a_planted_mistake(oracle, tensors):
     """A mistake planted in the oracle's composition (the post-attention
     norm skipped before the MLP) is far outside the tolerance: the check
