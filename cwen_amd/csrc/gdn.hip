@@ -153,14 +153,48 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
 
   // Stage nb positions of pending buffer `buf` into LDS; gates from the
   // buffer (replay) or computed from the raw inputs and saved (block).
+  // Every global load of a group of 8 positions is issued before the first
+  // wait, so staging costs one memory round trip per group, not one per
+  // position or per value; loads for positions past nb re-read position
+  // nb - 1 (inside the buffer) and are not stored.
   auto stage = [&](int nb, int buf, bool fresh) {
     const float *xc = p.xc + (size_t)buf * xstride;
     float *gs = p.gates + (size_t)buf * gstride;
+    const int lb = min(lane, nb - 1);
+    const float g_in = fresh ? p.decay[(size_t)lb * p.gs + hv] : gs[((size_t)lb * 2 + 0) * p.nvh + hv];
+    const float b_in = fresh ? p.beta[(size_t)lb * p.gs + hv] : gs[((size_t)lb * 2 + 1) * p.nvh + hv];
+    for (int b0 = 0; b0 < nb; b0 += 8) {
+      float qkr[8][4], vr[2];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {   // q and k of key head hk (l2-normalised by the conv)
+        const int b = min(b0 + u, nb - 1);
+        const float *xq = xc + (size_t)b * p.C + hk * DK;
+        const float *xk = xc + (size_t)b * p.C + (p.nkh + hk) * DK;
+        qkr[u][0] = xq[lane]; qkr[u][1] = xq[lane + 64];
+        qkr[u][2] = xk[lane]; qkr[u][3] = xk[lane + 64];
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {   // v: 8 positions x COLS columns, 2 per lane
+        const int e = lane + 64 * i, b = min(b0 + e / COLS, nb - 1);
+        vr[i] = xc[(size_t)b * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (b0 + u < nb) {
+          qk[b0 + u][lane] = qkr[u][0]; qk[b0 + u][lane + 64] = qkr[u][1];
+          qk[b0 + u][DK + lane] = qkr[u][2]; qk[b0 + u][DK + lane + 64] = qkr[u][3];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = lane + 64 * i;
+        if (b0 + e / COLS < nb) vs[b0 + e / COLS][e % COLS] = vr[i];
+      }
+    }
     if (lane < nb) {
-      float g, bt;
+      float g = g_in, bt = b_in;
       if (fresh) {
-        float dec = p.decay[(size_t)lane * p.gs + hv];
-        bt = p.beta[(size_t)lane * p.gs + hv];
+        float dec = g_in;
         if (p.A) {  // run.c:2697-2698 (softplus, sigmoid: run.c:392-399)
           const float x = dec + p.dt[hv];
           dec = p.A[hv] * (x > 20.f ? x : logf(1.f + expf(x)));
@@ -171,22 +205,9 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
           gs[((size_t)lane * 2 + 0) * p.nvh + hv] = g;
           gs[((size_t)lane * 2 + 1) * p.nvh + hv] = bt;
         }
-      } else {
-        g = gs[((size_t)lane * 2 + 0) * p.nvh + hv];
-        bt = gs[((size_t)lane * 2 + 1) * p.nvh + hv];
       }
       s_g[lane] = g;
       s_beta[lane] = bt;
-    }
-    for (int e = lane; e < nb * COLS; e += 64)
-      vs[e / COLS][e % COLS] = xc[(size_t)(e / COLS) * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
-#pragma unroll
-    for (int b = 0; b < MAXB; ++b) {  // q and k of key head hk (l2-normalised by the conv)
-      if (b >= nb) break;
-      const float *xq = xc + (size_t)b * p.C + hk * DK;
-      const float *xk = xc + (size_t)b * p.C + (p.nkh + hk) * DK;
-      qk[b][lane] = xq[lane]; qk[b][lane + 64] = xq[lane + 64];
-      qk[b][DK + lane] = xk[lane]; qk[b][DK + lane + 64] = xk[lane + 64];
     }
     __syncthreads();
   };
