@@ -343,7 +343,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
   const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   // Chunks in order, 256 at a time: thread j weighs chunk c0 + j into LDS,
   // then every thread (head dim d) accumulates them with its partial
-  // outputs loaded 8 at a time.
+  // outputs loaded MG at a time (independent loads in flight; the sums
+  // still run chunk by chunk in order).
   float L = 0.f, O = 0.f;
   for (int c0 = 0; c0 < nc; c0 += 256) {
     __syncthreads();  // previous tile's weights read
@@ -354,13 +355,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     }
     __syncthreads();
     const int n = min(256, nc - c0);
-    for (int j0 = 0; j0 < n; j0 += 8) {
-      float pv[8];
+    constexpr int MG = 32;
+    for (int j0 = 0; j0 < n; j0 += MG) {
+      float pv[MG];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < MG; ++u)
         pv[u] = j0 + u < n ? p.po[(base + (size_t)(c0 + j0 + u) * nq) * HD + d] : 0.f;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < MG; ++u) {
         if (j0 + u >= n) break;
         L = fmaf(s_w[j0 + u], s_l[j0 + u], L);
         O = fmaf(s_w[j0 + u], pv[u], O);
