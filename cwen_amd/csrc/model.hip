@@ -322,10 +322,15 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
   }
 }
 
-// ---- full attention, part 3: merge the chunks of each (position, head) in
-// chunk order, normalise, apply the sigmoid gate, write f16.  Grid: (B, NH).
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
-  const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+// ---- full attention, part 3: merge the chunks of each (position, head),
+// normalise, apply the sigmoid gate, write f16.  Grid: (B, NH); MGR groups
+// of HD threads (thread = head dim d) each take a contiguous quarter of the
+// chunks in order, and the groups' sums are added in group order: a fixed
+// order per position, whatever B is.
+constexpr int MGR = 4;
+__global__ __launch_bounds__(HD * MGR) void attn_merge_kernel(AttnParams p) {
+  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int d = tid % HD, grp = tid / HD;
   const int kvm = p.NH / p.NKV;
   const int hkv = h / kvm, m = h % kvm;
   const int nq = p.B * kvm;
@@ -333,41 +338,55 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
   const int pos = *p.last + 1 + b;
   if (pos < 0 || pos >= p.max_ctx) return;
   const int nc = pos / TC + 1;
-  __shared__ float red[4], s_w[256], s_l[256];
+  __shared__ float red[HD * MGR / 64], s_w[HD * MGR], s_l[HD * MGR], s_lo[2][MGR][HD];
   const size_t base = (size_t)hkv * p.nchunk * nq + qi;  // statistics of chunk c at base + c * nq
   float mx = -__builtin_inff();
-  for (int c = d; c < nc; c += 256) mx = fmaxf(mx, p.pm[base + (size_t)c * nq]);
+  for (int c = tid; c < nc; c += HD * MGR) mx = fmaxf(mx, p.pm[base + (size_t)c * nq]);
   mx = max64(mx);
-  if ((d & 63) == 0) red[d >> 6] = mx;
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // Chunks in order, 256 at a time: thread j weighs chunk c0 + j into LDS,
-  // then every thread (head dim d) accumulates them with its partial
-  // outputs loaded MG at a time (independent loads in flight; the sums
-  // still run chunk by chunk in order).
+  float M = red[0];
+#pragma unroll
+  for (int w = 1; w < HD * MGR / 64; ++w) M = fmaxf(M, red[w]);
+  // Chunks HD*MGR at a time: thread j weighs chunk c0 + j into LDS; group g
+  // then accumulates its quarter of them in order, its partial outputs
+  // loaded MG at a time.
   float L = 0.f, O = 0.f;
-  for (int c0 = 0; c0 < nc; c0 += 256) {
+  for (int c0 = 0; c0 < nc; c0 += HD * MGR) {
     __syncthreads();  // previous tile's weights read
-    if (c0 + d < nc) {
-      const size_t pi = base + (size_t)(c0 + d) * nq;
-      s_w[d] = expf(p.pm[pi] - M);
-      s_l[d] = p.pl[pi];
+    if (c0 + tid < nc) {
+      const size_t pi = base + (size_t)(c0 + tid) * nq;
+      s_w[tid] = expf(p.pm[pi] - M);
+      s_l[tid] = p.pl[pi];
     }
     __syncthreads();
-    const int n = min(256, nc - c0);
-    constexpr int MG = 32;
-    for (int j0 = 0; j0 < n; j0 += MG) {
+    const int n = min(HD * MGR, nc - c0);
+    const int per = (n + MGR - 1) / MGR;
+    const int j1 = min(n, (grp + 1) * per);
+    constexpr int MG = 8;
+    for (int j0 = grp * per; j0 < j1; j0 += MG) {
       float pv[MG];
 #pragma unroll
       for (int u = 0; u < MG; ++u)
-        pv[u] = j0 + u < n ? p.po[(base + (size_t)(c0 + j0 + u) * nq) * HD + d] : 0.f;
+        pv[u] = j0 + u < j1 ? p.po[(base + (size_t)(c0 + j0 + u) * nq) * HD + d] : 0.f;
 #pragma unroll
       for (int u = 0; u < MG; ++u) {
-        if (j0 + u >= n) break;
+        if (j0 + u >= j1) break;
         L = fmaf(s_w[j0 + u], s_l[j0 + u], L);
         O = fmaf(s_w[j0 + u], pv[u], O);
       }
     }
+  }
+  s_lo[0][grp][d] = L;
+  s_lo[1][grp][d] = O;
+  __syncthreads();
+  if (grp != 0) return;
+  L = s_lo[0][0][d];
+  O = s_lo[1][0][d];
+#pragma unroll
+  for (int g2 = 1; g2 < MGR; ++g2) {
+    L += s_lo[0][g2][d];
+    O += s_lo[1][g2][d];
   }
   const float g = p.qfull[(size_t)b * p.qfs + (size_t)h * 2 * HD + HD + d];
   const float y = (O / L) * (1.f / (1.f + expf(-g)));
@@ -439,7 +458,7 @@ int attention_launch(const float *qfull, int qfs, const float *kx, const float *
   hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
   if (MT <= 4) hipLaunchKernelGGL(attn_chunk_kernel<4>, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);
   else hipLaunchKernelGGL(attn_chunk_kernel<8>, dim3((unsigned)nwg, (unsigned)NKV), dim3(512), lds, st, p);
-  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)B, (unsigned)NH), dim3(HD), 0, st, p);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)B, (unsigned)NH), dim3(HD * MGR), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }
