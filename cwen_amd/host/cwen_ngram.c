@@ -102,7 +102,7 @@ static void evict_one(cwen_ngmap *m) {
 int cwen_ngmap_create(int n_key, int vocab, size_t cap, cwen_ngmap **out) {
   if (!out || n_key < 1 || n_key > NG_KEY_MAX || vocab < 1) return CWEN_EINVAL;
   if (cap == 0) cap = CWEN_NGMAP_CAP;
-  if (cap < 2 || (cap & (cap - 1))) return CWEN_EINVAL;
+  if (cap < 2 || (cap & (cap - 1)) || cap > SIZE_MAX / ((size_t)n_key * sizeof(int))) return CWEN_EINVAL;
   cwen_ngmap *m = (cwen_ngmap *)calloc(1, sizeof *m);
   if (!m) return CWEN_ENOMEM;
   m->n_key = n_key;
