@@ -171,15 +171,19 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
 // query row, whatever B is.  Scores: wave w takes 16-query tile w (both
 // 16-key halves, so the chunk softmax stays in the wave); a block with more
 // than 4 tiles runs 8-wave workgroups (NW = 8), so a wave never holds more
-// than one tile.  P.V: V is staged transposed; wave w takes head-dim tiles
-// (16/NW)w .. of every query tile.  Every output takes the same instruction
-// sequence for NW = 4 and 8.  A fixed grid of workgroups per kv head takes
+// than one tile.  K and V rows land in LDS straight from the cache by
+// 16-byte buffer loads (one 1 KB row per instruction; rows past the block's
+// last position load as zeros), in their natural [key][dim] layout.  P.V:
+// wave w takes head-dim tiles (16/NW)w .. of every query tile, reading V's 8
+// k-steps of a tile once for all query tiles.  Every output takes the same
+// instruction sequence for NW = 4 and 8.  A fixed grid of workgroups per kv head takes
 // chunks blockIdx.x, + gridDim.x, ... up to the block's last position (the
 // partials are per chunk, so the mapping does not change the arithmetic).
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-constexpr int KROW = HD + 4, VROW = TC + 4, PROW = TC + 4;
+constexpr int KROW = HD + 4, PROW = TC + 4;   // K and V rows: 1040 bytes, 16-byte aligned
 constexpr int NW_MAX = 8;    // waves of the largest workgroup: 16-query tiles per block (nq <= 128)
-constexpr int KV_FLOATS = TC * KROW > HD * VROW ? TC * KROW : HD * VROW;
+constexpr int KV_FLOATS = 2 * TC * KROW;     // K [TC][KROW] then V [TC][KROW]
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ float max16(float m) {
   m = fmaxf(m, dpp<0xB1>(m)); m = fmaxf(m, dpp<0x4E>(m));
@@ -197,8 +201,8 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
   const int pbase = *p.last + 1;
   const int tlast = min(pbase + p.B - 1, p.max_ctx - 1);  // last position of the block
   if ((int)blockIdx.x * TC > tlast) return;
-  float *KV = sm;                              // K [TC][KROW], then V^T [HD][VROW]
-  float *Ps = KV + KV_FLOATS;                  // [MT*16][PROW]
+  float *Ks = sm, *Vs = sm + TC * KROW;        // K and V rows of the chunk
+  float *Ps = sm + KV_FLOATS;                  // [MT*16][PROW]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
@@ -215,23 +219,24 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
                                             lg * (HD / 4) + 4 * k)
                         : (float4){0.f, 0.f, 0.f, 0.f};
   }
-  constexpr int KV_L = TC * (HD / 4) / (64 * NW);   // float4 of a chunk's K (or V) rows per thread
+  constexpr int KV_R = TC / NW;                     // K (and V) rows each wave lands per chunk
   constexpr int DT = 16 / NW;                       // head-dim tiles of P.V per wave
+  const __amdgpu_buffer_rsrc_t kr = make_rsrc(p.K, (uint32_t)((size_t)p.max_ctx * p.NKV * HD * 4));
+  const __amdgpu_buffer_rsrc_t vr = make_rsrc(p.V, (uint32_t)((size_t)p.max_ctx * p.NKV * HD * 4));
   for (int c = blockIdx.x; c * TC <= tlast; c += gridDim.x) {
     const int t0 = c * TC;
     const int tn = min(TC, tlast + 1 - t0);     // keys of this chunk that exist
-    float4 kv[KV_L], vr[KV_L];                  // row t = wave + NW u, float4 d4 = lane
+    __syncthreads();                            // previous chunk's reads of K, V and P done
 #pragma unroll
-    for (int u = 0; u < KV_L; ++u) {
+    for (int u = 0; u < KV_R; ++u) {            // row t = wave + NW u: 64 lanes x 16 bytes
       const int t = wave + NW * u;
-      const size_t at = ((size_t)(t0 + t) * p.NKV + hkv) * HD + lane * 4;
-      kv[u] = t < tn ? *(const float4 *)(p.K + at) : (float4){0.f, 0.f, 0.f, 0.f};
-      vr[u] = t < tn ? *(const float4 *)(p.V + at) : (float4){0.f, 0.f, 0.f, 0.f};  // held until P is done
+      const uint32_t row = (uint32_t)(((size_t)(t0 + t) * p.NKV + hkv) * HD * 4);
+      const uint32_t vo = t < tn ? (uint32_t)lane * 16 : 0xFFFFFFE0u;   // past the last key: zeros
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void_t *)(Ks + t * KROW), 16, vo, row, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void_t *)(Vs + t * KROW), 16, vo, row, 0, 0);
     }
-    __syncthreads();                            // previous chunk's reads of KV and Ps done
-#pragma unroll
-    for (int u = 0; u < KV_L; ++u) *(float4 *)(KV + (wave + NW * u) * KROW + lane * 4) = kv[u];
-    __syncthreads();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's rows have landed
+    __syncthreads();                                     // and every wave's
     // scores and the chunk softmax, one 16-query tile per wave
     if (wave < MT) {
       const int mt = wave;
@@ -239,7 +244,7 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
       // the lane group's K run, u over the second, summed at the end.
       f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
       f32x4_t u0 = {0.f, 0.f, 0.f, 0.f}, u1 = {0.f, 0.f, 0.f, 0.f};
-      const float *k0 = KV + lr * KROW + lg * (HD / 4), *k1 = k0 + 16 * KROW;
+      const float *k0 = Ks + lr * KROW + lg * (HD / 4), *k1 = k0 + 16 * KROW;
 #pragma unroll
       for (int k = 0; k < HD / 8; k += 4) {
         const float4 a = qreg[k / 4], b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
@@ -284,34 +289,30 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
         }
       }
     }
-    __syncthreads();                            // K reads and P writes done
+    __syncthreads();                            // P written
+    // P.V: head-dim tiles DT*wave .. DT*wave + DT-1 of every query tile.  In
+    // step k of a product, lane group g supplies key g*8 + k: P[q][g*8 + k]
+    // (two 16-byte reads per query tile) and V[g*8 + k][d] (one read per
+    // step, shared by the query tiles).
 #pragma unroll
-    for (int u = 0; u < KV_L; ++u) {            // V^T[d][t]
-      const int t = wave + NW * u;
-      KV[(lane * 4 + 0) * VROW + t] = vr[u].x;
-      KV[(lane * 4 + 1) * VROW + t] = vr[u].y;
-      KV[(lane * 4 + 2) * VROW + t] = vr[u].z;
-      KV[(lane * 4 + 3) * VROW + t] = vr[u].w;
-    }
-    __syncthreads();
-    // P.V: head-dim tiles DT*wave .. DT*wave + DT-1 of every query tile
-    for (int mt = 0; mt < MT; ++mt) {
-      const float *pa = Ps + (mt * 16 + lr) * PROW + lg * (TC / 4);
-      const float4 pa0 = *(const float4 *)pa, pa1 = *(const float4 *)(pa + 4);
+    for (int q = 0; q < DT; ++q) {
+      const int nd = wave * DT + q;
+      const float *vb = Vs + (lg * (TC / 4)) * KROW + nd * 16 + lr;
+      float vk[8];
 #pragma unroll
-      for (int q = 0; q < DT; ++q) {
-        const int nd = wave * DT + q;
-        const float *vb = KV + (nd * 16 + lr) * VROW + lg * (TC / 4);
-        const float4 vb0 = *(const float4 *)vb, vb1 = *(const float4 *)(vb + 4);
+      for (int k = 0; k < 8; ++k) vk[k] = vb[k * KROW];
+      for (int mt = 0; mt < MT; ++mt) {
+        const float *pa = Ps + (mt * 16 + lr) * PROW + lg * (TC / 4);
+        const float4 pa0 = *(const float4 *)pa, pa1 = *(const float4 *)(pa + 4);
         f32x4_t o = {0.f, 0.f, 0.f, 0.f};
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.x, vb0.x, o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.y, vb0.y, o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.z, vb0.z, o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.w, vb0.w, o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.x, vb1.x, o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.y, vb1.y, o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.z, vb1.z, o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.w, vb1.w, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.x, vk[0], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.y, vk[1], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.z, vk[2], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.w, vk[3], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.x, vk[4], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.y, vk[5], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.z, vk[6], o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.w, vk[7], o, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int qi = mt * 16 + 4 * lg + r;
