@@ -140,6 +140,41 @@ def test_real_model_types(env, oracle):
     m.free()
 
 
+def test_context_not_a_multiple_of_the_chunk(env, oracle):
+    """max_ctx 77: the attention's last 32-key chunk holds only positions
+    64..76, and its rows past the last position (and past the cache's end)
+    load as zeros.  The cache filled to its last slot in ragged blocks:
+    logits vs the oracle with the stated tolerance, and single positions
+    equal to the block bit for bit."""
+    gpu, ctx, _, tensors = env
+    cfg = {**CFG, "max_ctx": 77}
+    m = gpu.Model(ctx, **cfg)
+    for t in tensors:
+        m.set(*t)
+    toks = synth.prompt_tokens(12, 77, CFG["vocab"])
+    ref, tol = _oracle_logits(oracle, tensors, toks)
+    got, b0 = [], 0
+    for B in (16, 16, 16, 16, 13):
+        m.forward(toks[b0:b0 + B])
+        got.append(m.logits(B))
+        b0 += B
+    got = np.concatenate(got)
+    assert m.pos == 76
+    for p in range(len(toks)):
+        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
+    m.reset()
+    for b in range(0, 64, 16):
+        m.forward(toks[b:b + 16])
+    singles = []
+    for p in range(64, 77):
+        m.forward(toks[p:p + 1])
+        singles.append(m.logits(1)[0])
+    assert np.array_equal(np.stack(singles).view(np.uint32), got[64:].view(np.uint32))
+    with pytest.raises(gpu.CwenError):
+        m.forward(toks[:1])                 # the cache is full
+    m.free()
+
+
 def test_q6_k_embedding(env, oracle):
     """A Q6_K token_embd (run.c:1882-1883).  (1) Forward parity vs the oracle
     with a random Q6_K table, same tolerance as above.  (2) Exactness: a Q6_K
