@@ -159,7 +159,7 @@ F2_BYTES = F2_V * 20 * 210 + 8 * 5120 * 4 + 8 * F2_V * 4
 
 
 def c3_moved_bytes(B: int = 8, C: int = 10240, nvh: int = 48, dk: int = 128) -> int:
-    """HBM bytes this build's GDN block moves (each buffer counted once): the
+    """HBM bytes the device's GDN block moves (each buffer counted once): the
     base state read and the end state written (no per-position snapshots),
     raw qkv, conv taps, the start history slot read and one history slot
     written per position, the pending post-conv values and gates written for
@@ -301,7 +301,7 @@ def extra_leg(steps: int, warmup: int) -> dict:
                                "workload_bytes": C3_BYTES,
                                "workload_GB_s": C3_BYTES / (ms * 1e-3) / 1e9,
                                "launches": "gdn block: conv, delta rule (8 positions), gated norm",
-                               "note": "GB/s and frac over the bytes this build moves per block (two base states "
+                               "note": "GB/s and frac over the bytes the device moves per block (two base states "
                                        "and a replay of the accepted prefix, no per-position snapshots); "
                                        "workload_GB_s divides the workload definition's bytes, which count 8 "
                                        "per-position state snapshots (25.2 MB), by the same time"}
@@ -611,7 +611,7 @@ def main() -> int:
         cpu_child(args.cpu_child, args.B, reps=2000)
         return 0
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported", file=sys.stderr)
+        print(f"bench.py: runs on one GPU; --gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
     Bs = [int(b) for b in args.Bs.split(",")]
     if 8 not in Bs:

@@ -1,7 +1,7 @@
 /* cwen_run -- the command-line front end of the reference engine's `run`
  * (run.c:5080-5251 main, run_usage; the knobs of spec_config_init 4021-4052,
  * rope_env_init 4096-4104 and env_int / env_bool / arg_int_range 2481-2520)
- * over this build: the model is loaded from the GGUF file (and its CWENR
+ * over the GPU library: the model is loaded from the GGUF file (and its CWENR
  * sidecar) into HBM, and every forward pass runs on the GPU.
  *
  *   cwen_run [MODEL] [IDS_FILE] [N_PREDICT] [-d N]
@@ -10,7 +10,7 @@
  * stderr.  CWEN_SERVER=1 answers binary frames on stdin/stdout instead.
  * Knobs that steer the reference's CPU kernels (thread count, weight
  * residency and prefetch) have nothing to steer here and are ignored; the
- * features this build does not have (activation dumps, YaRN scaling, the
+ * features the GPU path does not provide (activation dumps, YaRN scaling, the
  * DFlash drafter) are refused before the model loads.
  */
 #define _POSIX_C_SOURCE 200809L
@@ -173,7 +173,7 @@ int main(int argc, char **argv) {
   for (size_t k = 0; k < sizeof refused / sizeof *refused; k++) {
     const char *e = getenv(refused[k]);
     if (e && e[0]) {
-      fprintf(stderr, "cwen_run: %s is not supported by this build\n", refused[k]);
+      fprintf(stderr, "cwen_run: %s is not supported here\n", refused[k]);
       return 1;
     }
   }

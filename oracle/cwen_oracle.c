@@ -1,7 +1,7 @@
 /* cwen oracle: scalar CPU restatement of the reference hot path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the thing measured or
- * shipped).  Each function restates the scalar branch of the cited run.c
+ * TEST INFRASTRUCTURE ONLY (the tests check results against it; it is never
+ * the thing measured or shipped).  Each function restates the scalar branch of the cited run.c
  * function with the same f32 evaluation order; it must be compiled with
  * -std=c11 (gcc: no FP contraction) so rounding matches the reference's
  * scalar build bit for bit.

@@ -2,8 +2,8 @@
 last positions of a 4224-token context on a small model with the 27B
 shape's attention geometry (24 query heads, 4 KV heads of dim 256: 6 query
 heads per KV head), so the device's long-context attention paths can be
-compared with the oracle on the GPU box without re-running 4224 serial oracle
-steps there.
+compared with the oracle where the GPU tests run, without re-running 4224
+serial oracle steps there.
 
     python tests/golden/make_c4_geometry_golden.py     # a few minutes
 

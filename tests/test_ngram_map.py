@@ -86,12 +86,12 @@ def test_full_table_evicts_like_reference(ref):
     first one in which no entry shifts back into the freed slot: there the
     reference keeps its victim marked in use and writes the new entry past
     the end of its arrays, so the reference is not run into that eviction
-    (a map of this build alone finds where it falls)."""
+    (our own map, run alone, finds where it falls)."""
     from cwen_amd import gpu
     R = ref
     n_key, cap, max_evictions = 2, 1 << 18, 1500
     hist = np.random.default_rng(3).integers(0, VOCAB, cap + 3000).astype(np.int32)
-    # where the first eviction without a shift falls, on a map of this build
+    # where the first eviction without a shift falls, on our own map
     probe = _map(n_key)
     _fill_full(probe, hist, cap)
     stop = cap - 10
