@@ -1123,28 +1123,42 @@ int tile_rows(int nsides) { return nsides == 2 ? WAVES / 2 : WAVES; }
 
 // Estimated length of a launch (microseconds at the 27B FFN shape's rates).
 // Workgroup i runs on CU i mod ncu (dispatch fills every CU's first slot,
-// then every second slot, ...).  A CU works through its workgroups' rounds,
-// plus one round of start-up each, at a rate that grows with the number of
-// workgroups it holds (measured: a lone
-// four-wave workgroup is latency-bound); the busiest CU sets the length.
+// then every second slot, ...).  A workgroup's work is its rounds plus one
+// round of start-up.  The workgroups on a CU share it evenly, at a total
+// rate that grows with how many are still running (a lone four-wave
+// workgroup is latency-bound), so a short piece slows a whole tile on its
+// CU only while both run; the busiest CU sets the length.  Rates from
+// 16480 x 5120 at B = 8 (258 tiles of 10 rounds): 12.0-12.4 us for a lone
+// tile per CU, 15.6 us with two whole tiles on two CUs, 14.5 / 13.2 / 13.2
+// us with the two last tiles split in 2 / 5 / 10 pieces.
 // Split remainder tiles add their partial-sum hand-off, early in the launch:
 // their pieces are dispatched first, so they are the oldest workgroups on
 // their CUs, which the hardware serves first.
 constexpr double kSplitEarly = 0.3;
-double cu_rate(int wgs) {  // rounds per microsecond
-  return wgs <= 1 ? 0.6 : wgs == 2 ? 1.2 : wgs == 3 ? 1.35 : wgs == 4 ? 1.45 : 1.5;
+double cu_rate(int wgs) {  // rounds per microsecond, all of a CU's workgroups together
+  return wgs <= 1 ? 0.77 : wgs == 2 ? 1.2 : wgs == 3 ? 1.35 : wgs == 4 ? 1.45 : 1.5;
+}
+// Time for one CU to finish workgroups of the given lengths (in rounds),
+// shared evenly among those still running.
+double cu_time(std::vector<double> &len) {
+  std::sort(len.begin(), len.end());
+  double t = 0.0, done = 0.0;
+  const int n = (int)len.size();
+  for (int i = 0; i < n; ++i) {
+    t += (len[(size_t)i] - done) * (n - i) / cu_rate(n - i);
+    done = len[(size_t)i];
+  }
+  return t;
 }
 double grid_cost(int ncu, int nst, const GemvGrid &c, double extra) {
-  std::vector<double> rounds((size_t)ncu, 0.0);
-  std::vector<int> wgs((size_t)ncu, 0);
+  std::vector<std::vector<double>> len((size_t)ncu);
   for (int i = 0; i < c.grid; ++i) {
     const int nr = i < c.nsplit ? std::min(nst - (i % c.S) * c.rps, c.rps) : nst;
-    rounds[(size_t)(i % ncu)] += nr + 1.0;
-    ++wgs[(size_t)(i % ncu)];
+    len[(size_t)(i % ncu)].push_back(nr + 1.0);
   }
   double worst = 0.0;
-  for (int k = 0; k < ncu; ++k)
-    if (wgs[(size_t)k]) worst = std::max(worst, rounds[(size_t)k] / cu_rate(wgs[(size_t)k]));
+  for (auto &l : len)
+    if (!l.empty()) worst = std::max(worst, cu_time(l));
   return worst + extra;
 }
 
