@@ -233,14 +233,6 @@ __device__ __forceinline__ half2_t i8pair(uint32_t w, uint32_t magic, bool upper
   return __builtin_bit_cast(half2_t, t) - h2c(1152.f);
 }
 
-// LDS hand-off barrier: waits for this wave's LDS writes only, not for its
-// outstanding global loads (unlike __syncthreads(), whose release fence
-// drains the load counter).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // gfx9 encoding: lgkmcnt(0), vmcnt/expcnt unchanged
-  __builtin_amdgcn_s_barrier();
-}
-
 // Total order on (logit, row) for the argmax: larger logit first, then the
 // lower row.  NaN ranks as -inf and -0 as +0, so the maximum key is the first
 // index of the maximum over the non-NaN logits -- argmax_of's strict '>' scan.

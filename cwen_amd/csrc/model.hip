@@ -198,9 +198,6 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
   const int kvm = p.NH / p.NKV;
   const int nq = p.B * kvm;
   const int MT = (nq + 15) / 16;               // 16-query tiles
-  const int pbase = *p.last + 1;
-  const int tlast = min(pbase + p.B - 1, p.max_ctx - 1);  // last position of the block
-  if ((int)blockIdx.x * TC > tlast) return;
   float *Ks = sm, *Vs = sm + TC * KROW;        // K and V rows of the chunk
   float *Ps = sm + KV_FLOATS;                  // [MT*16][PROW]
   const int tid = threadIdx.x, lane = tid & 63;
@@ -208,25 +205,35 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
   const int lr = lane & 15, lg = lane >> 4;
   const float scale = 1.f / sqrtf((float)HD);
   // The score phase's queries stay in registers: wave w holds 16-query tile
-  // w, lane (lr, lg) the HD/4 dims lg*HD/4 .. of query row lr (rows >= nq
-  // zero).  Keeping them out of LDS leaves room for several workgroups per CU.
+  // w, lane (lr, lg) the HD/4 dims lg*HD/4 .. of query row lr.  Keeping them
+  // out of LDS leaves room for several workgroups per CU.  They are requested
+  // first, before the block's position is known: query row qi belongs to
+  // position qi / kvm, so rows >= nq lie past the buffer range and load as
+  // zeros.
   float4 qreg[HD / 16];
   {
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(p.q, (uint32_t)((size_t)p.B * p.NH * HD * 4));
     const int qi = wave * 16 + lr;
+    const uint32_t qo = (uint32_t)((((qi / kvm) * p.NH + hkv * kvm + qi % kvm) * HD + lg * (HD / 4)) * 4);
 #pragma unroll
-    for (int k = 0; k < HD / 16; ++k)
-      qreg[k] = qi < nq ? *(const float4 *)(p.q + ((size_t)(qi / kvm) * p.NH + hkv * kvm + qi % kvm) * HD +
-                                            lg * (HD / 4) + 4 * k)
-                        : (float4){0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < HD / 16; ++k) qreg[k] = __builtin_bit_cast(float4, bload16(qr, qo + 16 * k));
   }
   constexpr int KV_R = TC / NW;                     // K (and V) rows each wave lands per chunk
   constexpr int DT = 16 / NW;                       // head-dim tiles of P.V per wave
   const __amdgpu_buffer_rsrc_t kr = make_rsrc(p.K, (uint32_t)((size_t)p.max_ctx * p.NKV * HD * 4));
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(p.V, (uint32_t)((size_t)p.max_ctx * p.NKV * HD * 4));
-  for (int c = blockIdx.x; c * TC <= tlast; c += gridDim.x) {
+  // The position is read after the queries are requested (a scalar load
+  // issued first would hold their address computation behind it).
+  __builtin_amdgcn_sched_barrier(0);
+  const int pbase = *p.last + 1;
+  const int tlast = min(pbase + p.B - 1, p.max_ctx - 1);  // last position of the block
+  if ((int)blockIdx.x * TC > tlast) return;
+  // Lands chunk c's K and V rows in LDS (rows past the block's last position
+  // as zeros); the first chunk's rows are requested with the queries in
+  // flight, so both arrive in one memory round trip.
+  auto land = [&](int c) __attribute__((always_inline)) {
     const int t0 = c * TC;
     const int tn = min(TC, tlast + 1 - t0);     // keys of this chunk that exist
-    __syncthreads();                            // previous chunk's reads of K, V and P done
 #pragma unroll
     for (int u = 0; u < KV_R; ++u) {            // row t = wave + NW u: 64 lanes x 16 bytes
       const int t = wave + NW * u;
@@ -235,21 +242,39 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void_t *)(Ks + t * KROW), 16, vo, row, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void_t *)(Vs + t * KROW), 16, vo, row, 0, 0);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's rows have landed
-    __syncthreads();                                     // and every wave's
+  };
+  int c = blockIdx.x;
+  land(c);
+  for (;;) {
+    const int t0 = c * TC;
+    const int tn = min(TC, tlast + 1 - t0);     // keys of this chunk that exist
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's rows (and queries) have landed
+    lds_barrier();                                       // and every wave's
     // scores and the chunk softmax, one 16-query tile per wave
     if (wave < MT) {
       const int mt = wave;
       // Four independent accumulators per 16 keys: s over the first half of
-      // the lane group's K run, u over the second, summed at the end.
+      // the lane group's K run, u over the second, summed at the end.  The
+      // K rows of step k + 4 are read from LDS while step k's products issue
+      // (the scheduling barriers keep the reads ahead of the products).
       f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
       f32x4_t u0 = {0.f, 0.f, 0.f, 0.f}, u1 = {0.f, 0.f, 0.f, 0.f};
       const float *k0 = Ks + lr * KROW + lg * (HD / 4), *k1 = k0 + 16 * KROW;
+      float4 kb[2][4];
+      auto kread = [&](int k, float4 (&d)[4]) __attribute__((always_inline)) {
+        d[0] = *(const float4 *)(k0 + k);
+        d[1] = *(const float4 *)(k1 + k);
+        d[2] = *(const float4 *)(k0 + k + HD / 8);
+        d[3] = *(const float4 *)(k1 + k + HD / 8);
+      };
+      kread(0, kb[0]);
 #pragma unroll
       for (int k = 0; k < HD / 8; k += 4) {
-        const float4 a = qreg[k / 4], b0 = *(const float4 *)(k0 + k), b1 = *(const float4 *)(k1 + k);
-        const float4 cq = qreg[(k + HD / 8) / 4], e0 = *(const float4 *)(k0 + k + HD / 8),
-                     e1 = *(const float4 *)(k1 + k + HD / 8);
+        if (k + 4 < HD / 8) kread(k + 4, kb[((k >> 2) + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        const float4 a = qreg[k / 4], cq = qreg[(k + HD / 8) / 4];
+        const float4 b0 = kb[(k >> 2) & 1][0], b1 = kb[(k >> 2) & 1][1];
+        const float4 e0 = kb[(k >> 2) & 1][2], e1 = kb[(k >> 2) & 1][3];
         s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b0.x, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b1.x, s1, 0, 0, 0);
         u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.x, e0.x, u0, 0, 0, 0);
@@ -266,6 +291,7 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
         s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b1.w, s1, 0, 0, 0);
         u0 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.w, e0.w, u0, 0, 0, 0);
         u1 = __builtin_amdgcn_mfma_f32_16x16x4f32(cq.w, e1.w, u1, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
       s0 += u0;
       s1 += u1;
@@ -289,37 +315,44 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
         }
       }
     }
-    __syncthreads();                            // P written
+    lds_barrier();                              // P written (the max / sum stores need not land)
     // P.V: head-dim tiles DT*wave .. DT*wave + DT-1 of every query tile.  In
     // step k of a product, lane group g supplies key g*8 + k: P[q][g*8 + k]
-    // (two 16-byte reads per query tile) and V[g*8 + k][d] (one read per
-    // step, shared by the query tiles).
+    // (two 16-byte reads per query tile) and V[g*8 + k][d] (read once, shared
+    // by the query tiles).  The DT products of a query tile run interleaved,
+    // each still summing its steps k = 0 .. 7 in order.
+    float vk[DT][8];
 #pragma unroll
     for (int q = 0; q < DT; ++q) {
-      const int nd = wave * DT + q;
-      const float *vb = Vs + (lg * (TC / 4)) * KROW + nd * 16 + lr;
-      float vk[8];
+      const float *vb = Vs + (lg * (TC / 4)) * KROW + (wave * DT + q) * 16 + lr;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) vk[k] = vb[k * KROW];
-      for (int mt = 0; mt < MT; ++mt) {
-        const float *pa = Ps + (mt * 16 + lr) * PROW + lg * (TC / 4);
-        const float4 pa0 = *(const float4 *)pa, pa1 = *(const float4 *)(pa + 4);
-        f32x4_t o = {0.f, 0.f, 0.f, 0.f};
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.x, vk[0], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.y, vk[1], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.z, vk[2], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa0.w, vk[3], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.x, vk[4], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.y, vk[5], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.z, vk[6], o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x4f32(pa1.w, vk[7], o, 0, 0, 0);
+      for (int k = 0; k < 8; ++k) vk[q][k] = vb[k * KROW];
+    }
+    for (int mt = 0; mt < MT; ++mt) {
+      const float *pa = Ps + (mt * 16 + lr) * PROW + lg * (TC / 4);
+      const float4 pa0 = *(const float4 *)pa, pa1 = *(const float4 *)(pa + 4);
+      const float pk[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
+      f32x4_t o[DT];
+#pragma unroll
+      for (int q = 0; q < DT; ++q) o[q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int q = 0; q < DT; ++q) o[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(pk[k], vk[q][k], o[q], 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < DT; ++q) {
+        const int nd = wave * DT + q;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int qi = mt * 16 + 4 * lg + r;
-          if (qi < nq) p.po[(((size_t)hkv * p.nchunk + c) * nq + qi) * HD + nd * 16 + lr] = o[r];
+          if (qi < nq) p.po[(((size_t)hkv * p.nchunk + c) * nq + qi) * HD + nd * 16 + lr] = o[q][r];
         }
       }
     }
+    c += gridDim.x;
+    if (c * TC > tlast) break;
+    lds_barrier();                              // this chunk's reads of K, V and P done
+    land(c);
   }
 }
 
