@@ -158,7 +158,7 @@ __device__ __forceinline__ void raise_flag(int *flag) {
 constexpr int CWEN_MAX_PARTS = 128;
 
 // ------------------------------------------------------------ gemv.hip
-enum { GEMV_EPI_STORE = 0, GEMV_EPI_PAIR = 1, GEMV_EPI_SWIGLU = 2, GEMV_EPI_ARGMAX = 3 };
+enum { GEMV_EPI_STORE = 0, GEMV_EPI_PAIR = 1, GEMV_EPI_SWIGLU = 2, GEMV_EPI_ARGMAX = 3, GEMV_EPI_CONV = 4 };
 struct ArgmaxOut {
   unsigned long long *keys;  // per-column keys, zero between launches
   int *cnt;                  // arrival counter, zero between launches
@@ -175,6 +175,16 @@ struct GemvOut {
   ArgmaxOut am;      // ARGMAX only
   float *ssq;        // STORE: per row tile, the sum of squares of the final y per column [row tile][CWEN_BMAX]
   const float *nwh;  // with yh: the f16 copy holds y * nwh[row] (the next RMSNorm's weight), nullable
+  // CONV (a STORE whose rows < cv_C are GatedDeltaNet q/k/v channels): they get the
+  // depthwise causal conv + SiLU (run.c conv1d_update) instead of a store:
+  // position b of channel c goes to the pending buffer, cv_xc[(P*BMAX + b)*
+  // cv_C + c], and its inputs b-2, b-1, b to history slot (cur + 1 + b) %
+  // cv_nslot, cv_H[slot*3*cv_C + 3c ..], with cur = cv_ctl[0], P = cv_ctl[3];
+  // positions before the block come from slot cur.  cv_w: [cv_C][4] taps.
+  const float *cv_w;
+  float *cv_H, *cv_xc;
+  const int *cv_ctl;
+  int cv_C, cv_nslot;
   int *rflag;        // with yh: set to 1 when an f16 value written is not finite (out of f16's range), nullable
 };
 // f32 activations that the GEMV converts to its f16 operand while staging.
@@ -231,7 +241,11 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
                      const float *decay, const float *beta, int gs, const float *kw, const float *wn,
                      float *out, int os, int B, hipStream_t st, _Float16 *outh = nullptr, int ohs = 0,
                      const float *A = nullptr, const float *dt = nullptr, int force_L0 = 0,
-                     int *rflag = nullptr);
+                     int *rflag = nullptr, bool conv_done = false);
+// The conv's part of a GemvOut for the block's in-projection (its output
+// rows < g->C): the GEMV then does what gdn_conv_kernel would, and
+// gdn_block_launch is called with conv_done.
+void gdn_conv_out(const cwen_gdn *g, const float *kw, GemvOut &o);
 // The state after replaying L positions of pending buffer buf from base slot
 // X into S_out (device, [nvh][dk][dk]).
 int gdn_peek_launch(const cwen_gdn *g, int L, int buf, float *S_out, hipStream_t st);

@@ -83,14 +83,11 @@ struct GdnParams {
 // position (blockIdx.y).  The 4-tap filter needs no running state: the
 // inputs at b-3 .. b-1 come from the block's own rows or, before the block,
 // from the history slot the block starts from, so every position is
-// computed at once with run.c's product/sum order.  A workgroup's 256
-// channels are two whole heads, all q/k or all v (the q/k channels are
-// 2 * nkh * 128); q and k are l2-normalised here (run.c:401-423), once per
-// position, so the recurrence and a later replay read the same normalised
-// values.  Each position's thread also writes that position's history slot
-// (inputs b-2, b-1, b).
+// computed at once with run.c's product/sum order.  The pending buffer
+// holds the post-conv values; the recurrence l2-normalises q and k as it
+// stages them, for the block and for a later replay alike.  Each position's
+// thread also writes that position's history slot (inputs b-2, b-1, b).
 __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
-  __shared__ float s_ss[4];        // per wave: the wave's sum of squares
   const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
   if (c >= p.C) return;           // whole waves (C is a multiple of 128)
   const int cur = p.ctl[0], P = p.ctl[3];
@@ -110,15 +107,7 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
   float y = silu_ref(x);
   float *hs = p.H_slots + (size_t)((cur + 1 + b) % p.nslot) * p.h_floats + (size_t)c * 3;
   hs[0] = in[1]; hs[1] = in[2]; hs[2] = in[3];
-  if (blockIdx.x * 256 < 2 * p.nkh * DK) {  // q / k heads: x / sqrt(sum x^2 + 1e-6)
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const float t = sum64(y * y);
-    if (lane == 0) s_ss[wave] = t;
-    __syncthreads();
-    const int w0 = wave & ~1;  // the head's two waves, in order
-    y *= 1.f / sqrtf(s_ss[w0] + s_ss[w0 + 1] + 1e-6f);
-  }
-  p.xc[((size_t)P * CWEN_BMAX + b) * p.C + c] = y;
+  p.xc[((size_t)P * CWEN_BMAX + b) * p.C + c] = y;   // q and k are l2-normalised by the recurrence
 }
 
 // 2. recurrence: workgroup (hv, slice) = one wave, columns
@@ -166,12 +155,19 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
     for (int b0 = 0; b0 < nb; b0 += 8) {
       float qkr[8][4], vr[2];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {   // q and k of key head hk (l2-normalised by the conv)
+      for (int u = 0; u < 8; ++u) {   // q and k of key head hk
         const int b = min(b0 + u, nb - 1);
         const float *xq = xc + (size_t)b * p.C + hk * DK;
         const float *xk = xc + (size_t)b * p.C + (p.nkh + hk) * DK;
         qkr[u][0] = xq[lane]; qkr[u][1] = xq[lane + 64];
         qkr[u][2] = xk[lane]; qkr[u][3] = xk[lane + 64];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {   // l2 norms (run.c:401-423): x / sqrt(sum x^2 + 1e-6), dims 0..63 then 64..127
+        const float rq = 1.f / sqrtf(sum64(qkr[u][0] * qkr[u][0]) + sum64(qkr[u][1] * qkr[u][1]) + 1e-6f);
+        const float rk = 1.f / sqrtf(sum64(qkr[u][2] * qkr[u][2]) + sum64(qkr[u][3] * qkr[u][3]) + 1e-6f);
+        qkr[u][0] *= rq; qkr[u][1] *= rq;
+        qkr[u][2] *= rk; qkr[u][3] *= rk;
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i) {   // v: 8 positions x COLS columns, 2 per lane
@@ -309,10 +305,19 @@ static void fill_params(GdnParams &p, const cwen_gdn *g) {
   p.nkh = g->nkh; p.nvh = g->nvh; p.C = g->C;
 }
 
+void gdn_conv_out(const cwen_gdn *g, const float *kw, GemvOut &o) {
+  o.cv_w = kw;
+  o.cv_H = g->H;
+  o.cv_xc = g->xc;
+  o.cv_ctl = g->ctl;
+  o.cv_C = g->C;
+  o.cv_nslot = g->nslot;
+}
+
 int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z, int zs,
                      const float *decay, const float *beta, int gs, const float *kw, const float *wn,
                      float *out, int os, int B, hipStream_t st, _Float16 *outh, int ohs, const float *A,
-                     const float *dt, int force_L0, int *rflag) {
+                     const float *dt, int force_L0, int *rflag, bool conv_done) {
   GdnParams p;
   fill_params(p, g);
   p.force_L0 = force_L0;
@@ -325,7 +330,8 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
   p.rflag = rflag;
   p.A = A; p.dt = dt;
   p.B = B;
-  hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((g->C + 255) / 256), (unsigned)B), dim3(256), 0, st, p);
+  if (!conv_done)
+    hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((g->C + 255) / 256), (unsigned)B), dim3(256), 0, st, p);
   hipLaunchKernelGGL(gdn_rec_kernel, dim3((unsigned)(g->nvh * (DK / COLS))), dim3(64), 0, st, p);
   hipLaunchKernelGGL(gdn_norm_kernel, dim3((unsigned)(g->nvh * B)), dim3(64), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());

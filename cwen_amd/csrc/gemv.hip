@@ -467,8 +467,31 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       else buf[xslot[i]] = xs[i][0];
     }
   };
+  // CONV: the ring slot and pending buffer are read with the kernel's first
+  // scalar loads; the taps and the history this lane's conv needs are
+  // requested here, so only the epilogue waits for them.
+  int cv_cur = 0, cv_P = 0;
+  if constexpr (EPI == GEMV_EPI_CONV) {
+    cv_cur = p.out.cv_ctl[0];
+    cv_P = p.out.cv_ctl[3];
+  }
   stage_store(act[0]);
   lds_barrier();
+  float cv_h[3] = {0.f, 0.f, 0.f};
+  float4 cv_w4 = {0.f, 0.f, 0.f, 0.f};
+  const bool cv_rows = EPI == GEMV_EPI_CONV && rg * Q4_ROWS < p.out.cv_C;   // wave-uniform
+  if constexpr (EPI == GEMV_EPI_CONV) {
+    if (cv_rows) {
+      const int row = rg * Q4_ROWS + n;
+      cv_w4 = *(const float4 *)(p.out.cv_w + (size_t)row * 4);
+      if (g == 0) {
+        const float *hin = p.out.cv_H + (size_t)cv_cur * p.out.cv_C * 3 + (size_t)row * 3;
+        cv_h[0] = hin[0];
+        cv_h[1] = hin[1];
+        cv_h[2] = hin[2];
+      }
+    }
+  }
 
   const Unpack uc = unpack_consts();
   floatx4_t acc[2];
@@ -697,6 +720,40 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 
   float sq[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's share of the row tile's sum of squares
   bool bad = false;                    // an f16 copy out of range
+  if constexpr (NS == 1 && EPI == GEMV_EPI_CONV) {
+    // GatedDeltaNet conv rows: lane (g, n) holds positions 4g .. 4g+3 of
+    // channel `row`; positions 4g-3 .. 4g-1 come from lane (g-1, n), or for
+    // g = 0 from the history slot the block starts from.
+    if (cv_rows) {
+      const float p1 = __shfl(res[1], lane - 16), p2 = __shfl(res[2], lane - 16), p3 = __shfl(res[3], lane - 16);
+      if (store) {
+        const int cur = cv_cur, P = cv_P;
+        const size_t hf = (size_t)o.cv_C * 3;
+        float a[7];
+        a[0] = g == 0 ? cv_h[0] : p1;
+        a[1] = g == 0 ? cv_h[1] : p2;
+        a[2] = g == 0 ? cv_h[2] : p3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[3 + e] = res[e];
+        const float4 w = cv_w4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int b = g * 4 + e;
+          if (b >= p.B) continue;
+          // ((st0*w0 + st1*w1) + st2*w2) + xin*w3, each product and sum rounded
+          const float x = __fadd_rn(__fadd_rn(__fadd_rn(__fmul_rn(a[e], w.x), __fmul_rn(a[e + 1], w.y)),
+                                              __fmul_rn(a[e + 2], w.z)),
+                                    __fmul_rn(a[e + 3], w.w));
+          o.cv_xc[((size_t)P * CWEN_BMAX + b) * o.cv_C + row] = silu_f(x);
+          float *hs = o.cv_H + (size_t)((cur + 1 + b) % o.cv_nslot) * hf + (size_t)row * 3;
+          hs[0] = a[e + 1];
+          hs[1] = a[e + 2];
+          hs[2] = a[e + 3];
+        }
+      }
+      store = false;
+    }
+  }
   if (store) {
     float v[4];
 #pragma unroll
@@ -1254,6 +1311,12 @@ int gemv_launch(cwen_ctx *ctx, const cwen_weight *w, int nsides, int side0, int 
       rc = CWEN_OK;
     } else if (nsides == 2 && epi == GEMV_EPI_SWIGLU) {
       launch_cb<GEMV_Q4, 2, GEMV_EPI_SWIGLU>(p, nrt, st);
+      rc = CWEN_OK;
+    } else if (nsides == 1 && epi == GEMV_EPI_CONV) {
+      if (!out.cv_w || !out.cv_H || !out.cv_xc || !out.cv_ctl || out.cv_C < 0 || out.cv_C > w->ne1 || out.cv_C % Q4_ROWS ||
+          out.cv_nslot < 1)
+        return CWEN_EINVAL;
+      launch_cb<GEMV_Q4, 1, GEMV_EPI_CONV>(p, nrt, st);
       rc = CWEN_OK;
     } else {
       rc = launch_fmt<GEMV_Q4>(p, nrt, nsides, epi, st);

@@ -353,11 +353,17 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
     const cwen_weight *wout;
     if (y.linear) {
       const Rows r = rows_of(c);
+      // A Q4 in-projection applies the causal conv to its q/k/v rows as it
+      // stores them (gdn_conv_out); z and the gates are stored as they are.
+      const bool fuse_conv = y.lin_in->fmt == GEMV_Q4;
       GemvOut o1 = {m->lin, nullptr, nullptr, r.lin, 0};
-      if ((rc = gemv_launch(ctx, y.lin_in, 1, 0, GEMV_EPI_STORE, m->xh, o1, B, st, nullptr, &n1))) return rc;
+      if (fuse_conv) gdn_conv_out(y.gdn, y.ssm_conv, o1);
+      if ((rc = gemv_launch(ctx, y.lin_in, 1, 0, fuse_conv ? GEMV_EPI_CONV : GEMV_EPI_STORE, m->xh, o1, B, st,
+                            nullptr, &n1)))
+        return rc;
       const float *qkv = m->lin, *z = m->lin + r.C, *ga = m->lin + r.o_alpha, *gb = m->lin + r.o_beta;
       if ((rc = gdn_block_launch(y.gdn, qkv, r.lin, z, r.lin, ga, gb, r.lin, y.ssm_conv, y.ssm_norm, nullptr, 0, B,
-                                 st, m->gh, r.Zh, y.ssm_a, y.ssm_dt, 0, rflag)))
+                                 st, m->gh, r.Zh, y.ssm_a, y.ssm_dt, 0, rflag, fuse_conv)))
         return rc;
       GemvOut o5 = {m->X, nullptr, m->xh, H, 1};
       o5.ssq = m->ssq;
