@@ -264,8 +264,14 @@ int attention_init();
 int attention_max_group();
 // `last` is a device int: the last filled cache slot before the block (the
 // block's positions are last+1 .. last+B).  The launch shape depends on
-// (B, NH, NKV, max_ctx) only, so a captured graph replays at any position.
+// (B, NH, NKV, max_ctx) and attention_wide(last_hint) only, so a captured
+// graph replays at any position of the same band; any hint gives the same
+// result.
 int attention_launch(const float *qfull, int qfs, const float *kx, const float *vx, int kvs, const float *qn,
                      const float *kn, float *qbuf, float *K, float *V, const int *last, int B, int NH, int NKV,
                      int npairs, int nrot, float theta, float eps, float *part, int max_ctx, _Float16 *yh,
-                     hipStream_t st, int *rflag = nullptr);
+                     hipStream_t st, int *rflag = nullptr, int last_hint = -1);
+// Whether a block whose last position is last_pos takes the wide chunk grid
+// (attention_launch's last_hint; -1 = not known, narrow).  Only the launch
+// shape depends on it, never the result.
+bool attention_wide(int last_pos);

@@ -126,6 +126,7 @@ struct AttnParams {
   float *po;           // partial outputs [NKV][nchunk][B*kvm][HD]
   float *pm, *pl;      // partial max / sum [NKV][nchunk][B*kvm]
   int nchunk;
+  int nbuf;            // chunk buffers in LDS: 2 lands the next chunk during the current one
   _Float16 *yh;        // gated outputs f16 [B][NH*HD]
   int *rflag;          // set to 1 when a gated output is out of f16's range, nullable
 };
@@ -198,8 +199,11 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
   const int kvm = p.NH / p.NKV;
   const int nq = p.B * kvm;
   const int MT = (nq + 15) / 16;               // 16-query tiles
-  float *Ks = sm, *Vs = sm + TC * KROW;        // K and V rows of the chunk
-  float *Ps = sm + KV_FLOATS;                  // [MT*16][PROW]
+  // nbuf chunk buffers, K [TC][KROW] then V [TC][KROW] each; with two, the
+  // next chunk's rows land in one while the current chunk is computed from
+  // the other.
+  const bool two = p.nbuf == 2;
+  float *Ps = sm + (two ? 2 : 1) * KV_FLOATS;  // [MT*16][PROW]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
@@ -228,28 +232,40 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
   const int pbase = *p.last + 1;
   const int tlast = min(pbase + p.B - 1, p.max_ctx - 1);  // last position of the block
   if ((int)blockIdx.x * TC > tlast) return;
-  // Lands chunk c's K and V rows in LDS (rows past the block's last position
-  // as zeros); the first chunk's rows are requested with the queries in
-  // flight, so both arrive in one memory round trip.
-  auto land = [&](int c) __attribute__((always_inline)) {
+  // Lands chunk c's K and V rows in LDS buffer `bf` (rows past the block's
+  // last position as zeros): 2 * KV_R loads per wave.  The first chunk's
+  // rows are requested with the queries in flight, so both arrive in one
+  // memory round trip.
+  auto land = [&](int c, int bf) __attribute__((always_inline)) {
     const int t0 = c * TC;
     const int tn = min(TC, tlast + 1 - t0);     // keys of this chunk that exist
+    float *Kd = sm + bf * KV_FLOATS, *Vd = Kd + TC * KROW;
 #pragma unroll
     for (int u = 0; u < KV_R; ++u) {            // row t = wave + NW u: 64 lanes x 16 bytes
       const int t = wave + NW * u;
       const uint32_t row = (uint32_t)(((size_t)(t0 + t) * p.NKV + hkv) * HD * 4);
       const uint32_t vo = t < tn ? (uint32_t)lane * 16 : 0xFFFFFFE0u;   // past the last key: zeros
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void_t *)(Ks + t * KROW), 16, vo, row, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void_t *)(Vs + t * KROW), 16, vo, row, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void_t *)(Kd + t * KROW), 16, vo, row, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void_t *)(Vd + t * KROW), 16, vo, row, 0, 0);
     }
   };
-  int c = blockIdx.x;
-  land(c);
+  int c = blockIdx.x, bf = 0;
+  land(c, bf);
   for (;;) {
     const int t0 = c * TC;
     const int tn = min(TC, tlast + 1 - t0);     // keys of this chunk that exist
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's rows (and queries) have landed
-    lds_barrier();                                       // and every wave's
+    const int cn = c + (int)gridDim.x;
+    const bool more = cn * TC <= tlast;
+    // The next chunk's rows go to the other buffer (its readers finished at
+    // the previous barrier); the wait then leaves just those in flight.
+    if (more && two) {
+      land(cn, bf ^ 1);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * KV_R) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    lds_barrier();                                       // every wave's rows of chunk c
+    const float *Ks = sm + bf * KV_FLOATS, *Vs = Ks + TC * KROW;
     // scores and the chunk softmax, one 16-query tile per wave
     if (wave < MT) {
       const int mt = wave;
@@ -349,10 +365,11 @@ __global__ __launch_bounds__(64 * NW) void attn_chunk_kernel(AttnParams p) {
         }
       }
     }
-    c += gridDim.x;
-    if (c * TC > tlast) break;
+    if (!more) break;
     lds_barrier();                              // this chunk's reads of K, V and P done
-    land(c);
+    c = cn;
+    if (two) bf ^= 1;
+    else land(c, 0);
   }
 }
 
@@ -460,14 +477,23 @@ int attention_init() {
   return CWEN_OK;
 }
 
-// Chunk workgroups per kv head: enough to cover the chip at long contexts;
-// more chunks than this are looped over.
-constexpr int ATTN_CHUNK_WGS = 128;
+// Chunk workgroups per kv head and chunk buffers, by the block's context.
+// Up to ATTN_NARROW_CHUNKS chunks: 64 workgroups per head (one per CU at the
+// 27B shape's 4 kv heads), each landing its next chunk while it computes the
+// current one; two workgroups' chunks on one CU do not overlap, so more
+// workgroups only add idle ones at short contexts.  Past that, 128 per head
+// with one buffer each (two resident per CU), whose per-chunk cost grows
+// more slowly.  Measured at 24/4 heads, B = 8, contexts 1024 / 4096 / 8000:
+// 64 x 2 buffers 9.5 / 25.9 / 37.2 us, 128 x 1 buffer 14.0 / 28.0 / 34.0 us,
+// 128 x 2 buffers (one workgroup per CU) 12.7 / 29.4 / 43.7 us.
+constexpr int ATTN_NARROW_CHUNKS = 192, ATTN_NARROW_WGS = 64, ATTN_WIDE_WGS = 128;
+
+bool attention_wide(int last_pos) { return last_pos >= 0 && last_pos / TC + 1 > ATTN_NARROW_CHUNKS; }
 
 int attention_launch(const float *qfull, int qfs, const float *kx, const float *vx, int kvs, const float *qn,
                      const float *kn, float *qbuf, float *K, float *V, const int *last, int B, int NH, int NKV,
                      int npairs, int nrot, float theta, float eps, float *part, int max_ctx, _Float16 *yh,
-                     hipStream_t st, int *rflag) {
+                     hipStream_t st, int *rflag, int last_hint) {
   AttnParams p;
   p.qfull = qfull; p.qfs = qfs; p.kx = kx; p.vx = vx; p.kvs = kvs;
   p.qn = qn; p.kn = kn;
@@ -482,10 +508,13 @@ int attention_launch(const float *qfull, int qfs, const float *kx, const float *
   p.yh = yh;
   p.rflag = rflag;
   // Every check before the first launch: a block never stops half-way.
-  const int nwg = p.nchunk < ATTN_CHUNK_WGS ? p.nchunk : ATTN_CHUNK_WGS;
+  const bool wide = attention_wide(last_hint);
+  const int wgs = wide ? ATTN_WIDE_WGS : ATTN_NARROW_WGS;
+  const int nwg = p.nchunk < wgs ? p.nchunk : wgs;
+  p.nbuf = wide ? 1 : 2;
   const int MT = (nq + 15) / 16;
   if (NH % NKV || MT > NW_MAX) return CWEN_EINVAL;   // one 16-query tile per wave
-  const size_t lds = ((size_t)MT * 16 * PROW + KV_FLOATS) * sizeof(float);
+  const size_t lds = ((size_t)MT * 16 * PROW + p.nbuf * KV_FLOATS) * sizeof(float);
   if (lds > 160 * 1024) return CWEN_EINVAL;
   int rc;
   if ((rc = attention_init())) return rc;

@@ -52,13 +52,14 @@ struct cwen_model {
   int pos = -1;                  // last filled slot (host copy)
   int *ctl = nullptr;            // device: [0] last filled slot, [1..4] the GDN layers' control word
   // With CWEN_GRAPHS=1 each (mode, B) block is captured once into a graph
-  // and replayed: the launch shapes depend on (mode, B) and the weight
-  // shapes only, the position and ring slot are read from ctl on the device.
+  // per attention band and replayed: the launch shapes depend on (mode, B),
+  // the weight shapes and attention_wide(pos + B) only, the position and
+  // ring slot are read from ctl on the device.
   // Off by default: replay measured no faster than eager launches (the
   // per-kernel cost is on the device side).
   int use_graphs = 0;
   hipStream_t cap = nullptr;     // capture stream
-  hipGraphExec_t gexec[3][CWEN_BMAX] = {};
+  hipGraphExec_t gexec[3][2][CWEN_BMAX] = {};  // [mode][attention_wide][B - 1]
   int *htok = nullptr;           // pinned token staging [BMAX]
   hipEvent_t tok_ev = nullptr;   // the last staging copy has been issued past this
   // device scratch
@@ -277,7 +278,7 @@ int mtp_pass(cwen_model *m, int B, const int *toks, const float *hsrc, int hs, c
   if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, m->xh2, o1, B, st, nullptr, &n1))) return rc;
   if ((rc = attention_launch(m->att, r.att, m->att + r.Qo2, m->att + r.Qo2 + r.Ko, r.att, y.q_norm, y.k_norm,
                              m->qbuf, y.K, y.V, m->mctl, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
-                             c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st, rflag)))
+                             c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st, rflag, m->pos + B)))
     return rc;
   GemvOut o5 = {m->X2, nullptr, m->xh2, H, 1};
   o5.ssq = m->ssq2;
@@ -377,7 +378,7 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
       if ((rc = gemv_launch(ctx, y.att_in, 1, 0, GEMV_EPI_STORE, m->xh, o1, B, st, nullptr, &n1))) return rc;
       if ((rc = attention_launch(m->att, r.att, m->att + r.Qo2, m->att + r.Qo2 + r.Ko, r.att, y.q_norm, y.k_norm,
                                  m->qbuf, y.K, y.V, m->ctl, B, c.n_head, c.n_kv_head, c.n_rot_pairs, c.n_rot,
-                                 c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st, rflag)))
+                                 c.rope_theta, c.rms_eps, m->apart, c.max_ctx, m->yh, st, rflag, m->pos + B)))
         return rc;
       GemvOut o5 = {m->X, nullptr, m->xh, H, 1};
       o5.ssq = m->ssq;
@@ -414,12 +415,13 @@ int block(cwen_model *m, int B, int mode, hipStream_t st) {
 }
 
 void drop_graphs(cwen_model *m) {
-  for (auto &row : m->gexec)
-    for (hipGraphExec_t &g : row)
-      if (g) {
-        (void)hipGraphExecDestroy(g);
-        g = nullptr;
-      }
+  for (auto &mode : m->gexec)
+    for (auto &row : mode)
+      for (hipGraphExec_t &g : row)
+        if (g) {
+          (void)hipGraphExecDestroy(g);
+          g = nullptr;
+        }
 }
 
 // Stage the tokens, then run the block: replay its graph (captured on first
@@ -433,7 +435,7 @@ int run_block(cwen_model *m, const int *toks, int B, int mode, hipStream_t st) {
   CWEN_HIP_TRY(hipEventRecord(m->tok_ev, st));
   // the MTP commit's launch shape depends on the position: eager
   if (!m->use_graphs || mtp_ready(m)) return block(m, B, mode, st);
-  hipGraphExec_t &ge = m->gexec[mode][B - 1];
+  hipGraphExec_t &ge = m->gexec[mode][attention_wide(m->pos + B)][B - 1];
   if (!ge) {
     hipGraph_t g = nullptr;
     CWEN_HIP_TRY(hipStreamBeginCapture(m->cap, hipStreamCaptureModeThreadLocal));

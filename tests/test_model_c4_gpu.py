@@ -4,16 +4,20 @@ The full 27B-shape model has 24 query heads over 4 KV heads (6 per KV head),
 and its benchmark prefills 4096 tokens in blocks of 16 into an 8192-slot
 cache.  That geometry takes attention paths the small test config never
 reaches: a block of 16 positions has 96 queries per KV head (more than four
-16-query tiles, so the chunk kernel runs 8-wave workgroups), and past 4096
+16-query tiles, so the chunk kernel runs 8-wave workgroups), and past 2048
 positions the key chunks outnumber the chunk workgroups (each takes several
-chunks).
+chunks, landing the next while it computes the current one).
 
   * test_c4_geometry_vs_oracle: a 2-layer model of that geometry (one
     GatedDeltaNet layer, one full-attention layer) prefilled to 4192
     positions in blocks of 16, then a block of 16 and two blocks of 8 with
     the head.  Their logits are compared with the oracle's serial forward
     over the same 4224 tokens (tests/golden/c4_geometry_logits.npz, written
-    by make_c4_geometry_golden.py).  Tolerance (stated): rel_err <= 2e-3
+    by make_c4_geometry_golden.py).  The same over 6400 tokens
+    (c4_geometry_wide_logits.npz): past 6144 positions the chunk kernel
+    switches from 64 double-buffered workgroups per KV head to 128
+    single-buffered ones, so the prefill crosses the switch and the
+    compared blocks run the wide grid.  Tolerance (stated): rel_err <= 2e-3
     per position, rel_err = max|d| / max|ref| over the vocab.  The device
     rounds every GEMV input to f16 (MFMA operands); the fixture's f16-input
     oracle shows that this rounding alone moves the oracle's own logits by
@@ -37,6 +41,7 @@ from util import rel_err
 pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "c4_geometry_logits.npz"
+GOLDEN_WIDE = GOLDEN.with_name("c4_geometry_wide_logits.npz")
 TOL = 2e-3
 
 
@@ -70,11 +75,12 @@ def _prefill(m, toks, n, B=16):
     assert m.pos == n - 1
 
 
-def test_c4_geometry_vs_oracle(env, oracle):
+@pytest.mark.parametrize("golden", [GOLDEN, GOLDEN_WIDE], ids=["narrow", "wide"])
+def test_c4_geometry_vs_oracle(env, oracle, golden):
     gpu, ctx, m, g = env
-    fx = np.load(GOLDEN)
+    fx = np.load(golden)
     n_ctx, n_cmp = int(fx["n_ctx"]), int(fx["n_cmp"])
-    toks = g.tokens()
+    toks = g.tokens(n_ctx)
     assert len(toks) == n_ctx
     p0 = n_ctx - n_cmp
     _prefill(m, toks, p0)
@@ -96,10 +102,10 @@ def test_c4_geometry_vs_oracle(env, oracle):
 
 
 @pytest.mark.parametrize("B", [16, 8])
-def test_c4_geometry_block_equals_singles(env, B):
+@pytest.mark.parametrize("p0", [4192, 6368])
+def test_c4_geometry_block_equals_singles(env, B, p0):
     gpu, ctx, m, g = env
-    toks = g.tokens()
-    p0 = 4192
+    toks = g.tokens(g.N_CTX_WIDE)
     _prefill(m, toks, p0)
     m.forward(toks[p0:p0 + B])
     block = m.logits(B).copy()
