@@ -173,7 +173,7 @@ struct GemvOut {
   int ys;
   int accumulate;    // y += result
   ArgmaxOut am;      // ARGMAX only
-  float *ssq;        // STORE: per row tile, the sum of squares of the final y per column [row tile][CWEN_BMAX]
+  float *ssq;        // STORE: per row tile, the sum of squares of the final y per column [CWEN_BMAX][CWEN_MAX_PARTS]
   const float *nwh;  // with yh: the f16 copy holds y * nwh[row] (the next RMSNorm's weight), nullable
   // CONV (a STORE whose rows < cv_C are GatedDeltaNet q/k/v channels): they get the
   // depthwise causal conv + SiLU (run.c conv1d_update) instead of a store:
@@ -194,9 +194,9 @@ struct GemvF32 {
 };
 // RMSNorm split between producer and consumer: the f16 operand holds w * x
 // (x not yet normalised) and output column c is multiplied by
-// 1 / sqrt(sum_p ssq[p][c] / K + eps), the partials summed in a fixed order.
+// 1 / sqrt(sum_p ssq[c][p] / K + eps), the partials summed in a fixed order.
 struct GemvPost {
-  const float *ssq;  // [npart][CWEN_BMAX]
+  const float *ssq;  // [CWEN_BMAX][CWEN_MAX_PARTS], partials 0 .. npart - 1 of each column
   int npart;         // 1 .. CWEN_MAX_PARTS
   float eps;
 };
@@ -226,7 +226,7 @@ bool gemv_grid_fits(const GemvGrid &g, size_t partials_floats, int ncounters);
 // Row tiles of a launch over w: the number of ssq partials it writes.
 int gemv_row_tiles(const cwen_weight *w);
 // post (f16 operand only): the operand is w * x with x not yet normalised;
-// each output column c is scaled by 1 / sqrt(sum_p post->ssq[p][c] / K +
+// each output column c is scaled by 1 / sqrt(sum_p post->ssq[c][p] / K +
 // post->eps), completing the RMSNorm (post->x, post->w unused).
 // scr (nullable) replaces the context's split-K scratch; a decomposition that
 // does not fit it returns CWEN_ESCRATCH before any launch.
@@ -251,7 +251,7 @@ void gdn_conv_out(const cwen_gdn *g, const float *kw, GemvOut &o);
 int gdn_peek_launch(const cwen_gdn *g, int L, int buf, float *S_out, hipStream_t st);
 
 // ------------------------------------------------------------ model.hip
-// Also writes each row's sum of squares to ssq[b] (one partial per column)
+// Also writes each row's sum of squares to ssq[b][0] (one partial per column)
 // and, when xh is given, the f16 operand x * nw of the first RMSNorm.
 // rflag (nullable) is set to 1 when an f16 value written is not finite.
 int embed_launch(const uint8_t *qs, const uint16_t *sc, int type, const int *toks, int B, int H, float *X,

@@ -347,14 +347,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
 
   // Post-scale: the producer's partial sums of squares of every staged
   // column, loaded first, so that waiting for them waits for nothing else
-  // (see psc below); ssq has CWEN_MAX_PARTS = 128 rows, so the loads need no
-  // guard.
+  // (see psc below).  ssq is [column][CWEN_MAX_PARTS = 128], so a wave's
+  // load of 64 partials of one column is one contiguous 256-byte run, and the
+  // loads need no guard.
   float pp[2][CB];
   if (p.pss) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int c = 0; c < CB; ++c) pp[j][c] = p.pss[(lane + 64 * j) * CWEN_BMAX + c];
+      for (int c = 0; c < CB; ++c) pp[j][c] = p.pss[c * CWEN_MAX_PARTS + lane + 64 * j];
   }
   __builtin_amdgcn_sched_barrier(0);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.wbytes);
@@ -788,7 +789,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   if (bad) raise_flag(o.rflag);
   if (o.ssq) {
     // Sum of squares of this row tile's outputs per column, in a fixed order
-    // (rows of a wave by the DPP tree, then row groups in order): ssq[rt][c],
+    // (rows of a wave by the DPP tree, then row groups in order): ssq[c][rt],
     // the partials a normalising consumer sums.  (STORE only: NS == 1, so
     // slot == ws.)
     float *const s_sq = (float *)&act[0][0];   // [SPW][16]
@@ -803,7 +804,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       float t = s_sq[tid];
 #pragma unroll
       for (int w = 1; w < SPW; ++w) t += s_sq[w * 16 + tid];
-      o.ssq[rt * CWEN_BMAX + tid] = t;
+      o.ssq[tid * CWEN_MAX_PARTS + rt] = t;
     }
   }
 }

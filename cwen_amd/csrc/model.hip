@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *qs, const uin
   }
   // The row's sum of squares: the one partial a normalising GEMV reads.
   const float t = sum256(sq, red);
-  if (threadIdx.x == 0) ssq[b] = t;
+  if (threadIdx.x == 0) ssq[(size_t)b * CWEN_MAX_PARTS] = t;   // ssq[column][partial]: one partial
 }
 
 // ---- full attention, part 1: per (position, head) q/k RMSNorm (one shared

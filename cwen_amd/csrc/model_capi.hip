@@ -66,7 +66,7 @@ struct cwen_model {
   int *toks = nullptr;
   int *res = nullptr;            // [0] range flag copy, [1] k, [2] bonus, [3..] argmax per column
   float *X = nullptr;            // residual stream [BMAX][H]
-  float *ssq = nullptr;          // partial sums of squares of X [CWEN_MAX_PARTS][BMAX]
+  float *ssq = nullptr;          // partial sums of squares of X [BMAX][CWEN_MAX_PARTS]
   _Float16 *xh = nullptr;        // f16 operand x * w of the next RMSNorm [BMAX][H]
   float *lin = nullptr;           // GDN layer input GEMV out [BMAX][lin_rows]
   _Float16 *gh = nullptr;        // GDN output f16 [BMAX][nvh*dk]
@@ -91,7 +91,7 @@ struct cwen_model {
   float *hprev = nullptr;                              // [H] target residual of position mtp_hpos
   float *hin = nullptr, *e2 = nullptr, *X2 = nullptr;  // [BMAX][H]
   _Float16 *cat = nullptr, *xh2 = nullptr;             // [BMAX][2H], [BMAX][H]
-  float *ssq2 = nullptr;                               // [CWEN_MAX_PARTS][BMAX]
+  float *ssq2 = nullptr;                               // [BMAX][CWEN_MAX_PARTS]
   float *mlogits = nullptr;                            // [BMAX][V] logits of the draft steps
 };
 
