@@ -1,6 +1,8 @@
 // C ABI entry points of libcwen_gpu: context, weight upload, GEMV dispatch.
 #include <stdlib.h>
 #include <string.h>
+#include <atomic>
+#include <mutex>
 #include "cwen_internal.h"
 
 namespace {
@@ -40,17 +42,22 @@ __device__ __align__(256) unsigned char scratch[kStaticBytes];
 // host code the array's name is not a device address: only these are passed
 // to kernels.
 constexpr int kMaxDevices = 64;
-unsigned char *g_scratch_dev[kMaxDevices];
+std::atomic<unsigned char *> g_scratch_dev[kMaxDevices];
 
 __global__ void zero_ints_kernel(int *p, int n) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
 }
 
 // Look up this device's scratch address and clear its counters (first
-// context on the device only; `device` is current).
+// context on the device only; `device` is current).  One mutex per device
+// serialises the first-time set-up: a second thread creating a context on
+// the same GPU waits for the counters to be cleared instead of clearing them
+// again under a noalloc call already running there.
+std::mutex g_scratch_mu[kMaxDevices];
 int static_scratch_init(int device) {
-  if (device >= kMaxDevices) return CWEN_EINVAL;
-  if (g_scratch_dev[device]) return CWEN_OK;
+  if (device < 0 || device >= kMaxDevices) return CWEN_EINVAL;
+  std::lock_guard<std::mutex> lk(g_scratch_mu[device]);
+  if (g_scratch_dev[device].load(std::memory_order_acquire)) return CWEN_OK;
   unsigned char *ptr = nullptr;
   CWEN_HIP_TRY(hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch)));
   if (!ptr) return CWEN_EHIP;
@@ -58,7 +65,7 @@ int static_scratch_init(int device) {
                      kStaticCounters);
   CWEN_HIP_TRY(hipGetLastError());
   CWEN_HIP_TRY(hipDeviceSynchronize());
-  g_scratch_dev[device] = ptr;
+  g_scratch_dev[device].store(ptr, std::memory_order_release);
   return CWEN_OK;
 }
 
@@ -391,8 +398,9 @@ int cwen_mlp_block_noalloc(const cwen_weight *Wgu, const cwen_weight *Wd, const 
   if (Wgu->nside != 2 || Wd->nside != 1 || Wd->ne0 != Wgu->ne1 || Wd->ne1 != Wgu->ne0) return CWEN_EINVAL;
   if ((rc = check_act(X, xs, Wgu->ne0, B)) || (rc = check_out(Y, ys, Wd->ne1, B))) return rc;
   if (Wgu->ne0 > CWEN_STATIC_KMAX || Wgu->ne1 > CWEN_STATIC_KMAX) return CWEN_ESCRATCH;
-  if (ctx->device < 0 || ctx->device >= kMaxDevices || !g_scratch_dev[ctx->device]) return CWEN_EINVAL;
-  unsigned char *const base = g_scratch_dev[ctx->device];
+  if (ctx->device < 0 || ctx->device >= kMaxDevices) return CWEN_EINVAL;
+  unsigned char *const base = g_scratch_dev[ctx->device].load(std::memory_order_acquire);
+  if (!base) return CWEN_EINVAL;
   const GemvScratch scr = {(float *)(base + kStaticPartOfs), kStaticPartialFloats, (int *)(base + kStaticCntOfs),
                            kStaticCounters};
   // Both launches' decompositions are checked before the first launch.

@@ -136,7 +136,6 @@ __device__ __forceinline__ float sum64(float v) {
          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
 }
 
-// run.c:378-384 silu_one: x * (1 / (1 + exp(-x)))
 // LDS hand-off barrier: waits for this wave's LDS writes only, not for its
 // outstanding global loads (unlike __syncthreads(), whose release fence
 // drains the memory counter: loads and stores in flight).
@@ -144,6 +143,7 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // gfx9 encoding: lgkmcnt(0), vmcnt/expcnt unchanged
   __builtin_amdgcn_s_barrier();
 }
+// run.c:378-384 silu_one: x * (1 / (1 + exp(-x)))
 __device__ __forceinline__ float silu_f(float x) { return x * (1.f / (1.f + expf(-x))); }
 
 // An f16 operand that is not finite: the f32 value left f16's range (or was

@@ -189,6 +189,13 @@ int main(int argc, char **argv) {
   env_num("CWEN_CTX", 64, CTX_MAX, &ctx_len);
   env_flag("CWEN_SERVER", &server);
   env_flag("CWEN_MTP", &want_mtp);
+  /* run.c:4045-4050: the default minimum (2) above a lowered maximum is
+     refused before the model loads, not left to drop every proposal */
+  if (scfg.min_draft > scfg.max_draft) {
+    fprintf(stderr, "cwen_run: CWEN_SPEC_MIN_DRAFT (%d) exceeds CWEN_SPEC_MAX_DRAFT (%d)\n", scfg.min_draft,
+            scfg.max_draft);
+    return 1;
+  }
   if (draft_tokens > 0) {   /* the flag wins over the environment */
     scfg.max_draft = draft_tokens;
     spec = 1;

@@ -133,7 +133,9 @@ int cwen_mlp_block(cwen_ctx *ctx, const cwen_weight *Wgu, const cwen_weight *Wd,
  * arrival counters) is one static device array of CWEN_STATIC_SCRATCH_BYTES
  * per GPU, held until the process ends; its address on a device is looked up
  * when the first context is created there (cwen_ctx_create), so Wgu and Wd
- * must come from a context.  Limits: d_model and d_ffn (Wgu's ne0 and ne1)
+ * must come from a context, and that first cwen_ctx_create on a GPU must
+ * return before any noalloc call runs there (it clears the array's arrival
+ * counters; concurrent first creations on one GPU are serialised).  Limits: d_model and d_ffn (Wgu's ne0 and ne1)
  * at most CWEN_STATIC_KMAX, and launch decompositions whose split-K pieces
  * fit the array (every 27B-shape FFN does); beyond them it returns
  * CWEN_ESCRATCH before any launch.  Every call on a GPU shares that GPU's

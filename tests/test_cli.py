@@ -71,6 +71,8 @@ def test_bad_arguments_exit_2(args, why):
     ({"CWEN_SPEC_NGRAM_N": "1"}, b"CWEN_SPEC_NGRAM_N must be an integer in [2, 256]"),
     ({"CWEN_SPEC_MAX_DRAFT": "16"}, b"CWEN_SPEC_MAX_DRAFT must be an integer in [1, 15]"),
     ({"CWEN_SPEC_MAX_DRAFT": "4", "CWEN_SPEC_MIN_DRAFT": "5"}, b"CWEN_SPEC_MIN_DRAFT must be an integer in [1, 4]"),
+    # run.c:4045-4050: the default minimum draft (2) above a maximum of 1
+    ({"CWEN_SPEC_MAX_DRAFT": "1"}, b"CWEN_SPEC_MIN_DRAFT (2) exceeds CWEN_SPEC_MAX_DRAFT (1)"),
     ({"CWEN_SPEC_COOLDOWN": "-1"}, b"CWEN_SPEC_COOLDOWN must be an integer"),
     ({"CWEN_CTX": "63"}, b"CWEN_CTX must be an integer in [64, 32768]"),
     ({"CWEN_CTX": "4k"}, b"CWEN_CTX must be an integer"),
