@@ -52,7 +52,8 @@
 //  * Each wave keeps one super-tile per weight stream in flight; every global
 //    load in the loop is unconditional and issued in a fixed order (scales,
 //    staging, then tiles), so the in-order load counter only waits for the
-//    data being consumed.
+//    data being consumed.  Weight loads are non-temporal (read once); the
+//    staged activations use the default policy.
 #include <algorithm>
 #include <type_traits>
 #include <vector>
@@ -399,12 +400,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
   using ScT = std::conditional_t<DM, uint4, uint2>;
   ScT sc[PD];
   auto sc_load = [&](uint32_t soff) __attribute__((always_inline)) -> ScT {
-    if constexpr (DM) return bload16(wr, ls, soff);
-    else return bload8(wr, ls, soff);
+    if constexpr (DM) return bload16_nt(wr, ls, soff);
+    else return bload8_nt(wr, ls, soff);
   };
   uint4 h5[PD];               // Q5_K: fifth bits of the round's 4 tiles (one dword each)
   auto h5_load = [&](uint32_t soff) __attribute__((always_inline)) -> uint4 {
-    if constexpr (FMT == GEMV_Q5K) return bload16(wr, F::HI_OFS + lq, soff);
+    if constexpr (FMT == GEMV_Q5K) return bload16_nt(wr, F::HI_OFS + lq, soff);
     else return make_uint4(0u, 0u, 0u, 0u);
   };
   uint32_t dq[PD] = {};       // Q6_K: f16 d of the round's two super-blocks
@@ -431,13 +432,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     const uint32_t ok = wofs + (uint32_t)(k < nround ? k : nround - 1) * sstride;
     sc[k] = sc_load(ok);
     h5[k] = h5_load(ok);
-    if constexpr (FMT == GEMV_Q6K) dq[k] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, ok, 0);
+    if constexpr (FMT == GEMV_Q6K) dq[k] = bload4_nt(wr, F::D_OFS + n * 4, ok);
 #pragma unroll
     for (int t = 0; t < TW; ++t) {
 #pragma unroll
-      for (int v = 0; v < TV; ++v) wq[k][t][v] = bload16(wr, tile_ofs(t, v), ok);
+      for (int v = 0; v < TV; ++v) wq[k][t][v] = bload16_nt(wr, tile_ofs(t, v), ok);
       if constexpr (FMT == GEMV_Q6K) {
-        if (t & 1) hq[k][t >> 1] = bload16(wr, F::HI_OFS + ((jb + t) >> 1) * 1024 + lq, ok);
+        if (t & 1) hq[k][t >> 1] = bload16_nt(wr, F::HI_OFS + ((jb + t) >> 1) * 1024 + lq, ok);
       }
       __builtin_amdgcn_sched_barrier(0);  // issue the ring in slot order
     }
@@ -540,7 +541,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
     const uint4 h5c = h5[cur % PD];  // Q5_K: this round's fifth bits (the set is reloaded for round rd + PD)
     sc[cur % PD] = sc_load(wofs + nw * sstride);
     if constexpr (FMT == GEMV_Q5K) h5[cur % PD] = h5_load(wofs + nw * sstride);
-    if constexpr (FMT == GEMV_Q6K) dq[cur % PD] = __builtin_amdgcn_raw_buffer_load_b32(wr, F::D_OFS + n * 4, wofs + nw * sstride, 0);
+    if constexpr (FMT == GEMV_Q6K) dq[cur % PD] = bload4_nt(wr, F::D_OFS + n * 4, wofs + nw * sstride);
     stage_load(nr);
     // LDS operands one tile ahead of their MFMAs: tile t + 1's reads are in
     // flight while tile t's products issue.
@@ -585,9 +586,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvParams p) {
       // Refill the slots once their registers are consumed, so the loads
       // land in the same registers (no loop-carried copies, no counter drain).
 #pragma unroll
-      for (int v = 0; v < TV; ++v) wq[cur % PD][t][v] = bload16(wr, tile_ofs(t, v), wofs + nw * sstride);
+      for (int v = 0; v < TV; ++v) wq[cur % PD][t][v] = bload16_nt(wr, tile_ofs(t, v), wofs + nw * sstride);
       if constexpr (FMT == GEMV_Q6K) {
-        if (t & 1) hq[cur % PD][t >> 1] = bload16(wr, F::HI_OFS + ((jb + t) >> 1) * 1024 + lq, wofs + nw * sstride);
+        if (t & 1) hq[cur % PD][t >> 1] = bload16_nt(wr, F::HI_OFS + ((jb + t) >> 1) * 1024 + lq, wofs + nw * sstride);
       }
       half8_t a[4];
 #pragma unroll
