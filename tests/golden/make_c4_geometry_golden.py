@@ -13,9 +13,15 @@ serial oracle steps there.
 The model and the tokens come from the seeded generators of cwen_amd.synth
 (numpy PCG64 streams), so only the outputs are stored: for each compared
 position the logits of the oracle's serial forward (tests/model_oracle.py,
-composed from the C restatement), and the same with every GEMV input rounded
-to f16 first (the device's operand precision), which measures how sensitive
-each position is to that rounding.
+composed from the C restatement) -- "ref"; the same with every GEMV input
+rounded to f16 first -- "ref16"; the oracle's device-rounding mode
+(tests/device_round.py) -- "refdev"; and "jit", how far that mode's logits
+move when each f16 operand is perturbed by 1e-6 * max|x| first (the larger of
+two seeded trials), the position's sensitivity to f32-level differences.
+
+    python tests/golden/make_c4_geometry_golden.py --device [--wide]
+
+adds "refdev" and "jit" to an existing file (three more serial passes).
 """
 from __future__ import annotations
 
@@ -72,8 +78,44 @@ def main(n_ctx: int = N_CTX, out_path: Path = OUT) -> None:
     print(f"wrote {out_path}")
 
 
+JITTER = 1e-6
+
+
+def add_device(n_ctx: int, out_path: Path) -> None:
+    """Adds the device-rounding mode's logits and their sensitivity."""
+    import device_round
+    from cwen_amd import synth
+    from model_oracle import OracleModel
+    from oracle.binding import Oracle
+    sys.path.insert(0, str(ROOT / "tests"))
+    from util import rel_err
+    O = Oracle()
+    tensors = list(synth.model_tensors(CFG, seed=SEED))
+    toks = tokens(n_ctx)
+    old = dict(np.load(out_path))
+    runs = []
+    for trial in range(3):
+        t0 = time.time()
+        device_round.JITTER = 0.0 if trial == 0 else JITTER
+        device_round.seed_jitter(trial)
+        om = OracleModel(O, CFG, tensors, device=True)
+        rows = []
+        for p, t in enumerate(toks):
+            lg = om.step(int(t), p)
+            if p >= n_ctx - N_CMP:
+                rows.append(lg)
+        runs.append(np.stack(rows).astype(np.float32))
+        print(f"device trial {trial}: {time.time() - t0:.0f} s", flush=True)
+    device_round.JITTER = 0.0
+    jit = np.array([max(rel_err(runs[1][i], runs[0][i]), rel_err(runs[2][i], runs[0][i])) for i in range(N_CMP)])
+    old["refdev"], old["jit"] = runs[0], jit.astype(np.float64)
+    np.savez_compressed(out_path, **old)
+    print(f"wrote {out_path}: jit max {jit.max():.2e}")
+
+
 if __name__ == "__main__":
-    if "--wide" in sys.argv:
-        main(N_CTX_WIDE, OUT_WIDE)
+    n, path = (N_CTX_WIDE, OUT_WIDE) if "--wide" in sys.argv else (N_CTX, OUT)
+    if "--device" in sys.argv:
+        add_device(n, path)
     else:
-        main()
+        main(n, path)

@@ -9,13 +9,21 @@ T_F32, T_Q4_0RS, T_Q4_0RSI, T_Q6_K = 0, 101, 102, 14
 
 
 class OracleModel:
-    """f16_inputs: round every GEMV input to f16 first -- the one precision
-    choice of the device path (its MFMA operands are f16), used by the tests
-    to measure how sensitive a position's logits are to that rounding."""
+    """f16_inputs: round every GEMV input to f16 first, used by the tests to
+    measure how sensitive a position's logits are to that rounding.
 
-    def __init__(self, O, cfg: dict, tensors, f16_inputs: bool = False):
+    device: round where the device rounds (tests/device_round.py) -- f16
+    weights from each format's one-rounding formula, f16 GEMV operands, an
+    RMSNorm input rounded as f16(x * w) with the norm scale applied to the
+    GEMV's output -- and sum the GEMVs in float64; everything else is the
+    C restatement, as in the other modes.  The device's logits differ from
+    this mode only by the order of its f32 sums."""
+
+    def __init__(self, O, cfg: dict, tensors, f16_inputs: bool = False, device: bool = False):
         self.O, self.c = O, cfg
         self.f16_inputs = f16_inputs
+        self.device = device
+        self.w16 = {}
         self.g = {}
         self.t = {}
         for layer, tid, wtype, data, sc, ne0, ne1 in tensors:
@@ -44,11 +52,32 @@ class OracleModel:
         self.V[NL] = np.zeros_like(self.K[NL])
         self.hprev, self.hpos = None, -1
 
+    def _w16(self, layer, tid, side):
+        key = (layer, tid, side)
+        if key not in self.w16:
+            import device_round
+            wtype, data, sc, ne0, ne1 = self.t[(layer, tid)]
+            self.w16[key] = device_round.weights(wtype, data, sc, ne0, ne1, side)
+        return self.w16[key]
+
     def mv(self, layer, tid, x, side=0):
+        """GEMV of tensor (layer, tid) on input x."""
+        if self.device:
+            import device_round
+            return device_round.gemv(self._w16(layer, tid, side), device_round.operand(x))
         wtype, data, sc, ne0, ne1 = self.t[(layer, tid)]
         if self.f16_inputs:
             x = x.astype(np.float16).astype(np.float32)
         return self.O.gemvb(wtype, data, sc, ne0, ne1, x[None, :], side)[0]
+
+    def mvn(self, layer, tid, x, wn, side=0):
+        """GEMV of tensor (layer, tid) on rmsnorm(x, wn) (run.c:346-368)."""
+        if self.device:
+            import device_round
+            xw = np.asarray(x, np.float32) * np.asarray(wn, np.float32)
+            return device_round.gemv(self._w16(layer, tid, side), device_round.operand(xw),
+                                     device_round.norm_scale(x, self.c["rms_eps"]))
+        return self.mv(layer, tid, self.O.rmsnorm(x, wn), side)
 
     def f32(self, layer, tid):
         return self.t[(layer, tid)][1]
@@ -74,11 +103,11 @@ class OracleModel:
         """layer_linear (run.c:2323-2358): the GatedDeltaNet sublayer, then the MLP."""
         from cwen_amd import gpu as G
         O, c = self.O, self.c
-        xb = O.rmsnorm(x, self.f32(l, G.ATTN_NORM))
-        qkv = self.mv(l, G.ATTN_QKV, xb)
-        z = self.mv(l, G.ATTN_GATE, xb)
-        a = self.mv(l, G.SSM_ALPHA, xb)
-        b = self.mv(l, G.SSM_BETA, xb)
+        wn = self.f32(l, G.ATTN_NORM)
+        qkv = self.mvn(l, G.ATTN_QKV, x, wn)
+        z = self.mvn(l, G.ATTN_GATE, x, wn)
+        a = self.mvn(l, G.SSM_ALPHA, x, wn)
+        b = self.mvn(l, G.SSM_BETA, x, wn)
         A, dt = self.f32(l, G.SSM_A), self.f32(l, G.SSM_DT)
         xa = (a + dt).astype(np.float32)
         sp = np.where(xa > 20, xa, np.log(np.float32(1) + np.exp(xa))).astype(np.float32)
@@ -93,23 +122,23 @@ class OracleModel:
     def full_layer(self, l, x, pos):
         """layer_full (run.c:2412-2458): gated attention over slots 0..pos, then the MLP."""
         from cwen_amd import gpu as G
-        xb = self.O.rmsnorm(x, self.f32(l, G.ATTN_NORM))
-        return self.mlp(l, self.full_attn(l, x, xb, pos, 0))
+        return self.mlp(l, self.full_attn(l, x, self.f32(l, G.ATTN_NORM), pos, 0))
 
     def head(self, x):
         """The head tail of forward_ex (run.c:2640-2644)."""
         from cwen_amd import gpu as G
-        return self.mv(-1, G.OUTPUT, self.O.rmsnorm(x, self.f32(-1, G.OUTPUT_NORM)))
+        return self.mvn(-1, G.OUTPUT, x, self.f32(-1, G.OUTPUT_NORM))
 
-    def full_attn(self, l, x, xb, pos, t0):
-        """layer_full (run.c:2412-2458): x + the gated attention over slots t0..pos."""
+    def full_attn(self, l, x, wn, pos, t0):
+        """layer_full (run.c:2412-2458): x + the gated attention over slots
+        t0..pos, on rmsnorm(x, wn)."""
         from cwen_amd import gpu as G
         O, c = self.O, self.c
         NH, NKV, HD = c["n_head"], c["n_kv_head"], c["head_dim"]
-        qf = self.mv(l, G.ATTN_Q, xb).reshape(NH, 2, HD)
+        qf = self.mvn(l, G.ATTN_Q, x, wn).reshape(NH, 2, HD)
         q, gate = qf[:, 0].copy(), qf[:, 1].copy()
-        k = self.mv(l, G.ATTN_KV, xb, 0).reshape(NKV, HD)
-        v = self.mv(l, G.ATTN_KV, xb, 1).reshape(NKV, HD)
+        k = self.mvn(l, G.ATTN_KV, x, wn, 0).reshape(NKV, HD)
+        v = self.mvn(l, G.ATTN_KV, x, wn, 1).reshape(NKV, HD)
         qn, kn = self.f32(l, G.ATTN_Q_NORM), self.f32(l, G.ATTN_K_NORM)
         q = np.stack([O.rmsnorm(q[h], qn) for h in range(NH)])
         k = np.stack([O.rmsnorm(k[h], kn) for h in range(NKV)])
@@ -122,23 +151,27 @@ class OracleModel:
     def mlp(self, l, x):
         from cwen_amd import gpu as G
         O = self.O
-        xb = O.rmsnorm(x, self.f32(l, G.POST_NORM))
-        h = O.silu_mul(self.mv(l, G.FFN_GATE_UP, xb, 0), self.mv(l, G.FFN_GATE_UP, xb, 1))
+        wn = self.f32(l, G.POST_NORM)
+        h = O.silu_mul(self.mvn(l, G.FFN_GATE_UP, x, wn, 0), self.mvn(l, G.FFN_GATE_UP, x, wn, 1))
         return (x + self.mv(l, G.FFN_DOWN, h)).astype(np.float32)
 
-    def mtp_step(self, tok: int, pos: int, h: np.ndarray) -> np.ndarray:
-        """mtp_step (run.c:3099-3133): the nextn block at stream slot pos on
-        token tok and predecessor hidden h; returns the shared-head-normed
-        hidden.  The stream's attention covers slots 1..pos."""
+    def mtp_block(self, tok: int, pos: int, h: np.ndarray) -> np.ndarray:
+        """The nextn block of mtp_step (run.c:3099-3133) at stream slot pos on
+        token tok and predecessor hidden h, before the shared head norm.  The
+        stream's attention covers slots 1..pos."""
         from cwen_amd import gpu as G
         O, NL = self.O, self.c["n_layers"]
         wtype, qs, sc, H, _ = self.t[(-1, G.TOK_EMBD)]
         e = O.embed(wtype, qs, sc, int(tok), H)
         cat = np.concatenate([O.rmsnorm(e, self.f32(-1, G.NEXTN_ENORM)), O.rmsnorm(h, self.f32(-1, G.NEXTN_HNORM))])
         x = self.mv(-1, G.NEXTN_EH_PROJ, cat.astype(np.float32))
-        x = self.full_attn(NL, x, O.rmsnorm(x, self.f32(NL, G.ATTN_NORM)), pos, 1)
-        x = self.mlp(NL, x)
-        return O.rmsnorm(x, self.f32(-1, G.NEXTN_SHEAD_NORM))
+        x = self.full_attn(NL, x, self.f32(NL, G.ATTN_NORM), pos, 1)
+        return self.mlp(NL, x)
+
+    def mtp_step(self, tok: int, pos: int, h: np.ndarray) -> np.ndarray:
+        """mtp_step (run.c:3099-3133): the shared-head-normed hidden."""
+        from cwen_amd import gpu as G
+        return self.O.rmsnorm(self.mtp_block(tok, pos, h), self.f32(-1, G.NEXTN_SHEAD_NORM))
 
     def mtp_commit(self, pos: int, tok: int, x_pre: np.ndarray) -> None:
         """mtp_commit (run.c:3150-3163): step the committed position (from
@@ -159,7 +192,9 @@ class OracleModel:
         from cwen_amd import gpu as G
         assert self.hpos == pos
         h, out = self.hprev, []
+        shn = self.f32(-1, G.NEXTN_SHEAD_NORM)
         for t, tok in enumerate([pend] + list(inputs)):
-            h = self.mtp_step(int(tok), pos + 1 + t, h)
-            out.append(self.mv(-1, G.OUTPUT, h))
+            x = self.mtp_block(int(tok), pos + 1 + t, h)
+            h = self.O.rmsnorm(x, shn)
+            out.append(self.mvn(-1, G.OUTPUT, x, shn))
         return np.stack(out)

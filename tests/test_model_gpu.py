@@ -4,18 +4,17 @@ on a small config of the same hybrid architecture.
 Checked:
   * forward parity: per-position logits of the device forward pass vs the
     oracle's serial forward composed from its C restatements
-    (tests/model_oracle.py).  Tolerance (stated), per position p:
-        rel_err(device, oracle) <= 1e-2 + 2 * rel_err(oracle16, oracle)
-    where oracle16 is the same oracle with every GEMV input rounded to f16
-    (the device's operand precision).  Every GEMV and state on the path is
-    within 1e-3 of the oracle (their own tests); over the layers the f16
-    operand rounding compounds, and at an ill-conditioned position of this
-    random-init model (position 14 of the 70-token case) rounding the inputs
-    alone moves the oracle's own logits by 1.4e-2 -- in either direction,
-    depending on how the roundings fall.  The second term allows exactly
-    that measured spread, and the whole bound is capped at 4e-2.  The fixed
-    1e-3 bound at the native dimensions over all 64 layers is
-    tests/test_model_drift_gpu.py's.
+    (tests/model_oracle.py) in its device-rounding mode: every weight and
+    GEMV operand rounded to f16 where the device rounds it
+    (tests/device_round.py), sums in float64.  Tolerance (stated), per
+    position: rel_err(device, oracle_device) <= 1e-4, rel_err = max|d| /
+    max|ref| over the vocab.  What is left between the two is the order of
+    the device's f32 sums.  The device-rounding mode itself is pinned to the
+    plain oracle on the CPU (tests/test_device_round.py); f16 rounding moves
+    this random-init model's logits by up to ~1e-2 at ill-conditioned
+    positions, so a bound against the plain oracle would have to be that
+    loose.  The fixed 1e-3 bound against run.c at the native dimensions over
+    all 64 layers is tests/test_model_drift_gpu.py's.
   * block == serial, bit for bit: one block of B positions gives the same
     logits as B single-position passes (the property spec == serial rests on).
   * verify with crafted drafts walks and rolls back exactly: accepted drafts
@@ -31,7 +30,9 @@ from util import rel_err
 
 pytestmark = pytest.mark.gpu
 CWEN_BMAX = 16
-TOL_CAP = 4e-2
+TOL_DEV = 1e-4    # device vs the oracle's device-rounding mode, plus JIT_FACTOR x the position's sensitivity
+JITTER = 1e-6     # relative perturbation before each f16 rounding that the sensitivity is measured with
+JIT_FACTOR = 2.0
 
 CFG = dict(n_layers=4, d_model=1024, d_ffn=2048, vocab=4096, n_head=4, n_kv_head=2, head_dim=256,
            n_rot_pairs=32, n_rot=64, gdn_nkh=2, gdn_nvh=4, gdn_dk=128, full_interval=4, max_ctx=512,
@@ -54,17 +55,32 @@ def env():
     torch.cuda.synchronize()
 
 
-def _oracle_logits(oracle, tensors, toks):
-    """The oracle's logits per position and the stated tolerance per position
-    (module docstring): 1e-2 plus twice the spread that rounding the GEMV
-    inputs to f16 causes in the oracle itself."""
+def _oracle_logits(oracle, tensors, toks, cfg=None):
+    """The oracle's device-rounding logits per position and the stated
+    tolerance per position (module docstring)."""
+    import device_round
     from model_oracle import OracleModel
-    OM = OracleModel(oracle, CFG, tensors)
+    OM = OracleModel(oracle, cfg or CFG, tensors, device=True)
     ref = np.stack([OM.step(t, p) for p, t in enumerate(toks)])
-    O16 = OracleModel(oracle, CFG, tensors, f16_inputs=True)
-    ref16 = np.stack([O16.step(t, p) for p, t in enumerate(toks)])
-    tol = np.array([min(1e-2 + 2 * rel_err(ref16[p], ref[p]), TOL_CAP) for p in range(len(toks))])
-    return ref, tol
+    jit = np.zeros(len(toks))
+    try:
+        device_round.JITTER = JITTER
+        for trial in (1, 2):
+            device_round.seed_jitter(trial)
+            OJ = OracleModel(oracle, cfg or CFG, tensors, device=True)
+            jit = np.maximum(jit, [rel_err(OJ.step(t, p), ref[p]) for p, t in enumerate(toks)])
+    finally:
+        device_round.JITTER = 0.0
+    return ref, TOL_DEV + JIT_FACTOR * jit
+
+
+def _check(got, ref, tol, what=""):
+    errs = [rel_err(got[p], ref[p]) for p in range(len(ref))]
+    worst = max(range(len(errs)), key=lambda p: errs[p] / tol[p])
+    print(f"{what}: max rel_err vs the device-rounding oracle {max(errs):.2e}; "
+          f"worst err / tol {errs[worst] / tol[worst]:.2f} at position {worst} (tol {tol[worst]:.2e})", flush=True)
+    for p, e in enumerate(errs):
+        assert e <= tol[p], (p, e, tol[p])
 
 
 def test_forward_parity_vs_oracle(env, oracle):
@@ -80,8 +96,7 @@ def test_forward_parity_vs_oracle(env, oracle):
         for b in range(B):
             assert am[b] == oracle.argmax(lg[b])   # the head's argmax is exact on its own logits
     got = np.concatenate(got)
-    for p in range(len(toks)):
-        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
+    _check(got, ref, tol, "two blocks")
     assert m.pos == len(toks) - 1
 
 
@@ -101,8 +116,7 @@ def test_forward_parity_across_key_chunks(env, oracle):
         assert all(am[i] == oracle.argmax(got[-1][i]) for i in range(B))
         b0 += B
     got = np.concatenate(got)
-    for p in range(len(toks)):
-        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
+    _check(got, ref, tol, "70 positions across key chunks")
 
 
 def test_real_model_types(env, oracle):
@@ -124,8 +138,7 @@ def test_real_model_types(env, oracle):
         m.forward(toks[b0:b0 + B])
         got.append(m.logits(B))
     got = np.concatenate(got)
-    for p in range(len(toks)):
-        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
+    _check(got, ref, tol, "real model types")
     m.reset()
     singles = []
     for p in range(8):
@@ -160,8 +173,7 @@ def test_context_not_a_multiple_of_the_chunk(env, oracle):
         b0 += B
     got = np.concatenate(got)
     assert m.pos == 76
-    for p in range(len(toks)):
-        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
+    _check(got, ref, tol, "max_ctx 77")
     m.reset()
     for b in range(0, 64, 16):
         m.forward(toks[b:b + 16])
@@ -193,8 +205,7 @@ def test_q6_k_embedding(env, oracle):
     ref, tol = _oracle_logits(oracle, rest + [q6], toks)
     m.forward(toks)
     got = m.logits(len(toks))
-    for p in range(len(toks)):
-        assert rel_err(got[p], ref[p]) <= tol[p], (p, rel_err(got[p], ref[p]), tol[p])
+    _check(got, ref, tol, "Q6_K embedding")
     # (2) the same values through both layouts
     g = np.random.default_rng(10)
     n = g.integers(0, 16, (V, H)).astype(np.uint8)
