@@ -5,9 +5,11 @@ Workload (one "step"): the 27B-shape FFN of a draft block of B activation rows,
   launch 1  gate/up 17408x5120 Q4_0 CWENR-RSI pair, SwiGLU fused  -> h [B][17408]
   launch 2  down    5120x17408 Q4_0 CWENR-RS                       -> y [B][5120]
 with seeded synthetic weights (f16 scales |N(0,0.02)|/8, nibbles uniform) and
-f32 N(0,1) activations.  The headline is B=8; B=1 and B=16 are reported beside
-it.  Four independent weight copies (600 MB, more than the 256 MB MALL) are
-rotated step by step so every step streams its weights from HBM.
+f32 N(0,1) activations.  The headline is B=8; B=1, 4 and 16 are reported
+beside it.  Eight independent weight copies are rotated step by step, so every
+launch streams its weights from HBM: 8 x 100 MB gate/up and 8 x 50 MB down,
+each kernel's rotation more than the 256 MB MALL (four copies of down, 200
+MB, would partly hit it when down is timed alone).
 
 Prints ONE JSON line (driver contract).  `--gpus N` with N > 1 exits: this
 build runs on one GPU.
@@ -30,7 +32,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "verified tok/s + HBM GB/s (% of peak), Q4_0 27B-shape verify B=1/8/16"
 H, I = 5120, 17408
 PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
-NCOPIES = 4
+NCOPIES = 8
 COPY_BYTES = 256 << 20     # calibration copy for the counter profile
 TRAFFIC_FILE = "q4_gemv_swiglu_ffn_b8_traffic.json"
 
@@ -79,6 +81,35 @@ def calibrate_copy(nbytes: int = COPY_BYTES, reps: int = 3) -> None:
         dst.copy_(src)
         torch.cuda.synchronize()
     del src, dst
+
+
+def hbm_ceiling(reps: int = 20) -> dict:
+    """Plain device copies and reads of known size on this GPU (torch's own
+    copy and sum kernels): the bandwidth a streaming kernel reaches here,
+    beside the 8 TB/s vendor peak.  Buffers are rotated so each launch
+    streams from HBM (> 256 MB MALL).  Mean over back-to-back launches
+    between events, as the GEMV legs are timed."""
+    import torch
+    out = {}
+    stream = torch.cuda.current_stream()
+    for name, nbytes, nbuf in (("copy_256MiB", 256 << 20, 4), ("copy_100MB", 100_270_080, 6)):
+        n = nbytes // 4
+        src = [torch.ones(n, dtype=torch.float32, device="cuda") for _ in range(nbuf)]
+        dst = [torch.empty_like(src[0]) for _ in range(nbuf)]
+        ms = time_launches(lambda i: dst[i % nbuf].copy_(src[(i + 1) % nbuf]), reps, 3, stream)
+        out[name] = {"ms": round(ms, 5), "GB_s": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1),
+                     "frac_of_peak": round(2 * n * 4 / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes_read_written": 2 * n * 4}
+        del src, dst
+    n = 100_270_080 // 4
+    bufs = [torch.ones(n, dtype=torch.float32, device="cuda") for _ in range(6)]
+    acc = torch.empty((), device="cuda")
+    ms = time_launches(lambda i: torch.sum(bufs[i % 6], dim=0, out=acc), reps, 3, stream)
+    out["read_100MB"] = {"ms": round(ms, 5), "GB_s": round(n * 4 / (ms * 1e-3) / 1e9, 1),
+                         "frac_of_peak": round(n * 4 / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes_read": n * 4,
+                         "kernel": "torch.sum (a reduction: reads once)"}
+    del bufs
+    torch.cuda.synchronize()
+    return out
 
 
 def load_traffic() -> dict | None:
@@ -340,6 +371,7 @@ def c4_leg(n_prompt: int, cycles: int, serial: bool = True) -> dict:
         return {"prompt_tokens": n_prompt, "cycles": int(st.cycles), "tokens": int(len(spec)),
                 "ms_per_cycle": round(st.decode_s / st.cycles * 1e3, 3), "prefill_s": round(st.prefill_s, 3)}
     serial, st2 = m.generate_serial(prompt, len(spec), with_stats=True)
+    rollback = c4_rollback(m, prompt, serial, cycles)
     m.free()
     mean_ctx = n_prompt + len(spec) / 2
     gbs = c4_step_bytes(mean_ctx) * st.cycles / st.decode_s / 1e9
@@ -354,8 +386,48 @@ def c4_leg(n_prompt: int, cycles: int, serial: bool = True) -> dict:
             "GB_s_per_cycle": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
             "prefill_s": round(st.prefill_s, 3),
             "spec_equals_serial": bool(np.array_equal(spec, serial)),
+            "rollback_cycles": rollback,
             "note": "random-init weights; greedy output of such a model is highly repetitive, "
                     "so n-gram drafts are accepted far more often than on a trained model"}
+
+
+def c4_rollback(m, prompt, serial, cycles: int, p_bad: float = 0.4) -> dict:
+    """Verify cycles with rejected drafts: after the same prefill, each cycle
+    drafts the next 7 tokens of the serial decode's stream, each replaced
+    w.p. p_bad by another token (c2's rule), and verifies them
+    (cwen_model_verify: forward_block + walk + rollback, run.c:4946-4988).
+    A walk that stops at draft j keeps drafts 0..j-1 and the bonus; the next
+    block replays that accepted prefix of the recurrent state before its own
+    positions.  Checked: every cycle's k is the first replaced draft's
+    index, and the emitted tokens equal the serial stream."""
+    import time as _t
+    V = C4_CFG["vocab"]
+    rng = np.random.default_rng(11)
+    m.reset()
+    for b0 in range(0, len(prompt) - 1, 16):
+        m.forward(prompt[b0:min(len(prompt) - 1, b0 + 16)], want_argmax=False)
+    pend, i, ks, emitted, ok = int(prompt[-1]), 0, [], [], True
+    t0 = _t.perf_counter()
+    while len(ks) < cycles and i + 8 <= len(serial):
+        drafts = np.array(serial[i:i + 7], dtype=np.int64)
+        bad = rng.random(7) < p_bad
+        for j in np.flatnonzero(bad):
+            drafts[j] = (drafts[j] + 1 + rng.integers(0, V - 1)) % V     # any other token
+        k, bonus = m.verify(np.concatenate([[pend], drafts]).astype(np.int32))
+        want_k = int(np.argmax(bad)) if bad.any() else 7
+        ok &= k == want_k and bonus == int(serial[i + k])
+        emitted.extend(list(drafts[:k]) + [bonus])
+        ks.append(k)
+        i += k + 1
+        pend = bonus
+    dt = _t.perf_counter() - t0
+    ks = np.array(ks)
+    return {"cycles": int(len(ks)), "ms_per_cycle": round(dt / len(ks) * 1e3, 3),
+            "tok_s": round(len(emitted) / dt, 1), "mean_k": round(float(ks.mean()), 3),
+            "share_replaying_a_prefix": round(float(np.mean(ks < 7)), 3),
+            "k_and_bonus_as_drafted": bool(ok),
+            "emitted_equals_serial": bool(np.array_equal(np.array(emitted), np.asarray(serial[:len(emitted)]))),
+            "draft_replacement_p": p_bad}
 
 
 def mtp_leg(n_prompt: int, n_gen: int) -> dict:
@@ -593,7 +665,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--Bs", default="8,1,16",
+    ap.add_argument("--Bs", default="8,1,4,16",
                     help="comma-separated block sizes; the first is the headline (must include 8)")
     ap.add_argument("--no-extra", action="store_true", help="skip the c0/c2/c3 kernel measurements")
     ap.add_argument("--no-c4", action="store_true", help="skip the full-model speculative decode")
@@ -624,6 +696,8 @@ def main() -> int:
 
     if args.calibrate_copy:
         calibrate_copy()
+    ceiling = hbm_ceiling()
+    done("HBM ceiling")
     res = gpu_leg(args.steps, args.warmup, Bs)
     done("FFN leg")
     extra = None if args.no_extra else extra_leg(args.steps, args.warmup)
@@ -664,7 +738,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4_0 weights, f16 MFMA operands, f32 accumulate",
-        "data": "synthetic (seeded Q4_0 weights, N(0,1) activations), 4 weight copies rotated",
+        "data": f"synthetic (seeded Q4_0 weights, N(0,1) activations), {NCOPIES} weight copies rotated",
         "config": {
             "workload": "FFN block verify: gate/up 17408x5120 Q4_0 RSI + SwiGLU, down 5120x17408 Q4_0 RS",
             "B": 8, "d_model": H, "ffn": I, "weight_copies": NCOPIES,
@@ -688,6 +762,7 @@ def main() -> int:
             "traffic_source": None if traffic is None else traffic["source"],
             "algorithmic_bytes": b1,
         },
+        "hbm_ceiling": ceiling,
         "cpu_baseline": cpu_base,
         "other_configs": extra,
         "c4_full_model_spec_b8": c4,
