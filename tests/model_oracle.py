@@ -8,6 +8,25 @@ import numpy as np
 T_F32, T_Q4_0RS, T_Q4_0RSI, T_Q6_K = 0, 101, 102, 14
 
 
+def np_attention(Kg: np.ndarray, Vg: np.ndarray, t0: int, pos: int, q: np.ndarray, gate: np.ndarray) -> np.ndarray:
+    """The oracle's gated attention (orc_attention, after run.c:2362-2409):
+    per query head h of KV group h // (nh / nkv), softmax over keys t0..pos of
+    (q . k) / sqrt(hd), the weighted sum of the values, times sigmoid(gate),
+    in f32 with BLAS products.  Kg, Vg are group-major [nkv][t][hd]."""
+    nkv, hd = Kg.shape[0], Kg.shape[2]
+    nh = q.shape[0]
+    kvm = nh // nkv
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    out = np.empty((nh, hd), np.float32)
+    for g in range(nkv):
+        s = (q[g * kvm:(g + 1) * kvm].astype(np.float32) @ Kg[g, t0:pos + 1].T) * scale
+        e = np.exp(s - s.max(axis=1, keepdims=True))
+        e /= e.sum(axis=1, keepdims=True)
+        out[g * kvm:(g + 1) * kvm] = e @ Vg[g, t0:pos + 1]
+    g32 = np.asarray(gate, np.float32)
+    return (out * (np.float32(1.0) / (np.float32(1.0) + np.exp(-g32)))).astype(np.float32)
+
+
 class OracleModel:
     """f16_inputs: round every GEMV input to f16 first, used by the tests to
     measure how sensitive a position's logits are to that rounding.
@@ -19,10 +38,14 @@ class OracleModel:
     C restatement, as in the other modes.  The device's logits differ from
     this mode only by the order of its f32 sums."""
 
-    def __init__(self, O, cfg: dict, tensors, f16_inputs: bool = False, device: bool = False):
+    def __init__(self, O, cfg: dict, tensors, f16_inputs: bool = False, device: bool = False,
+                 fast_attention: bool = False):
         self.O, self.c = O, cfg
         self.f16_inputs = f16_inputs
         self.device = device
+        # fast_attention: np_attention (BLAS, f32) instead of the C restatement
+        # of the attention, for contexts of tens of thousands of positions.
+        self.fast_attention = fast_attention
         self.w16 = {}
         self.g = {}
         self.t = {}
@@ -50,6 +73,10 @@ class OracleModel:
         NL = c["n_layers"]
         self.K[NL] = np.zeros((c["max_ctx"], c["n_kv_head"], c["head_dim"]), np.float32)
         self.V[NL] = np.zeros_like(self.K[NL])
+        # group-major copies [n_kv_head][max_ctx][head_dim] for np_attention
+        self.Kg = {l: np.zeros((c["n_kv_head"], c["max_ctx"], c["head_dim"]), np.float32)
+                   for l in self.K} if self.fast_attention else {}
+        self.Vg = {l: np.zeros_like(a) for l, a in self.Kg.items()}
         self.hprev, self.hpos = None, -1
 
     def _w16(self, layer, tid, side):
@@ -145,7 +172,11 @@ class OracleModel:
         q = O.rope(q, pos, c["n_rot_pairs"], c["n_rot"], c["rope_theta"])
         k = O.rope(k, pos, c["n_rot_pairs"], c["n_rot"], c["rope_theta"])
         self.K[l][pos], self.V[l][pos] = k, v
-        att = O.attention(self.K[l][:pos + 1], self.V[l][:pos + 1], t0, pos, q, gate)
+        if self.fast_attention:
+            self.Kg[l][:, pos], self.Vg[l][:, pos] = k, v
+            att = np_attention(self.Kg[l], self.Vg[l], t0, pos, q, gate)
+        else:
+            att = O.attention(self.K[l][:pos + 1], self.V[l][:pos + 1], t0, pos, q, gate)
         return (x + self.mv(l, G.ATTN_OUTPUT, att.reshape(-1))).astype(np.float32)
 
     def mlp(self, l, x):

@@ -104,3 +104,35 @@ def test_device_mode_is_an_f16_scale_perturbation(oracle):
     for p in range(len(toks)):
         spread = rel_err(ref16[p], ref[p])
         assert 0 < rel_err(dev[p], ref[p]) <= 4 * spread + 1e-4, (p, rel_err(dev[p], ref[p]), spread)
+
+
+def test_np_attention_equals_the_c_restatement(oracle):
+    """np_attention (tests/model_oracle.py, for the long-context fixtures) vs
+    orc_attention at the 27B shape's 24 / 4 heads of 256, with and without a
+    first slot t0 > 0: within 2e-6 (f32 sums in another order)."""
+    from model_oracle import np_attention
+    g = np.random.default_rng(3)
+    T, nkv, nh, hd = 300, 4, 24, 256
+    K = g.standard_normal((T, nkv, hd)).astype(np.float32)
+    V = g.standard_normal((T, nkv, hd)).astype(np.float32)
+    Kg, Vg = np.ascontiguousarray(K.transpose(1, 0, 2)), np.ascontiguousarray(V.transpose(1, 0, 2))
+    for t0, pos in ((0, 0), (0, 37), (0, 299), (1, 150)):
+        q = (0.3 * g.standard_normal((nh, hd))).astype(np.float32)
+        gate = g.standard_normal((nh, hd)).astype(np.float32)
+        want = oracle.attention(K[:pos + 1], V[:pos + 1], t0, pos, q, gate)
+        got = np_attention(Kg, Vg, t0, pos, q, gate)
+        assert rel_err(got, want) <= 2e-6, (t0, pos, rel_err(got, want))
+
+
+def test_fast_attention_model_equals_the_c_attention_model(oracle):
+    """The oracle's forward with np_attention equals it with the C attention
+    within 1e-5 over 40 positions (with the nextn stream), in the plain mode:
+    with f16 roundings downstream, attention differences of 1e-6 flip a few
+    of them and move the logits by ~1e-4 (the sensitivity the model tests
+    measure)."""
+    tensors = list(synth.model_tensors(CFG, seed=8, mtp=True))
+    toks = synth.prompt_tokens(8, 40, CFG["vocab"])
+    ref, ref_d = _logits(oracle, tensors, toks)
+    fast, fast_d = _logits(oracle, tensors, toks, fast_attention=True)
+    errs = [rel_err(fast[p], ref[p]) for p in range(len(toks))] + [rel_err(fast_d[t], ref_d[t]) for t in range(2)]
+    assert max(errs) <= 1e-5, max(errs)
