@@ -17,12 +17,14 @@ chunks, landing the next while it computes the current one).
     (c4_geometry_wide_logits.npz): past 6144 positions the chunk kernel
     switches from 64 double-buffered workgroups per KV head to 128
     single-buffered ones, so the prefill crosses the switch and the
-    compared blocks run the wide grid.  Tolerance (stated): rel_err <= 2e-3
-    per position, rel_err = max|d| / max|ref| over the vocab.  The device
-    rounds every GEMV input to f16 (MFMA operands); the fixture's f16-input
-    oracle shows that this rounding alone moves the oracle's own logits by
-    up to 1.1e-3 at these positions (measured on the device: 1.0e-3).  Every
-    row's argmax is also checked bit-exact against the device's own logits.
+    compared blocks run the wide grid.  The reference is the oracle's
+    device-rounding mode (tests/device_round.py: f16 weights and operands
+    where the device rounds them, float64 sums).  Tolerance (stated), as in
+    tests/test_model_gpu.py: per position, rel_err <= 1e-4 + 2 * jit, jit
+    = how far the mode's own logits move when each f16 operand is perturbed
+    by 1e-6 * max|x| first (the fixture's "jit"); rel_err = max|d| /
+    max|ref| over the vocab.  Every row's argmax is also checked bit-exact
+    against the device's own logits.
   * block == single positions bit for bit at the same geometry and context.
   * test_27b_shape_spec_equals_serial (slow): the full 64-layer 27B shape
     (device-generated random-init weights), max_ctx 8192, a 4160-token
@@ -42,7 +44,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "c4_geometry_logits.npz"
 GOLDEN_WIDE = GOLDEN.with_name("c4_geometry_wide_logits.npz")
-TOL = 2e-3
+TOL_DEV, JIT_FACTOR = 1e-4, 2.0     # as in tests/test_model_gpu.py
 
 
 def _golden_cfg():
@@ -75,8 +77,7 @@ def _prefill(m, toks, n, B=16):
     assert m.pos == n - 1
 
 
-@pytest.mark.parametrize("golden", [GOLDEN, GOLDEN_WIDE], ids=["narrow", "wide"])
-def test_c4_geometry_vs_oracle(env, oracle, golden):
+def _vs_oracle(env, oracle, golden):
     gpu, ctx, m, g = env
     fx = np.load(golden)
     n_ctx, n_cmp = int(fx["n_ctx"]), int(fx["n_cmp"])
@@ -93,12 +94,15 @@ def test_c4_geometry_vs_oracle(env, oracle, golden):
         got.extend(list(lg))
         b0 += B
     got = np.stack(got)
-    ref, ref16 = fx["ref"], fx["ref16"]
+    ref, jit = fx["refdev"], fx["jit"]
     errs = [rel_err(got[i], ref[i]) for i in range(n_cmp)]
-    spread = [rel_err(ref16[i], ref[i]) for i in range(n_cmp)]
-    print(f"c4 geometry: max rel_err {max(errs):.3e} (oracle f16-input spread {max(spread):.3e})", flush=True)
+    tol = TOL_DEV + JIT_FACTOR * jit
+    worst = max(range(n_cmp), key=lambda i: errs[i] / tol[i])
+    print(f"c4 geometry: max rel_err vs the device-rounding oracle {max(errs):.3e}; worst err / tol "
+          f"{errs[worst] / tol[worst]:.2f} at position {p0 + worst} (tol {tol[worst]:.2e}); vs the plain oracle "
+          f"{max(rel_err(got[i], fx['ref'][i]) for i in range(n_cmp)):.3e}", flush=True)
     for i in range(n_cmp):
-        assert errs[i] <= TOL, (p0 + i, errs[i], spread[i])
+        assert errs[i] <= tol[i], (p0 + i, errs[i], tol[i])
 
 
 @pytest.mark.parametrize("B", [16, 8])
