@@ -77,6 +77,11 @@ def _prefill(m, toks, n, B=16):
     assert m.pos == n - 1
 
 
+@pytest.mark.parametrize("golden", [GOLDEN, GOLDEN_WIDE], ids=["narrow", "wide"])
+def test_c4_geometry_vs_oracle(env, oracle, golden):
+    _vs_oracle(env, oracle, golden)
+
+
 def _vs_oracle(env, oracle, golden):
     gpu, ctx, m, g = env
     fx = np.load(golden)
