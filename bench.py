@@ -108,7 +108,64 @@ def hbm_ceiling(reps: int = 20) -> dict:
                          "frac_of_peak": round(n * 4 / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes_read": n * 4,
                          "kernel": "torch.sum (a reduction: reads once)"}
     del bufs
+    out.update(read_probes(reps, stream))
     torch.cuda.synchronize()
+    return out
+
+
+# The gate/up launch's grid at the 27B FFN shape on 256 CUs: 2176 weight
+# streams (1088 row groups x gate/up) of 10 rounds; 512 whole 4-stream tiles,
+# and the 32 remainder tiles split into 5 pieces of 2 rounds, dispatched first.
+GU_GRID = {"nstream": 2176, "rounds": 10, "nwhole": 512, "npieces": 160, "prs": 2}
+
+
+def read_probes(reps: int, stream) -> dict:
+    """Read-only streams with no arithmetic (cwen_amd/probe/stream_probe.hip):
+    a plain read of 88 MiB, and the gate/up GEMV's own weight stream (its grid,
+    super-tile layout, per-wave loads and activation staging loads) without
+    the dequant, LDS staging, MFMA and epilogue.  The second is the rate the
+    GEMV's load structure allows; the GEMV's own rate beside it shows what its
+    arithmetic costs."""
+    import ctypes
+    import torch
+    lib_path = ROOT / "cwen_amd" / "libcwen_probe.so"
+    if not lib_path.exists():
+        return {"read_probes": None, "read_probes_note": f"{lib_path.name} not built"}
+    lib = ctypes.CDLL(str(lib_path))
+    vp, sz, ci = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+    lib.cwen_probe_gemv_grid.argtypes = [vp, sz, vp, sz, vp, ci, ci, ci, ci, ci, ci, vp]
+    lib.cwen_probe_read.argtypes = [vp, sz, vp, ci, ctypes.POINTER(sz), vp]
+    st = ctypes.c_void_p(stream.cuda_stream)
+    g = GU_GRID
+    wbytes = g["nstream"] * g["rounds"] * 4608
+    bufs = [torch.ones(wbytes // 4, dtype=torch.float32, device="cuda") for _ in range(6)]
+    xb = torch.ones(g["rounds"] * 8192 // 4, dtype=torch.float32, device="cuda")
+    sink = torch.zeros(16, dtype=torch.int32, device="cuda")
+    out = {}
+
+    def grid_launch(i):
+        rc = lib.cwen_probe_gemv_grid(bufs[i % 6].data_ptr(), wbytes, xb.data_ptr(), xb.numel() * 4, sink.data_ptr(),
+                                      g["nstream"], g["rounds"], g["nwhole"], g["npieces"], g["prs"], 2, st)
+        if rc:
+            raise RuntimeError("cwen_probe_gemv_grid refused its arguments")
+    ms = time_launches(grid_launch, reps, 3, stream)
+    out["read_gemv_grid_100MB"] = {
+        "ms": round(ms, 5), "GB_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+        "frac_of_peak": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes_read": wbytes,
+        "kernel": "gemv_grid_probe<2>: the gate/up GEMV's weight stream and staging loads, no arithmetic",
+        "grid": dict(g)}
+    nread = sz(0)
+    iters = wbytes // (512 * 4 * 4096)   # whole steps of the grid that fit the buffer
+
+    def read_launch(i):
+        if lib.cwen_probe_read(bufs[i % 6].data_ptr(), wbytes, sink.data_ptr(), iters, ctypes.byref(nread), st):
+            raise RuntimeError("cwen_probe_read refused its arguments")
+    ms = time_launches(read_launch, reps, 3, stream)
+    out["read_linear"] = {
+        "ms": round(ms, 5), "GB_s": round(nread.value / (ms * 1e-3) / 1e9, 1),
+        "frac_of_peak": round(nread.value / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes_read": nread.value,
+        "kernel": "read_probe: 512 workgroups x 4 waves, 4 KB per wave per step, non-temporal"}
+    del bufs
     return out
 
 

@@ -1,8 +1,11 @@
 """Build recipe for the native parts of cwen_amd (in-tree, no JIT cache).
 
-    python -m cwen_amd.build          # libcwen_gpu.so (HIP, gfx950)
+    python -m cwen_amd.build          # libcwen_gpu.so (HIP, gfx950) and the rest
 
-Produces cwen_amd/libcwen_gpu.so from cwen_amd/csrc/*.hip with hipcc.
+Produces cwen_amd/libcwen_gpu.so from cwen_amd/csrc/*.hip with hipcc, the host
+library and CLI from cwen_amd/host, and cwen_amd/libcwen_probe.so (bench.py's
+read-stream probes, cwen_amd/probe) -- a measurement aid, not part of the
+product library.
 """
 from __future__ import annotations
 
@@ -76,6 +79,19 @@ def build_host(verbose: bool = False) -> Path:
     return HOST_LIB
 
 
+PROBE_LIB = PKG / "libcwen_probe.so"
+
+
+def build_probe(verbose: bool = False) -> Path:
+    """The read-stream probes bench.py times for its HBM-ceiling leg."""
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, *HIP_FLAGS, "-shared", str(PKG / "probe" / "stream_probe.hip"), "-o", str(tmp)])
+    os.replace(tmp, PROBE_LIB)
+    if verbose:
+        print(f"built {PROBE_LIB}")
+    return PROBE_LIB
+
+
 CLI = PKG / "cwen_run"
 
 
@@ -106,5 +122,6 @@ if __name__ == "__main__":
     build_gpu(verbose=True)
     build_host(verbose=True)
     build_cli(verbose=True)
+    build_probe(verbose=True)
     if "--oracle" in sys.argv:
         build_oracle(verbose=True)
