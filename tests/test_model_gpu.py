@@ -7,9 +7,13 @@ Checked:
     (tests/model_oracle.py) in its device-rounding mode: every weight and
     GEMV operand rounded to f16 where the device rounds it
     (tests/device_round.py), sums in float64.  Tolerance (stated), per
-    position: rel_err(device, oracle_device) <= 1e-4, rel_err = max|d| /
-    max|ref| over the vocab.  What is left between the two is the order of
-    the device's f32 sums.  The device-rounding mode itself is pinned to the
+    position: rel_err(device, oracle_device) <= 1e-4 + 2 * jit, rel_err =
+    max|d| / max|ref| over the vocab, jit = how far the mode's own logits at
+    that position move when each f16 operand is perturbed by 1e-6 * max|x|
+    before its rounding (the larger of two seeded trials).  What is left
+    between device and mode is the order of the device's f32 sums, which
+    an f16 rounding downstream can amplify by a flip; jit measures that
+    amplification per position.  The device-rounding mode itself is pinned to the
     plain oracle on the CPU (tests/test_device_round.py); f16 rounding moves
     this random-init model's logits by up to ~1e-2 at ill-conditioned
     positions, so a bound against the plain oracle would have to be that
