@@ -349,16 +349,20 @@ class ModelCfg(C.Structure):
 class SpecCfg(C.Structure):
     _fields_ = [("n_key", C.c_int), ("max_draft", C.c_int), ("min_draft", C.c_int), ("cooldown", C.c_int),
                 ("max_cycles", C.c_int), ("mtp", C.c_int), ("ngmap", C.c_void_p), ("cycle_log", C.c_void_p),
-                ("cycle_log_cap", C.c_int), ("debug", C.c_int)]
+                ("cycle_log_cap", C.c_int), ("debug", C.c_int), ("fa_streak", C.c_void_p)]
 
 
 def spec_cfg(n_key: int = 16, max_draft: int = 8, min_draft: int = 2, cooldown: int = 8, max_cycles: int = 0,
              mtp: int = 1, ngmap: "NgMap | None" = None, cycle_log: np.ndarray | None = None,
-             debug: int = 0) -> SpecCfg:
-    """A speculation config; cycle_log (int32, even length) receives (E, k) per cycle."""
+             debug: int = 0, fa_streak: np.ndarray | None = None) -> SpecCfg:
+    """A speculation config; cycle_log (int32, even length) receives (E, k) per cycle;
+    fa_streak (one int32) carries the full-accept streak from call to call."""
+    if fa_streak is not None and (fa_streak.dtype != np.int32 or fa_streak.size < 1):
+        raise ValueError("fa_streak must be an int32 array of at least one element")
     return SpecCfg(n_key, max_draft, min_draft, cooldown, max_cycles, mtp, None if ngmap is None else ngmap.h,
                    None if cycle_log is None else cycle_log.ctypes.data,
-                   0 if cycle_log is None else cycle_log.size // 2, debug)
+                   0 if cycle_log is None else cycle_log.size // 2, debug,
+                   None if fa_streak is None else fa_streak.ctypes.data)
 
 
 class NgMap:

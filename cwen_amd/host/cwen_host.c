@@ -26,6 +26,7 @@ void cwen_spec_default(cwen_spec_cfg *cfg) {
   cfg->cycle_log = NULL;
   cfg->cycle_log_cap = 0;
   cfg->debug = 0;
+  cfg->fa_streak = NULL;
 }
 
 /* run.c:4533-4549 */
@@ -120,7 +121,8 @@ static int spec_loop(const spec_model *M, const int *prompt, int n_prompt, int n
   st.prefill_s = t1 - t0;
   memcpy(hist, prompt, sizeof(int) * (size_t)n_prompt);
   const int cap = M->capacity(M->ud);
-  int hn = n_prompt, g = 0, streak = 0, cool = 0, fa_streak = 0, upd = 0;
+  int hn = n_prompt, g = 0, streak = 0, cool = 0, upd = 0;
+  int fa_streak = cfg.fa_streak ? *cfg.fa_streak : 0;
   if (n_gen > 0 && M->pos(M->ud) + 1 < cap) {
     hist[hn++] = pend;
     out[g++] = pend;
@@ -188,6 +190,7 @@ static int spec_loop(const spec_model *M, const int *prompt, int n_prompt, int n
     else if (++streak >= 3) { streak = 0; cool = cfg.cooldown; }
   }
   st.decode_s = now_s() - t1;
+  if (cfg.fa_streak) *cfg.fa_streak = fa_streak;
   free(hist);
   if (cfg.debug)
     fprintf(stderr, "spec: %lld passes, %lld with drafts (%lld kept whole, %lld cut short), %.2f drafts kept on "

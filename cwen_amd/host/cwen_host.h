@@ -75,6 +75,11 @@ typedef struct {
                       draft count E at [2c] and kept drafts k at [2c + 1] */
   int cycle_log_cap;
   int debug;       /* one line per cycle on stderr (run.c CWEN_SPEC_DEBUG) */
+  int *fa_streak;  /* full-accept streak carried from call to call, as the
+                      reference's function-static one is (run.c:4967): when
+                      non-NULL a call starts from *fa_streak and leaves its
+                      final value there; NULL starts every call at 0.
+                      cwen_serve carries one across its requests. */
 } cwen_spec_cfg;
 
 typedef struct {

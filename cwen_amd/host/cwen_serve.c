@@ -94,6 +94,14 @@ int cwen_serve(cwen_model *m, const cwen_model_cfg *cfg, int fd_in, int fd_out, 
   FILE *in = open_dup(fd_in, "rb"), *wr = open_dup(fd_out, "wb");
   int rc = (!tokens || !out) ? CWEN_ENOMEM : (!in || !wr) ? CWEN_EINVAL : CWEN_OK;
   int served = 0;
+  /* the full-accept streak lives across requests, as run.c's function-static
+   * one does (run.c:4967), unless the caller carries its own */
+  cwen_spec_cfg sc;
+  int fa_carry = 0;
+  if (spec) {
+    sc = *spec;
+    if (!sc.fa_streak) sc.fa_streak = &fa_carry;
+  }
   while (!rc) {
     uint32_t np = 0, ng = 0;
     const int r = read_frame(in, tokens, cfg->max_ctx, cfg->vocab, &np, &ng);
@@ -102,7 +110,7 @@ int cwen_serve(cwen_model *m, const cwen_model_cfg *cfg, int fd_in, int fd_out, 
       rc = put_reply(wr, NULL, 0);
       continue;
     }
-    const int n = spec ? cwen_generate_spec(m, tokens, (int)np, (int)ng, spec, out, NULL)
+    const int n = spec ? cwen_generate_spec(m, tokens, (int)np, (int)ng, &sc, out, NULL)
                        : cwen_generate_serial(m, tokens, (int)np, (int)ng, out, NULL);
     if (n < 0) {
       rc = n;

@@ -24,10 +24,10 @@ from spec_oracle import ReferenceDriver, repetitive_stream  # noqa: E402
 STAT_KEYS = ("cycles", "drafted", "full", "rejected", "kept")
 
 
-def _ours(stream, n_prompt, n_gen, max_ctx, n_key, max_draft, min_draft, cooldown, ngmap):
+def _ours(stream, n_prompt, n_gen, max_ctx, n_key, max_draft, min_draft, cooldown, ngmap, fa_streak=None):
     from cwen_amd import gpu
     log = np.full(2 * 4096, -1, np.int32)
-    cfg = gpu.spec_cfg(n_key, max_draft, min_draft, cooldown, 0, 0, ngmap, log)
+    cfg = gpu.spec_cfg(n_key, max_draft, min_draft, cooldown, 0, 0, ngmap, log, fa_streak=fa_streak)
     out, st = gpu.spec_replay(stream, n_prompt, n_gen, max_ctx, cfg)
     n = st.cycles
     return out, [tuple(x) for x in log[:2 * n].reshape(-1, 2).tolist()], {k: getattr(st, k) for k in STAT_KEYS}
@@ -81,24 +81,49 @@ def test_output_is_the_stream():
 
 def test_map_across_requests_equals_reference(ref):
     """One map serving three requests in turn, as the reference's server keeps
-    NGM across frames: each request's cycles equal the reference's.  (The
-    reference also keeps its full-accept streak across requests in a
-    function-static variable; this driver starts each request at zero, so
-    the restatement's streak is reset between requests here.)"""
+    NGM across frames, and the full-accept streak carried from request to
+    request, as the reference's function-static one is (run.c:4967): each
+    request's cycles equal the reference's."""
     from cwen_amd import gpu
     n_key = 4
     D = ReferenceDriver(ref, n_key)
     M = gpu.NgMap(n_key, 248320)
+    carry = np.zeros(1, np.int32)
+    carried = []
     for r in range(3):
         # one seed: the requests share phrases, so the map's earlier entries matter
         n_prompt = 150 + 20 * r
         stream = repetitive_stream(30, n_prompt, 250)
-        D.fa_streak = 0
         want_out, want_log, want_st = D.run(stream, n_prompt, 250, 4096)
-        got_out, got_log, got_st = _ours(stream, n_prompt, 250, 4096, n_key, 8, 2, 8, M)
+        got_out, got_log, got_st = _ours(stream, n_prompt, 250, 4096, n_key, 8, 2, 8, M, carry)
         assert got_log == want_log and got_st == want_st
         assert np.array_equal(got_out, want_out)
+        assert int(carry[0]) == D.fa_streak
+        carried.append(int(carry[0]))
     assert M.used() == ref.ng_used()
+    assert any(carried), "no request ended inside a full-accept streak: the carry was not exercised"
+
+
+def test_carried_streak_equals_reference(ref):
+    """A request started from a carried full-accept streak (0, 3 or 7) ends
+    with the same streak as the restatement started the same way, with the
+    same cycles.  Every request starts with E_cap at its cap, and the first
+    short walk resets the streak, so the streak a request starts from changes
+    none of its drafts: the three logs are equal."""
+    from cwen_amd import gpu  # noqa: F401
+    stream = repetitive_stream(7, 120, 200)
+    logs = []
+    for start in (0, 3, 7):
+        D = ReferenceDriver(ref, 4, use_map=False)
+        D.fa_streak = start
+        want_out, want_log, want_st = D.run(stream, 120, 200, 4096)
+        carry = np.array([start], np.int32)
+        got_out, got_log, got_st = _ours(stream, 120, 200, 4096, 4, 8, 2, 8, None, carry)
+        assert got_log == want_log and got_st == want_st
+        assert np.array_equal(got_out, want_out)
+        assert int(carry[0]) == D.fa_streak
+        logs.append(got_log)
+    assert logs[0] == logs[1] == logs[2]
 
 
 def test_replay_rejects_a_stream_too_short():
