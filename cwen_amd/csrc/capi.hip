@@ -128,7 +128,7 @@ int cwen_ctx_create(int device, cwen_ctx **out) {
   cwen_ctx *c = (cwen_ctx *)calloc(1, sizeof(cwen_ctx));
   if (!c) return CWEN_ENOMEM;
   c->device = device;
-  c->wg_per_cu = env_int("CWEN_GEMV_WG_PER_CU", 2, 1, 16);
+  c->wg_per_cu = env_int("CWEN_GEMV_WG_PER_CU", 1, 1, 16);
   if (hipDeviceGetAttribute(&c->ncu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c->ncu < 1) {
     free(c);
     return CWEN_EHIP;

@@ -1220,7 +1220,9 @@ double grid_cost(int ncu, int nst, const GemvGrid &c, double extra) {
 // (chosen by grid_cost) that spread them over the CUs: without that, the
 // CUs that get one whole tile more than the others would set the launch's
 // length.
-GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
+// split_basis: the tile count that sizes the split (the single-side one for
+// both launch kinds, so a pair launch splits K as its single sides do).
+GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst, int split_basis) {
   GemvGrid best = {ntile, 0, 1, nst, 0};
   // More than half as many tiles as CUs: whole tiles, one per CU.  Split in
   // two, most CUs would get two pieces of the same total length plus the
@@ -1229,9 +1231,10 @@ GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
   if (ntile < ctx->ncu && 2 * ntile > ctx->ncu) return best;
   if (ntile < ctx->ncu) {
     const int target = ctx->wg_per_cu * ctx->ncu;
-    // At most wg_per_cu workgroups per CU: one more on some CUs than on the
-    // others would set the launch's length.
-    int S = std::min(std::max(target / ntile, 1), std::max(nst / 2, 1));
+    // At most wg_per_cu workgroups per CU for a single-side launch (one more
+    // on some CUs than on the others would set the launch's length); a pair
+    // launch, twice the tiles, takes the same pieces.
+    int S = std::min(std::max(target / split_basis, 1), std::max(nst / 2, 1));
     const int rps = (nst + S - 1) / S;
     S = (nst + rps - 1) / rps;
     const GemvGrid cand = {ntile * S, ntile * S, S, rps, 0};
@@ -1260,9 +1263,10 @@ GemvGrid choose_grid(const cwen_ctx *ctx, int ntile, int nst) {
 // an interleaved pair computed whole puts its two sides on a wave pair.
 void gemv_choose_split(const cwen_ctx *ctx, cwen_weight *w) {
   w->rows = 1;
+  const int single = (w->nrg + tile_rows(1) - 1) / tile_rows(1);
   for (int ns = 1; ns <= w->nside; ++ns) {
     const int rpw = tile_rows(ns);
-    w->cfg[ns - 1] = choose_grid(ctx, (w->nrg + rpw - 1) / rpw, w->nst);
+    w->cfg[ns - 1] = choose_grid(ctx, (w->nrg + rpw - 1) / rpw, w->nst, single);
   }
 }
 
