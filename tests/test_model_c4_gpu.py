@@ -25,7 +25,15 @@ chunks, landing the next while it computes the current one).
     by 1e-6 * max|x| first (the fixture's "jit"); rel_err = max|d| /
     max|ref| over the vocab.  Every row's argmax is also checked bit-exact
     against the device's own logits.
-  * block == single positions bit for bit at the same geometry and context.
+  * test_c4_geometry_long_context_vs_oracle: the same model in a 32768-slot
+    cache (run.c:85 MAX_SEQ, the interface's maximum) prefilled to 16416
+    positions, then the same three blocks, against
+    c4_geometry_16k_logits.npz (make_c4_geometry_golden.py --long 16k):
+    514 key chunks, so the chunk kernel runs its wide grid several chunks
+    per workgroup and each of the merge's four groups sums 128-129 chunk
+    partials.  Same bound.
+  * block == single positions bit for bit at the same geometry and context,
+    and near the end of the 32768-slot cache.
   * test_27b_shape_spec_equals_serial (slow): the full 64-layer 27B shape
     (device-generated random-init weights), max_ctx 8192, a 4160-token
     prompt: a block equals its single positions bit for bit, verify blocks
@@ -77,9 +85,51 @@ def _prefill(m, toks, n, B=16):
     assert m.pos == n - 1
 
 
+@pytest.fixture(scope="module")
+def env_long():
+    """The same model in a 32768-slot cache (the interface's maximum,
+    run.c:85 MAX_SEQ)."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from cwen_amd import gpu
+    g = _golden_cfg()
+    ctx = gpu.Context(0)
+    m = gpu.Model(ctx, **g.LONG_CFG)
+    for t in synth.model_tensors(g.LONG_CFG, seed=g.SEED):
+        m.set(*t)
+    yield gpu, ctx, m, g
+    m.free()
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("golden", [GOLDEN, GOLDEN_WIDE], ids=["narrow", "wide"])
 def test_c4_geometry_vs_oracle(env, oracle, golden):
     _vs_oracle(env, oracle, golden)
+
+
+@pytest.mark.parametrize("which", ["16k"])
+def test_c4_geometry_long_context_vs_oracle(env_long, oracle, which):
+    """16448 positions in a 32768-slot cache: 514 key chunks, so each of the
+    merge's four groups sums 128 or 129 chunk partials.  Same comparison and
+    tolerance as above, against c4_geometry_16k_logits.npz."""
+    _vs_oracle(env_long, oracle, GOLDEN.with_name(f"c4_geometry_{which}_logits.npz"))
+
+
+@pytest.mark.parametrize("B", [16, 8])
+def test_c4_geometry_long_context_block_equals_singles(env_long, B):
+    """A block equals its single positions bit for bit near the end of the
+    32768-slot cache."""
+    gpu, ctx, m, g = env_long
+    p0 = 32736 - B
+    toks = g.tokens(32736)
+    _prefill(m, toks, p0)
+    m.forward(toks[p0:p0 + B])
+    block = m.logits(B).copy()
+    _prefill(m, toks, p0)
+    for b in range(B):
+        m.forward(toks[p0 + b:p0 + b + 1])
+        assert np.array_equal(m.logits(1)[0].view(np.uint32), block[b].view(np.uint32)), b
 
 
 def _vs_oracle(env, oracle, golden):
