@@ -26,12 +26,12 @@ chunks, landing the next while it computes the current one).
     max|ref| over the vocab.  Every row's argmax is also checked bit-exact
     against the device's own logits.
   * test_c4_geometry_long_context_vs_oracle: the same model in a 32768-slot
-    cache (run.c:85 MAX_SEQ, the interface's maximum) prefilled to 16416
-    positions, then the same three blocks, against
-    c4_geometry_16k_logits.npz (make_c4_geometry_golden.py --long 16k):
-    514 key chunks, so the chunk kernel runs its wide grid several chunks
-    per workgroup and each of the merge's four groups sums 128-129 chunk
-    partials.  Same bound.
+    cache (run.c:85 MAX_SEQ, the interface's maximum) prefilled to 16416 and
+    32704 positions, then the same three blocks, against
+    c4_geometry_{16k,32k}_logits.npz (make_c4_geometry_golden.py --long):
+    514 and 1023 key chunks, so the chunk kernel runs its wide grid several
+    chunks per workgroup and each of the merge's four groups sums 128-129
+    and 255-256 chunk partials.  Same bound.
   * block == single positions bit for bit at the same geometry and context,
     and near the end of the 32768-slot cache.
   * test_27b_shape_spec_equals_serial (slow): the full 64-layer 27B shape
@@ -108,11 +108,12 @@ def test_c4_geometry_vs_oracle(env, oracle, golden):
     _vs_oracle(env, oracle, golden)
 
 
-@pytest.mark.parametrize("which", ["16k"])
+@pytest.mark.parametrize("which", ["16k", "32k"])
 def test_c4_geometry_long_context_vs_oracle(env_long, oracle, which):
-    """16448 positions in a 32768-slot cache: 514 key chunks, so each of the
-    merge's four groups sums 128 or 129 chunk partials.  Same comparison and
-    tolerance as above, against c4_geometry_16k_logits.npz."""
+    """16448 and 32736 positions in a 32768-slot cache: 514 and 1023 key
+    chunks, so each of the merge's four groups sums 128-129 and 255-256
+    chunk partials.  Same comparison and tolerance as above, against
+    c4_geometry_{16k,32k}_logits.npz."""
     _vs_oracle(env_long, oracle, GOLDEN.with_name(f"c4_geometry_{which}_logits.npz"))
 
 
