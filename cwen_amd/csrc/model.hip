@@ -170,9 +170,11 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnParams p) {
 // element g*run + k of the reduction dimension, so a lane reads 4 steps with
 // one 16-byte LDS read; the summation order is fixed and the same for every
 // query row, whatever B is.  Scores: wave w takes 16-query tile w (both
-// 16-key halves, so the chunk softmax stays in the wave); a block with more
-// than 4 tiles runs 8-wave workgroups (NW = 8), so a wave never holds more
-// than one tile.  K and V rows land in LDS straight from the cache by
+// 16-key halves, so the chunk softmax stays in the wave); workgroups have 8
+// waves (NW = 8), so a wave never holds more than one tile, and with fewer
+// tiles the idle waves still share the K/V landing and the P.V products
+// (8-wave workgroups measured 0.7 % faster per verify cycle than 4-wave ones
+// at 1-3 tiles).  K and V rows land in LDS straight from the cache by
 // 16-byte buffer loads (one 1 KB row per instruction; rows past the block's
 // last position load as zeros), in their natural [key][dim] layout.  P.V:
 // wave w takes head-dim tiles (16/NW)w .. of every query tile, reading V's 8
@@ -468,10 +470,8 @@ int attention_max_group() { return NW_MAX * 16 / CWEN_BMAX; }
 int attention_init() {
   static bool done = false;
   if (!done) {
-    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     160 * 1024));
-    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     160 * 1024));
+    CWEN_HIP_TRY(hipFuncSetAttribute((const void *)attn_chunk_kernel<NW_MAX>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
     done = true;
   }
   return CWEN_OK;
@@ -519,8 +519,7 @@ int attention_launch(const float *qfull, int qfs, const float *kx, const float *
   int rc;
   if ((rc = attention_init())) return rc;
   hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)B, (unsigned)(NH + NKV)), dim3(HD), 0, st, p);
-  if (MT <= 4) hipLaunchKernelGGL(attn_chunk_kernel<4>, dim3((unsigned)nwg, (unsigned)NKV), dim3(256), lds, st, p);
-  else hipLaunchKernelGGL(attn_chunk_kernel<8>, dim3((unsigned)nwg, (unsigned)NKV), dim3(512), lds, st, p);
+  hipLaunchKernelGGL(attn_chunk_kernel<NW_MAX>, dim3((unsigned)nwg, (unsigned)NKV), dim3(64 * NW_MAX), lds, st, p);
   hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)B, (unsigned)NH), dim3(HD * MGR), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
