@@ -50,7 +50,7 @@ def _run(env, W, X, side=0, mode="single"):
     return H.cpu().numpy()
 
 
-SHAPES = [(16, 512), (20, 1024), (100, 512), (48, 5120), (1024, 1024), (5120, 5120)]
+SHAPES = [(16, 512), (20, 1024), (100, 512), (48, 5120), (1024, 1024), (5120, 5120), (48, 65536)]   # K up to CWEN_KMAX
 
 
 @pytest.mark.parametrize("M,K", SHAPES)
@@ -174,6 +174,9 @@ def test_argument_errors(env):
         gpu.Weight(ctx, gpu.T_Q6_K, synth.q6_k(108, M, 512), None, 288, M)   # K-quant: whole 256s
     with pytest.raises(gpu.CwenError):
         gpu.Weight(ctx, 1, qs, sc, K, M)                   # F16 is not a supported type
+    qs3, sc3 = synth.q4_rs(108, M, 65536 + 32)
+    with pytest.raises(gpu.CwenError):
+        gpu.Weight(ctx, T_RS, qs3, sc3, 65536 + 32, M)     # K past CWEN_KMAX
 
 
 @pytest.mark.slow
