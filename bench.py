@@ -32,6 +32,10 @@ sys.path.insert(0, str(ROOT))
 METRIC = "verified tok/s + HBM GB/s (% of peak), Q4_0 27B-shape verify B=1/8/16"
 H, I = 5120, 17408
 PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
+# Back-to-back launches behind each single-kernel timing (the roofline kernel
+# and the kernel legs), at least: a 20-launch window of a 23 us kernel is
+# 0.5 ms, short against the run-to-run swings of the kernel's duration.
+KERNEL_LAUNCHES = 200
 NCOPIES = 8
 COPY_BYTES = 256 << 20     # calibration copy for the counter profile
 TRAFFIC_FILE = "q4_gemv_swiglu_ffn_b8_traffic.json"
@@ -215,13 +219,15 @@ def gpu_leg(steps: int, warmup: int, Bs: list[int]) -> dict:
         torch.cuda.synchronize()
         ms_step = t0.elapsed_time(t1) / steps
         # Average launch duration of each of the two GEMV kernels mlp_block
-        # runs (same entry points, f16 operands): `steps` back-to-back
-        # launches of one kernel between two events on the launch stream.
+        # runs (same entry points, f16 operands): max(steps, KERNEL_LAUNCHES)
+        # back-to-back launches of one kernel between two events on the
+        # launch stream.
         gpu.act_to_f16(ctx, X, Xh, H, B, stream=stream)
+        kl = max(steps, KERNEL_LAUNCHES)
         l1_ms = time_launches(lambda i: gpu.gemvb_swiglu_f16(ctx, Wgu[i % NCOPIES], Xh, None, B, Hh=Hh,
-                                                             stream=stream), steps, warmup, stream)
+                                                             stream=stream), kl, warmup, stream)
         l2_ms = time_launches(lambda i: gpu.gemvb_f16(ctx, Wd[i % NCOPIES], Hh, Y, B, accumulate=True,
-                                                      stream=stream), steps, warmup, stream)
+                                                      stream=stream), kl, warmup, stream)
         b1, b2 = ffn_bytes(B)
         out[B] = {
             "ms_per_step": ms_step,
@@ -285,6 +291,7 @@ def extra_leg(steps: int, warmup: int) -> dict:
     ctx = gpu.Context(0)
     stream = torch.cuda.current_stream()
     out = {}
+    steps = max(steps, KERNEL_LAUNCHES)   # single-kernel legs: windows long enough to average the swings
 
     # c0: 24 copies x 14.7 MB > 256 MB MALL
     Ws = [gpu.Weight(ctx, gpu.T_Q4_0, synth.q4_gguf(0, 5120, 5120, key=c), None, 5120, 5120) for c in range(24)]
