@@ -460,7 +460,6 @@ int cwen_gdn_create(cwen_ctx *ctx, int nkh, int nvh, int dk, cwen_gdn **out) {
       hipMalloc((void **)&g->H, hf * g->nslot * sizeof(float)) != hipSuccess ||
       hipMalloc((void **)&g->xc, (size_t)2 * CWEN_BMAX * g->C * sizeof(float)) != hipSuccess ||
       hipMalloc((void **)&g->gates, (size_t)2 * CWEN_BMAX * 2 * nvh * sizeof(float)) != hipSuccess ||
-      hipMalloc((void **)&g->ob, (size_t)CWEN_BMAX * nvh * dk * sizeof(float)) != hipSuccess ||
       hipMalloc((void **)&g->ctl, 4 * sizeof(int)) != hipSuccess) {
     cwen_gdn_free(g);
     return CWEN_ENOMEM;
@@ -479,7 +478,7 @@ int cwen_gdn_free(cwen_gdn *g) {
   if (!g) return CWEN_EINVAL;
   (void)hipSetDevice(g->ctx->device);
   (void)hipDeviceSynchronize();
-  for (float *p : {g->S, g->H, g->xc, g->gates, g->ob, g->S_peek})
+  for (float *p : {g->S, g->H, g->xc, g->gates, g->S_peek})
     if (p) (void)hipFree(p);
   if (g->ctl && g->own_ctl) (void)hipFree(g->ctl);
   free(g);

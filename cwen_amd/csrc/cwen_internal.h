@@ -72,7 +72,6 @@ struct cwen_gdn {
   int last_B;               // positions of the last, uncommitted block (0: none)
   float *S, *H;             // device: base states [2][nvh][dk][dk], history ring [nslot][C][3]
   float *xc, *gates;        // pending post-conv values [2][BMAX][C], g and beta [2][BMAX][2][nvh]
-  float *ob;                // scratch: pre-norm outputs [BMAX][nvh*dk]
   float *S_peek;            // scratch for cwen_gdn_get_state (allocated on first use)
 };
 // Host copy of committing n positions of a block of B (0: no block, no-op):

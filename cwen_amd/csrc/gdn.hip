@@ -29,17 +29,19 @@
 // ctl = {ring slot, base slot, replay count, pending parity} is advanced by
 // the commit (cwen_gdn_commit, or the model's device commit).
 //
-// Design (gfx950): three launches on the caller's stream.
+// Design (gfx950): two launches on the caller's stream (one inside the
+// model, whose in-projection GEMV applies the conv in its epilogue).
 //  1. conv: one thread per (channel, position): the 4-tap filter reads its
 //     inputs from the block's rows or the start history slot, so every
 //     position is computed at once; it writes the post-SiLU value to the
 //     pending buffer and that position's history slot to the ring.
-//  2. recurrence: the delta rule is column-local (sk[j], delta[j] and o[j]
-//     read only column j), so a head's 128 columns split over 8 single-wave
-//     workgroups of 16 columns (384 workgroups at 48 heads).  A lane owns a
-//     4-column x 8-row block of S in registers for the whole block; a column
-//     sum is a 16-lane DPP reduction.
-//  3. norm: one wave per (position, value head) applies the gated RMSNorm.
+//  2. recurrence + gated RMSNorm: the delta rule is column-local (sk[j],
+//     delta[j] and o[j] read only column j), so a head's 128 columns split
+//     over the 8 waves of one workgroup, 16 columns each (48 workgroups of
+//     512 threads at 48 heads).  A lane owns a 4-column x 8-row block of S
+//     in registers for the whole block; a column sum is a 16-lane DPP
+//     reduction.  The head's outputs meet in LDS and the same workgroup
+//     applies the norm, one wave per position.
 // Every position runs the same instructions whatever B is, so a block of B
 // equals B single-position blocks bit for bit.
 #include "cwen_internal.h"
@@ -75,7 +77,6 @@ struct GdnParams {
   const float *A, *dt;        // raw gates when non-null: decay = A*softplus(decay + dt), beta = sigmoid(beta)
   float *xc;                  // pending post-conv values [2][BMAX][C]
   float *gates;               // pending g, beta [2][BMAX][2][nvh]
-  float *ob;                  // scratch: pre-norm outputs [B][nvh*DK]
   int nkh, nvh, C, B;
 };
 
@@ -110,27 +111,31 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(GdnParams p) {
   p.xc[((size_t)P * CWEN_BMAX + b) * p.C + c] = y;   // q and k are l2-normalised by the recurrence
 }
 
-// 2. recurrence: workgroup (hv, slice) = one wave, columns
-// slice*16 .. slice*16+15 of head hv.  Lane: row group rg = lane & 15 (rows
-// 8rg..8rg+7), column group cg = lane >> 4 (4 columns).  The replay and the
-// block's own positions share one LDS layout per phase: q|k normalised, the
-// v slice, g and beta.
-__global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
+// 2. recurrence and gated RMSNorm: workgroup hv = 8 waves, wave w the
+// columns w*16 .. w*16+15 of value head hv.  Lane: row group rg = lane & 15
+// (rows 8rg..8rg+7), column group cg = lane >> 4 (4 columns).  The head's
+// 128 outputs of a position meet in LDS, so the norm follows a workgroup
+// barrier, not another launch.  Staging is shared: wave w l2-normalises q
+// and k of positions w and w + 8, each wave stages its own v columns, the
+// last wave the gates.  The replay and the block's own positions share one
+// LDS layout per phase.
+constexpr int RW = DK / COLS;       // waves per head
+__global__ __launch_bounds__(64 * RW) void gdn_rec_kernel(GdnParams p) {
   __shared__ __align__(16) float qk[MAXB][2 * DK];   // normalised q | k per position
-  __shared__ __align__(16) float vs[MAXB][COLS];
+  __shared__ __align__(16) float vs[MAXB][DK];
+  __shared__ __align__(16) float ob[MAXB][DK];       // pre-norm outputs of the block
   __shared__ float s_g[MAXB], s_beta[MAXB];
-  const int lane = threadIdx.x;
-  const int hv = blockIdx.x / (DK / COLS);
-  const int slice = blockIdx.x % (DK / COLS);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hv = blockIdx.x, slice = wave;
   const int hk = hv % p.nkh;
   const bool peek = p.S_peek != nullptr;
   const int X = p.ctl[1], P = p.ctl[3];
-  const int L = peek ? p.peek_L : (p.force_L0 ? 0 : p.ctl[2]);  // positions to replay
-  const int Pr = peek ? p.peek_buf : (P ^ 1);                   // their pending buffer
+  const int L = peek ? p.peek_L : (p.force_L0 ? 0 : p.ctl[2]);
+  const int Pr = peek ? p.peek_buf : (P ^ 1);
   const int B = peek ? 0 : p.B;
   const int rg = lane & 15, cg = lane >> 4;
   const int i0 = rg * 8, j0 = slice * COLS + cg * 4;
-  const size_t xstride = (size_t)CWEN_BMAX * p.C;               // floats per pending buffer
+  const size_t xstride = (size_t)CWEN_BMAX * p.C;
   const size_t gstride = (size_t)CWEN_BMAX * 2 * p.nvh;
 
   float4 s[8];
@@ -139,55 +144,66 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) s[r] = *(const float4 *)(Sh + (size_t)(i0 + r) * DK + j0);
   }
+  // The norm's inputs of this wave's positions (w, w + 8), requested now.
+  float2 zr[MAXB / RW] = {}, wn2 = {0.f, 0.f};
+  if (B > 0) {
+    wn2 = *(const float2 *)(p.wn + 2 * lane);
+#pragma unroll
+    for (int u = 0; u < MAXB / RW; ++u) {
+      const int b = wave + RW * u;
+      if (b < B) {
+        zr[u].x = p.z[(size_t)b * p.zs + hv * DK + 2 * lane];
+        zr[u].y = p.z[(size_t)b * p.zs + hv * DK + 2 * lane + 1];
+      }
+    }
+  }
 
-  // Stage nb positions of pending buffer `buf` into LDS; gates from the
-  // buffer (replay) or computed from the raw inputs and saved (block).
-  // Every global load of a group of 8 positions is issued before the first
-  // wait, so staging costs one memory round trip per group, not one per
-  // position or per value; loads for positions past nb re-read position
-  // nb - 1 (inside the buffer) and are not stored.
   auto stage = [&](int nb, int buf, bool fresh) {
     const float *xc = p.xc + (size_t)buf * xstride;
     float *gs = p.gates + (size_t)buf * gstride;
-    const int lb = min(lane, nb - 1);
-    const float g_in = fresh ? p.decay[(size_t)lb * p.gs + hv] : gs[((size_t)lb * 2 + 0) * p.nvh + hv];
-    const float b_in = fresh ? p.beta[(size_t)lb * p.gs + hv] : gs[((size_t)lb * 2 + 1) * p.nvh + hv];
-    for (int b0 = 0; b0 < nb; b0 += 8) {
-      float qkr[8][4], vr[2];
+    const bool gw = wave == RW - 1 && lane < nb;   // the gates' lanes
+    float g_in = 0.f, b_in = 0.f;
+    if (gw) {
+      g_in = fresh ? p.decay[(size_t)lane * p.gs + hv] : gs[((size_t)lane * 2 + 0) * p.nvh + hv];
+      b_in = fresh ? p.beta[(size_t)lane * p.gs + hv] : gs[((size_t)lane * 2 + 1) * p.nvh + hv];
+    }
+    // q and k of key head hk, positions wave and wave + RW
+    float qkr[MAXB / RW][4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {   // q and k of key head hk
-        const int b = min(b0 + u, nb - 1);
-        const float *xq = xc + (size_t)b * p.C + hk * DK;
-        const float *xk = xc + (size_t)b * p.C + (p.nkh + hk) * DK;
-        qkr[u][0] = xq[lane]; qkr[u][1] = xq[lane + 64];
-        qkr[u][2] = xk[lane]; qkr[u][3] = xk[lane + 64];
-      }
+    for (int u = 0; u < MAXB / RW; ++u) {
+      const int b = min(wave + RW * u, nb - 1);
+      const float *xq = xc + (size_t)b * p.C + hk * DK;
+      const float *xk = xc + (size_t)b * p.C + (p.nkh + hk) * DK;
+      qkr[u][0] = xq[lane]; qkr[u][1] = xq[lane + 64];
+      qkr[u][2] = xk[lane]; qkr[u][3] = xk[lane + 64];
+    }
+    // v: this wave's COLS columns, 8 positions per group, 2 values per lane
+    float vr[MAXB / 8][2];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {   // l2 norms (run.c:401-423): x / sqrt(sum x^2 + 1e-6), dims 0..63 then 64..127
-        const float rq = 1.f / sqrtf(sum64(qkr[u][0] * qkr[u][0]) + sum64(qkr[u][1] * qkr[u][1]) + 1e-6f);
-        const float rk = 1.f / sqrtf(sum64(qkr[u][2] * qkr[u][2]) + sum64(qkr[u][3] * qkr[u][3]) + 1e-6f);
-        qkr[u][0] *= rq; qkr[u][1] *= rq;
-        qkr[u][2] *= rk; qkr[u][3] *= rk;
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {   // v: 8 positions x COLS columns, 2 per lane
-        const int e = lane + 64 * i, b = min(b0 + e / COLS, nb - 1);
-        vr[i] = xc[(size_t)b * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (b0 + u < nb) {
-          qk[b0 + u][lane] = qkr[u][0]; qk[b0 + u][lane + 64] = qkr[u][1];
-          qk[b0 + u][DK + lane] = qkr[u][2]; qk[b0 + u][DK + lane + 64] = qkr[u][3];
-        }
-      }
+    for (int h = 0; h < MAXB / 8; ++h)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int e = lane + 64 * i;
-        if (b0 + e / COLS < nb) vs[b0 + e / COLS][e % COLS] = vr[i];
+        const int e = lane + 64 * i, b = min(8 * h + e / COLS, nb - 1);
+        vr[h][i] = xc[(size_t)b * p.C + 2 * p.nkh * DK + hv * DK + slice * COLS + e % COLS];
+      }
+#pragma unroll
+    for (int u = 0; u < MAXB / RW; ++u) {   // l2 norms (run.c:401-423)
+      const int b = wave + RW * u;
+      if (b < nb) {
+        const float rq = 1.f / sqrtf(sum64(qkr[u][0] * qkr[u][0]) + sum64(qkr[u][1] * qkr[u][1]) + 1e-6f);
+        const float rk = 1.f / sqrtf(sum64(qkr[u][2] * qkr[u][2]) + sum64(qkr[u][3] * qkr[u][3]) + 1e-6f);
+        qk[b][lane] = qkr[u][0] * rq; qk[b][lane + 64] = qkr[u][1] * rq;
+        qk[b][DK + lane] = qkr[u][2] * rk; qk[b][DK + lane + 64] = qkr[u][3] * rk;
       }
     }
-    if (lane < nb) {
+#pragma unroll
+    for (int h = 0; h < MAXB / 8; ++h)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = lane + 64 * i, b = 8 * h + e / COLS;
+        if (b < nb) vs[b][slice * COLS + e % COLS] = vr[h][i];
+      }
+    if (gw) {
       float g = g_in, bt = b_in;
       if (fresh) {
         float dec = g_in;
@@ -197,10 +213,8 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
           bt = 1.f / (1.f + expf(-bt));
         }
         g = expf(dec);
-        if (slice == 0) {
-          gs[((size_t)lane * 2 + 0) * p.nvh + hv] = g;
-          gs[((size_t)lane * 2 + 1) * p.nvh + hv] = bt;
-        }
+        gs[((size_t)lane * 2 + 0) * p.nvh + hv] = g;
+        gs[((size_t)lane * 2 + 1) * p.nvh + hv] = bt;
       }
       s_g[lane] = g;
       s_beta[lane] = bt;
@@ -208,7 +222,6 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
     __syncthreads();
   };
 
-  // The delta rule over staged positions 0..nb-1; emit: write the outputs.
   const float scale = 1.f / sqrtf((float)DK);
   auto run = [&](int nb, bool emit) {
     for (int b = 0; b < nb; ++b) {
@@ -225,7 +238,7 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
         sk.z = fmaf(s[r].z, kr[r], sk.z); sk.w = fmaf(s[r].w, kr[r], sk.w);
       }
       sk = (float4){sum16(sk.x), sum16(sk.y), sum16(sk.z), sum16(sk.w)};
-      const float4 v4 = *(const float4 *)&vs[b][cg * 4];
+      const float4 v4 = *(const float4 *)&vs[b][j0];
       const float4 dl = {beta * (v4.x - sk.x), beta * (v4.y - sk.y), beta * (v4.z - sk.z), beta * (v4.w - sk.w)};
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
@@ -240,7 +253,7 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
           o.z = fmaf(s[r].z, qr[r], o.z); o.w = fmaf(s[r].w, qr[r], o.w);
         }
         o = (float4){sum16(o.x) * scale, sum16(o.y) * scale, sum16(o.z) * scale, sum16(o.w) * scale};
-        if (rg == 0) *(float4 *)(p.ob + (size_t)b * p.nvh * DK + hv * DK + j0) = o;
+        if (rg == 0) *(float4 *)&ob[b][j0] = o;
       }
     }
   };
@@ -257,34 +270,33 @@ __global__ __launch_bounds__(64) void gdn_rec_kernel(GdnParams p) {
       store(p.S_peek);
       return;
     }
-    store(p.S_base + (size_t)X * p.s_floats);   // this block's start state, in place
-    __syncthreads();                             // LDS reused below
+    store(p.S_base + (size_t)X * p.s_floats);
+    __syncthreads();
   } else if (peek) {
     store(p.S_peek);
     return;
   }
   stage(B, P, true);
   run(B, true);
-  store(p.S_base + (size_t)(X ^ 1) * p.s_floats);  // this block's end state
-}
-
-// 3. gated RMSNorm: one wave per (position, value head).
-__global__ __launch_bounds__(64) void gdn_norm_kernel(GdnParams p) {
-  const int b = blockIdx.x / p.nvh, hv = blockIdx.x % p.nvh;
-  const int lane = threadIdx.x;
-  const float2 o = *(const float2 *)(p.ob + (size_t)b * p.nvh * DK + hv * DK + 2 * lane);
-  const float ss = sum64(o.x * o.x + o.y * o.y);
-  const float sc = 1.f / sqrtf(ss / DK + 1e-6f);
-  const float zx = p.z[(size_t)b * p.zs + hv * DK + 2 * lane], zy = p.z[(size_t)b * p.zs + hv * DK + 2 * lane + 1];
-  const float2 w = *(const float2 *)(p.wn + 2 * lane);
-  float2 r;
-  r.x = w.x * o.x * sc * silu_ref(zx);
-  r.y = w.y * o.y * sc * silu_ref(zy);
-  if (p.out) *(float2 *)(p.out + (size_t)b * p.os + hv * DK + 2 * lane) = r;
-  if (p.outh) {
-    const half2_t h = {(_Float16)r.x, (_Float16)r.y};
-    *(half2_t *)(p.outh + (size_t)b * p.ohs + hv * DK + 2 * lane) = h;
-    if (f16_bad(h[0]) || f16_bad(h[1])) raise_flag(p.rflag);
+  store(p.S_base + (size_t)(X ^ 1) * p.s_floats);
+  __syncthreads();
+  // gated RMSNorm of positions wave and wave + RW: out = wn * o * (1 / sqrt(mean(o^2) + 1e-6)) * silu(z)
+#pragma unroll
+  for (int u = 0; u < MAXB / RW; ++u) {
+    const int b = wave + RW * u;
+    if (b >= B) break;
+    const float2 o = *(const float2 *)&ob[b][2 * lane];
+    const float ss = sum64(o.x * o.x + o.y * o.y);
+    const float sc = 1.f / sqrtf(ss / DK + 1e-6f);
+    float2 r;
+    r.x = wn2.x * o.x * sc * silu_ref(zr[u].x);
+    r.y = wn2.y * o.y * sc * silu_ref(zr[u].y);
+    if (p.out) *(float2 *)(p.out + (size_t)b * p.os + hv * DK + 2 * lane) = r;
+    if (p.outh) {
+      const half2_t h = {(_Float16)r.x, (_Float16)r.y};
+      *(half2_t *)(p.outh + (size_t)b * p.ohs + hv * DK + 2 * lane) = h;
+      if (f16_bad(h[0]) || f16_bad(h[1])) raise_flag(p.rflag);
+    }
   }
 }
 
@@ -301,7 +313,7 @@ static void fill_params(GdnParams &p, const cwen_gdn *g) {
   p.S_peek = nullptr;
   p.peek_L = p.peek_buf = 0;
   p.rflag = nullptr;
-  p.xc = g->xc; p.gates = g->gates; p.ob = g->ob;
+  p.xc = g->xc; p.gates = g->gates;
   p.nkh = g->nkh; p.nvh = g->nvh; p.C = g->C;
 }
 
@@ -332,8 +344,7 @@ int gdn_block_launch(const cwen_gdn *g, const float *qkv, int qs, const float *z
   p.B = B;
   if (!conv_done)
     hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((g->C + 255) / 256), (unsigned)B), dim3(256), 0, st, p);
-  hipLaunchKernelGGL(gdn_rec_kernel, dim3((unsigned)(g->nvh * (DK / COLS))), dim3(64), 0, st, p);
-  hipLaunchKernelGGL(gdn_norm_kernel, dim3((unsigned)(g->nvh * B)), dim3(64), 0, st, p);
+  hipLaunchKernelGGL(gdn_rec_kernel, dim3((unsigned)g->nvh), dim3(64 * RW), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }
@@ -347,7 +358,7 @@ int gdn_peek_launch(const cwen_gdn *g, int L, int buf, float *S_out, hipStream_t
   p.qkv = nullptr; p.qs = 0; p.z = nullptr; p.zs = 0; p.decay = p.beta = nullptr; p.gs = 0;
   p.kw = p.wn = nullptr; p.out = nullptr; p.os = 0; p.outh = nullptr; p.ohs = 0; p.A = p.dt = nullptr;
   p.B = 0;
-  hipLaunchKernelGGL(gdn_rec_kernel, dim3((unsigned)(g->nvh * (DK / COLS))), dim3(64), 0, st, p);
+  hipLaunchKernelGGL(gdn_rec_kernel, dim3((unsigned)g->nvh), dim3(64 * RW), 0, st, p);
   CWEN_HIP_TRY(hipGetLastError());
   return CWEN_OK;
 }
