@@ -169,6 +169,21 @@ def read_probes(reps: int, stream) -> dict:
         "ms": round(ms, 5), "GB_s": round(nread.value / (ms * 1e-3) / 1e9, 1),
         "frac_of_peak": round(nread.value / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes_read": nread.value,
         "kernel": "read_probe: 512 workgroups x 4 waves, 4 KB per wave per step, non-temporal"}
+    # The same read at 16 MiB per launch, about the size of a 5120 x 5120
+    # Q4_0 GEMV (14.7 MB), rotated over 30 regions (503 MB > the MALL): what
+    # one launch of that size costs with no arithmetic.
+    span = 2 * 512 * 4 * 4096
+    regions = [(b, off) for b in range(6) for off in range(0, wbytes - span + 1, span)]
+
+    def read16_launch(i):
+        b, off = regions[i % len(regions)]
+        if lib.cwen_probe_read(bufs[b].data_ptr() + off, span, sink.data_ptr(), 2, ctypes.byref(nread), st):
+            raise RuntimeError("cwen_probe_read refused its arguments")
+    ms = time_launches(read16_launch, reps, 3, stream)
+    out["read_linear_16MiB"] = {
+        "ms": round(ms, 5), "GB_s": round(nread.value / (ms * 1e-3) / 1e9, 1),
+        "frac_of_peak": round(nread.value / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes_read": nread.value,
+        "kernel": "read_probe as above, 2 steps per wave, one launch per 16 MiB region"}
     del bufs
     return out
 
