@@ -96,10 +96,12 @@ def test_gdn_block_parity_and_rollback(env, oracle, nkh, nvh, B):
     G.free()
 
 
-def test_gdn_block_equals_serial_bitwise(env):
-    """One block of B positions == B one-position blocks, each committed."""
+@pytest.mark.parametrize("B", [8, 16])
+def test_gdn_block_equals_serial_bitwise(env, B):
+    """One block of B positions == B one-position blocks, each committed
+    (at B = 16 each wave of the recurrence stages two positions)."""
     _, gpu, ctx = env
-    nkh, nvh, B = 16, 48, 8
+    nkh, nvh = 16, 48
     S, hist, kw, wn, qkv, z, decay, beta = _inputs(3, B, nkh, nvh)
     Gb = gpu.GDN(ctx, nkh, nvh)
     Gb.set_state(S, hist)
@@ -114,6 +116,41 @@ def test_gdn_block_equals_serial_bitwise(env):
         Ss, hs = Gs.get_state(0)
         assert np.array_equal(Sb, Ss) and np.array_equal(hb, hs), b
     Gb.free()
+    Gs.free()
+
+
+def test_gdn_long_replay_then_full_block(env, oracle):
+    """Commit 12 of a block of 16, then a block of 16: the second launch
+    replays 12 positions (more than one per recurrence wave) before its own
+    16.  Its outputs and end state equal, bit for bit, those of a state that
+    took the same 12 positions as single committed blocks, and match the
+    oracle continued from the 12th position (rel_err <= 1e-3)."""
+    _, gpu, ctx = env
+    nkh, nvh, B, L = 16, 48, 16, 12
+    S, hist, kw, wn, qkv, z, decay, beta = _inputs(11, B, nkh, nvh)
+    _, _, _, _, qkv2, z2, decay2, beta2 = _inputs(12, B, nkh, nvh)
+    G = gpu.GDN(ctx, nkh, nvh)
+    G.set_state(S, hist)
+    _gpu_block(env, G, kw, wn, qkv, z, decay, beta)
+    G.commit(L)
+    out_r = _gpu_block(env, G, kw, wn, qkv2, z2, decay2, beta2)
+    G.commit(B)
+    Gs = gpu.GDN(ctx, nkh, nvh)
+    Gs.set_state(S, hist)
+    for b in range(L):
+        _gpu_block(env, Gs, kw, wn, qkv[b:b + 1], z[b:b + 1], decay[b:b + 1], beta[b:b + 1])
+        Gs.commit(1)
+    out_s = _gpu_block(env, Gs, kw, wn, qkv2, z2, decay2, beta2)
+    Gs.commit(B)
+    assert np.array_equal(out_r.view(np.uint32), out_s.view(np.uint32))
+    Sr, hr = G.get_state(0)
+    Ss, hs = Gs.get_state(0)
+    assert np.array_equal(Sr.view(np.uint32), Ss.view(np.uint32)) and np.array_equal(hr, hs)
+    _, states = _oracle_run(oracle, S, hist, kw, wn, qkv[:L], z[:L], decay[:L], beta[:L], nkh, nvh)
+    ref2, states2 = _oracle_run(oracle, *states[L - 1], kw, wn, qkv2, z2, decay2, beta2, nkh, nvh)
+    assert rel_err(out_r, ref2) <= TOL, rel_err(out_r, ref2)
+    assert rel_err(Sr, states2[-1][0]) <= TOL and np.array_equal(hr, states2[-1][1])
+    G.free()
     Gs.free()
 
 
