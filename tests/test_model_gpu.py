@@ -352,9 +352,12 @@ def test_block_equals_serial_bitwise(env, B):
         assert np.array_equal(m.logits(1)[0], block[b]), b
 
 
-def test_verify_walk_and_rollback(env):
+@pytest.mark.parametrize("emax", [8, 16])
+def test_verify_walk_and_rollback(env, emax):
     """Drafts built from the serial stream with planted mistakes: every
-    accepted draft and bonus must equal the serial stream."""
+    accepted draft and bonus must equal the serial stream.  Blocks of up to
+    emax positions (E < emax drafts), so with emax = 16 the accepted prefix
+    the next block replays reaches 15 positions."""
     gpu, ctx, m, _ = env
     V = CFG["vocab"]
     prompt = synth.prompt_tokens(3, 40, V)
@@ -368,8 +371,9 @@ def test_verify_walk_and_rollback(env):
                                                           len(prompt), C.byref(nxt)))
     out = [nxt.value]
     seen_partial = seen_full = False
+    longest = 0        # longest accepted prefix of a partly rejected block
     while len(out) < n_gen:
-        E = int(g.integers(0, 8))
+        E = int(g.integers(0, emax))
         fut = serial[len(out):len(out) + E].astype(np.int32)
         E = len(fut)
         drafts = fut.copy()
@@ -381,9 +385,13 @@ def test_verify_walk_and_rollback(env):
         assert k == want_k, (len(out), E, k, want_k)
         seen_partial |= k < E
         seen_full |= E > 0 and k == E
+        if k < E:
+            longest = max(longest, k)
         out.extend(drafts[:k].tolist())
         out.append(bonus)
     assert seen_partial and seen_full
+    if emax == 16:
+        assert longest >= 8, longest          # a replay longer than 8 positions happened
     assert np.array_equal(np.array(out[:n_gen]), serial)
 
 
