@@ -228,7 +228,8 @@ __global__ __launch_bounds__(256) void mtp_cat_kernel(const float *e, const floa
     const _Float16 b = (_Float16)(hr[i] * rh * wpre[i] * r1 * hnorm[i]);
     out[i] = a;
     out[H + i] = b;
-    bad |= f16_bad(a) | f16_bad(b);
+    bad |= f16_bad(a);
+    bad |= f16_bad(b);
   }
   if (bad) raise_flag(rflag);
 }
